@@ -1,0 +1,93 @@
+// Shared runtime pieces of libaxis_hip: the device handle, the stream-ordered caching allocator,
+// error reporting and launch helpers.  Compiled for gfx950 only.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <map>
+#include <string>
+#include <unordered_map>
+
+#include "../../include/axis_hip.h"
+
+struct axis_device_s {
+    int ordinal = 0;
+    hipStream_t stream = nullptr;
+    // Free blocks by rounded size.  All launches share one stream, so a block released after its
+    // last use was enqueued can serve any later launch without a host wait.
+    std::multimap<size_t, void *> free_blocks;
+    std::unordered_map<void *, size_t> live;
+    size_t in_use = 0;
+    size_t cached = 0;
+    int multiprocessors = 256;
+};
+
+struct axis_plan_s {
+    int32_t *offsets = nullptr;       // groups + 1
+    int32_t *left = nullptr;          // count
+    int32_t *right = nullptr;         // count, or null
+    int32_t *chunk_offsets = nullptr; // chunks + 1: absolute bounds into left/right
+    int32_t *chunk_group = nullptr;   // groups + 1: first chunk of each group
+    int64_t groups = 0;
+    int64_t count = 0;
+    int64_t chunks = 0;
+};
+
+namespace axis {
+
+constexpr int kGroupedChunk = 512;  // runtime/backend.rs:27 (GROUPED_CHUNK)
+
+int fail(int code, const std::string &message);
+int hip_fail(hipError_t error, const char *what);
+int enter(axis_device device);  // validates the handle and makes its GPU current
+int launch_status(const char *kernel);
+int alloc(axis_device device, size_t bytes, void **out);
+void release(axis_device device, void *ptr);
+
+// RAII scratch block from the device's caching allocator (returned on scope exit; stream order
+// makes the reuse safe).
+struct Scratch {
+    axis_device device = nullptr;
+    void *ptr = nullptr;
+    Scratch() = default;
+    Scratch(const Scratch &) = delete;
+    Scratch &operator=(const Scratch &) = delete;
+    ~Scratch() {
+        if (ptr) release(device, ptr);
+    }
+    int get(axis_device d, size_t bytes) {
+        device = d;
+        return alloc(d, bytes, &ptr);
+    }
+    template <class T> T *as() const { return static_cast<T *>(ptr); }
+};
+
+inline unsigned blocks_for(int64_t work, int per_block, int64_t cap = 1 << 20) {
+    int64_t b = (work + per_block - 1) / per_block;
+    if (b < 1) b = 1;
+    if (b > cap) b = cap;
+    return static_cast<unsigned>(b);
+}
+
+inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace axis
+
+#define AXIS_ENTER(dev)                                  \
+    do {                                                 \
+        int axis_enter_status = axis::enter(dev);        \
+        if (axis_enter_status) return axis_enter_status; \
+    } while (0)
+
+#define AXIS_REQUIRE(cond, msg)                                         \
+    do {                                                                \
+        if (!(cond)) return axis::fail(AXIS_ERROR_INVALID, (msg));     \
+    } while (0)
+
+#define AXIS_HIP(call)                                       \
+    do {                                                     \
+        hipError_t axis_hip_error = (call);                  \
+        if (axis_hip_error != hipSuccess)                    \
+            return axis::hip_fail(axis_hip_error, #call);    \
+    } while (0)

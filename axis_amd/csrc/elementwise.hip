@@ -1,0 +1,487 @@
+// Bandwidth-bound elementwise, layout and reduction entries (runtime/backend.rs kernels
+// :2057-2188, :2588-2640, :2797-2801) and the fused bias/reduction entries of axis_hip.h.
+//
+// Streaming kernels move 16-byte vectors when every pointer is 16-byte aligned, with a scalar
+// tail; reductions keep the reference's association (sequential chunks of 512, then chunk
+// partials in order) so they are bit-identical to a sequential restatement.  Built with
+// -ffp-contract=off: every expression rounds exactly as written.
+#include <cfloat>
+
+#include "common.hpp"
+#include "fastdiv.hpp"
+
+namespace {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int kBlock = 256;
+
+// ---------------------------------------------------------------- generic streaming map
+
+template <class F>
+__global__ void __launch_bounds__(kBlock) map_kernel(F f, int64_t len, bool vec) {
+    const int64_t tid = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    if (vec) {
+        const int64_t nv = len / 4;
+        for (int64_t v = tid; v < nv; v += stride) f.vec(v);
+        for (int64_t i = nv * 4 + tid; i < len; i += stride) f.one(i);
+    } else {
+        for (int64_t i = tid; i < len; i += stride) f.one(i);
+    }
+}
+
+template <class F>
+int launch_map(axis_device device, const F &f, int64_t len, bool vec, const char *name) {
+    if (len <= 0) return AXIS_OK;
+    const int64_t work = vec ? (len + 3) / 4 : len;
+    const unsigned blocks = axis::blocks_for(work, kBlock, (int64_t)device->multiprocessors * 16);
+    map_kernel<<<blocks, kBlock, 0, device->stream>>>(f, len, vec);
+    return axis::launch_status(name);
+}
+
+#define LOAD4(p, v) (reinterpret_cast<const floatx4 *>(p)[v])
+#define STORE4(p, v, x) (reinterpret_cast<floatx4 *>(p)[v] = (x))
+
+struct MaskGradient {
+    const float *g, *w;
+    float *out;
+    __device__ void one(int64_t i) const { out[i] = w[i] > 0.0f ? g[i] : 0.0f; }
+    __device__ void vec(int64_t v) const {
+        floatx4 a = LOAD4(g, v), m = LOAD4(w, v), r;
+        for (int c = 0; c < 4; ++c) r[c] = m[c] > 0.0f ? a[c] : 0.0f;
+        STORE4(out, v, r);
+    }
+};
+
+struct Relu {
+    const float *a;
+    float *out;
+    __device__ void one(int64_t i) const { out[i] = a[i] > 0.0f ? a[i] : 0.0f; }
+    __device__ void vec(int64_t v) const {
+        floatx4 x = LOAD4(a, v), r;
+        for (int c = 0; c < 4; ++c) r[c] = x[c] > 0.0f ? x[c] : 0.0f;
+        STORE4(out, v, r);
+    }
+};
+
+struct ReluBackward {
+    const float *g, *a;
+    float *out;
+    __device__ void one(int64_t i) const { out[i] = a[i] > 0.0f ? g[i] : 0.0f; }
+    __device__ void vec(int64_t v) const {
+        floatx4 x = LOAD4(a, v), d = LOAD4(g, v), r;
+        for (int c = 0; c < 4; ++c) r[c] = x[c] > 0.0f ? d[c] : 0.0f;
+        STORE4(out, v, r);
+    }
+};
+
+struct Scale {
+    const float *a;
+    float factor;
+    float *out;
+    __device__ void one(int64_t i) const { out[i] = a[i] * factor; }
+    __device__ void vec(int64_t v) const { STORE4(out, v, LOAD4(a, v) * factor); }
+};
+
+template <int OP>
+struct Binary {
+    const float *a, *b;
+    float *out;
+    __device__ static float apply(float x, float y) {
+        return OP == 0 ? x + y : OP == 1 ? x - y : OP == 2 ? x * y : x / y;
+    }
+    __device__ void one(int64_t i) const { out[i] = apply(a[i], b[i]); }
+    __device__ void vec(int64_t v) const {
+        floatx4 x = LOAD4(a, v), y = LOAD4(b, v), r;
+        for (int c = 0; c < 4; ++c) r[c] = apply(x[c], y[c]);
+        STORE4(out, v, r);
+    }
+};
+
+struct InverseSqrt {
+    const float *a;
+    float eps;
+    float *out;
+    __device__ void one(int64_t i) const { out[i] = 1.0f / sqrtf(a[i] + eps); }
+    __device__ void vec(int64_t v) const {
+        floatx4 x = LOAD4(a, v), r;
+        for (int c = 0; c < 4; ++c) r[c] = 1.0f / sqrtf(x[c] + eps);
+        STORE4(out, v, r);
+    }
+};
+
+struct MultiplyScalar {
+    const float *a, *s;
+    float *out;
+    __device__ void one(int64_t i) const { out[i] = a[i] * s[0]; }
+    __device__ void vec(int64_t v) const { STORE4(out, v, LOAD4(a, v) * s[0]); }
+};
+
+bool all_aligned(std::initializer_list<const void *> ptrs) {
+    for (const void *p : ptrs)
+        if (p && !axis::aligned16(p)) return false;
+    return true;
+}
+
+// ---------------------------------------------------------------- select_axis
+
+struct SelectArgs {
+    int32_t rank;
+    int32_t coordinate;
+    FastDiv place[10];   // divisor giving the coordinate from the flat index
+    FastDiv extent[10];
+    int32_t far[10];     // stride on the other side
+    int32_t selected[10];
+    int32_t len;
+};
+
+__global__ void __launch_bounds__(kBlock) select_axis_kernel(const float *__restrict__ input,
+                                                             float *__restrict__ out, SelectArgs a) {
+    const uint32_t o = blockIdx.x * kBlock + threadIdx.x;
+    if (o >= (uint32_t)a.len) return;
+    int64_t index = 0;
+    for (int d = 0; d < a.rank; ++d) {
+        if (a.selected[d])
+            index += (int64_t)a.coordinate * a.far[d];
+        else
+            index += (int64_t)a.extent[d].mod(a.place[d].div(o)) * a.far[d];
+    }
+    out[o] = input[index];
+}
+
+__global__ void __launch_bounds__(kBlock) select_axis_backward_kernel(const float *__restrict__ gradient,
+                                                                      float *__restrict__ out,
+                                                                      SelectArgs a) {
+    const uint32_t i = blockIdx.x * kBlock + threadIdx.x;
+    if (i >= (uint32_t)a.len) return;
+    int64_t index = 0;
+    bool live = true;
+    for (int d = 0; d < a.rank; ++d) {
+        const int32_t c = (int32_t)a.extent[d].mod(a.place[d].div(i));
+        if (a.selected[d])
+            live = live && c == a.coordinate;
+        else
+            index += (int64_t)c * a.far[d];
+    }
+    out[i] = live ? gradient[index] : 0.0f;
+}
+
+int select_args(const int32_t *metadata, int32_t rank, int32_t coordinate, int64_t len, bool forward,
+                SelectArgs *a) {
+    AXIS_REQUIRE(metadata, "null select metadata");
+    AXIS_REQUIRE(rank >= 0 && rank <= 10, "select_axis rank must be 0..10");
+    AXIS_REQUIRE(len >= 1 && len <= INT32_MAX - kBlock, "select_axis length out of range");
+    a->rank = rank;
+    a->coordinate = coordinate;
+    a->len = (int32_t)len;
+    for (int d = 0; d < rank; ++d) {
+        const int32_t extent = metadata[3 * d], in_stride = metadata[3 * d + 1],
+                      out_stride = metadata[3 * d + 2];
+        AXIS_REQUIRE(extent >= 1, "select_axis extents must be positive");
+        a->extent[d] = FastDiv((uint32_t)extent);
+        a->selected[d] = out_stride < 0;
+        if (forward) {
+            // out index decodes through output_stride; the input is addressed by input_stride.
+            a->place[d] = FastDiv((uint32_t)(out_stride < 0 ? 1 : out_stride));
+            a->far[d] = in_stride;
+        } else {
+            a->place[d] = FastDiv((uint32_t)(in_stride < 1 ? 1 : in_stride));
+            a->far[d] = out_stride;
+        }
+    }
+    return AXIS_OK;
+}
+
+// ---------------------------------------------------------------- sum of squares
+
+__device__ __forceinline__ float wave_sum(float v) {
+    for (int offset = 32; offset > 0; offset >>= 1) v += __shfl_xor(v, offset);
+    return v;
+}
+
+__global__ void __launch_bounds__(kBlock) sum_squares_kernel(const float *__restrict__ a, int64_t len,
+                                                             float *__restrict__ partial) {
+    __shared__ float waves[kBlock / 64];
+    float s = 0.0f;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < len; i += (int64_t)gridDim.x * kBlock)
+        s += a[i] * a[i];
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0) waves[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float t = 0.0f;
+        for (int w = 0; w < kBlock / 64; ++w) t += waves[w];
+        partial[blockIdx.x] = t;
+    }
+}
+
+__global__ void __launch_bounds__(kBlock) sum_kernel(const float *__restrict__ partial, int n,
+                                                     float *__restrict__ out) {
+    __shared__ float waves[kBlock / 64];
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < n; i += kBlock) s += partial[i];
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0) waves[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float t = 0.0f;
+        for (int w = 0; w < kBlock / 64; ++w) t += waves[w];
+        out[0] = t;
+    }
+}
+
+// ---------------------------------------------------------------- bias entries
+
+struct BiasAdd {
+    const float *a, *bias;
+    float *out, *relu_out;
+    FastDiv width_div;
+    int64_t width;
+    __device__ void one(int64_t i) const {
+        const float z = a[i] + bias[i % width];
+        out[i] = z;
+        if (relu_out) relu_out[i] = z > 0.0f ? z : 0.0f;
+    }
+    __device__ void vec(int64_t v) const {
+        const floatx4 x = LOAD4(a, v);
+        const int64_t c0 = (v * 4) % width;  // width % 4 == 0 on this path
+        const floatx4 b = LOAD4(bias + c0, 0);
+        const floatx4 z = x + b;
+        STORE4(out, v, z);
+        if (relu_out) {
+            floatx4 r;
+            for (int c = 0; c < 4; ++c) r[c] = z[c] > 0.0f ? z[c] : 0.0f;
+            STORE4(relu_out, v, r);
+        }
+    }
+};
+
+// Stage one of the bias gradient: partial[q][c] = sum of rows [512q, 512q+512) of column c,
+// sequentially; optionally masked by relu_input > 0 (and the masked gradient written out).
+template <bool MASK>
+__global__ void __launch_bounds__(kBlock) column_chunk_kernel(const float *__restrict__ g,
+                                                              const float *__restrict__ relu_input,
+                                                              float *__restrict__ masked_out,
+                                                              float *__restrict__ partial,
+                                                              int64_t rows, int64_t width,
+                                                              int64_t column_blocks) {
+    const int64_t q = blockIdx.x / column_blocks;
+    const int64_t c = (blockIdx.x % column_blocks) * kBlock + threadIdx.x;
+    if (c >= width) return;
+    const int64_t r0 = q * axis::kGroupedChunk;
+    const int64_t r1 = r0 + axis::kGroupedChunk < rows ? r0 + axis::kGroupedChunk : rows;
+    float sum = 0.0f;
+    int64_t idx = r0 * width + c;
+#pragma unroll 8
+    for (int64_t r = r0; r < r1; ++r, idx += width) {
+        float v = g[idx];
+        if (MASK) {
+            v = relu_input[idx] > 0.0f ? v : 0.0f;
+            masked_out[idx] = v;
+        }
+        sum = sum + v;
+    }
+    partial[q * width + c] = sum;
+}
+
+__global__ void __launch_bounds__(kBlock) column_combine_kernel(const float *__restrict__ partial,
+                                                                int64_t chunks, int64_t width,
+                                                                float scale, float *__restrict__ out) {
+    const int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (c >= width) return;
+    float sum = 0.0f;
+    for (int64_t q = 0; q < chunks; ++q) sum = sum + partial[q * width + c];
+    out[c] = sum * scale;
+}
+
+// out[o][i] = factor * sum_r a[o][r][i] in the reference's chunked order.
+__global__ void __launch_bounds__(kBlock) reduce_middle_kernel(const float *__restrict__ a,
+                                                               float *__restrict__ out, int64_t outer,
+                                                               int64_t reduce, int64_t inner,
+                                                               float factor) {
+    const int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (t >= outer * inner) return;
+    const int64_t o = t / inner, i = t % inner;
+    const float *base = a + o * reduce * inner + i;
+    float total = 0.0f;
+    for (int64_t r0 = 0; r0 < reduce; r0 += axis::kGroupedChunk) {
+        const int64_t r1 = r0 + axis::kGroupedChunk < reduce ? r0 + axis::kGroupedChunk : reduce;
+        float partial = 0.0f;
+        for (int64_t r = r0; r < r1; ++r) partial = partial + base[r * inner];
+        total = total + partial;
+    }
+    out[t] = total * factor;
+}
+
+struct BroadcastMiddle {
+    const float *g;
+    float *out;
+    int64_t reduce, inner;
+    float factor;
+    __device__ void one(int64_t idx) const {
+        const int64_t i = idx % inner;
+        const int64_t o = idx / (reduce * inner);
+        out[idx] = g[o * inner + i] * factor;
+    }
+    __device__ void vec(int64_t v) const {
+        const int64_t idx = v * 4;  // inner % 4 == 0 on this path
+        const int64_t i = idx % inner;
+        const int64_t o = idx / (reduce * inner);
+        STORE4(out, v, LOAD4(g + o * inner + i, 0) * factor);
+    }
+};
+
+}  // namespace
+
+extern "C" {
+
+int axis_mask_gradient(axis_device device, const float *gradient, const float *winners, float *out,
+                       int64_t len) {
+    AXIS_ENTER(device);
+    AXIS_REQUIRE(len >= 0 && (len == 0 || (gradient && winners && out)), "bad mask_gradient args");
+    return launch_map(device, MaskGradient{gradient, winners, out}, len,
+                      all_aligned({gradient, winners, out}), "mask_gradient");
+}
+
+int axis_relu(axis_device device, const float *a, float *out, int64_t len) {
+    AXIS_ENTER(device);
+    AXIS_REQUIRE(len >= 0 && (len == 0 || (a && out)), "bad relu args");
+    return launch_map(device, Relu{a, out}, len, all_aligned({a, out}), "relu");
+}
+
+int axis_relu_backward(axis_device device, const float *gradient, const float *a, float *out,
+                       int64_t len) {
+    AXIS_ENTER(device);
+    AXIS_REQUIRE(len >= 0 && (len == 0 || (gradient && a && out)), "bad relu_backward args");
+    return launch_map(device, ReluBackward{gradient, a, out}, len, all_aligned({gradient, a, out}),
+                      "relu_backward");
+}
+
+int axis_scale(axis_device device, const float *a, float factor, float *out, int64_t len) {
+    AXIS_ENTER(device);
+    AXIS_REQUIRE(len >= 0 && (len == 0 || (a && out)), "bad scale args");
+    return launch_map(device, Scale{a, factor, out}, len, all_aligned({a, out}), "scale");
+}
+
+int axis_binary(axis_device device, const float *a, const float *b, int32_t op, float *out,
+                int64_t len) {
+    AXIS_ENTER(device);
+    AXIS_REQUIRE(op >= 0 && op <= 3, "binary op must be 0 (add), 1 (sub), 2 (mul) or 3 (div)");
+    AXIS_REQUIRE(len >= 0 && (len == 0 || (a && b && out)), "bad binary args");
+    const bool v = all_aligned({a, b, out});
+    switch (op) {
+    case 0: return launch_map(device, Binary<0>{a, b, out}, len, v, "binary_add");
+    case 1: return launch_map(device, Binary<1>{a, b, out}, len, v, "binary_sub");
+    case 2: return launch_map(device, Binary<2>{a, b, out}, len, v, "binary_mul");
+    default: return launch_map(device, Binary<3>{a, b, out}, len, v, "binary_div");
+    }
+}
+
+int axis_select_axis(axis_device device, const float *input, float *out, const int32_t *metadata,
+                     int32_t rank, int32_t coordinate, int64_t output_len) {
+    AXIS_ENTER(device);
+    AXIS_REQUIRE(input && out, "null select_axis buffer");
+    SelectArgs a{};
+    if (int s = select_args(metadata, rank, coordinate, output_len, true, &a)) return s;
+    select_axis_kernel<<<axis::blocks_for(output_len, kBlock, INT32_MAX), kBlock, 0, device->stream>>>(
+        input, out, a);
+    return axis::launch_status("select_axis_kernel");
+}
+
+int axis_select_axis_backward(axis_device device, const float *gradient, float *out,
+                              const int32_t *metadata, int32_t rank, int32_t coordinate,
+                              int64_t input_len) {
+    AXIS_ENTER(device);
+    AXIS_REQUIRE(gradient && out, "null select_axis_backward buffer");
+    SelectArgs a{};
+    if (int s = select_args(metadata, rank, coordinate, input_len, false, &a)) return s;
+    select_axis_backward_kernel<<<axis::blocks_for(input_len, kBlock, INT32_MAX), kBlock, 0,
+                                  device->stream>>>(gradient, out, a);
+    return axis::launch_status("select_axis_backward_kernel");
+}
+
+int axis_inverse_sqrt(axis_device device, const float *a, float epsilon, float *out, int64_t len) {
+    AXIS_ENTER(device);
+    AXIS_REQUIRE(len >= 0 && (len == 0 || (a && out)), "bad inverse_sqrt args");
+    return launch_map(device, InverseSqrt{a, epsilon, out}, len, all_aligned({a, out}),
+                      "inverse_sqrt");
+}
+
+int axis_multiply_scalar(axis_device device, const float *a, const float *scalar, float *out,
+                         int64_t len) {
+    AXIS_ENTER(device);
+    AXIS_REQUIRE(scalar, "device scalar multiplier must contain exactly one value");
+    AXIS_REQUIRE(len >= 0 && (len == 0 || (a && out)), "bad multiply_scalar args");
+    return launch_map(device, MultiplyScalar{a, scalar, out}, len, all_aligned({a, out}),
+                      "multiply_scalar");
+}
+
+int axis_sum_squares(axis_device device, const float *a, int64_t len, float *out) {
+    AXIS_ENTER(device);
+    AXIS_REQUIRE(len >= 1, "sum of squares requires a nonempty buffer");
+    AXIS_REQUIRE(a && out, "null sum_squares buffer");
+    const int blocks = (int)axis::blocks_for(len, kBlock * 8, 1024);
+    axis::Scratch partial;
+    if (int s = partial.get(device, sizeof(float) * blocks)) return s;
+    sum_squares_kernel<<<blocks, kBlock, 0, device->stream>>>(a, len, partial.as<float>());
+    if (int s = axis::launch_status("sum_squares_kernel")) return s;
+    sum_kernel<<<1, kBlock, 0, device->stream>>>(partial.as<float>(), blocks, out);
+    return axis::launch_status("sum_kernel");
+}
+
+int axis_bias_add(axis_device device, const float *a, const float *bias, float *out,
+                  float *relu_out, int64_t rows, int64_t width) {
+    AXIS_ENTER(device);
+    AXIS_REQUIRE(a && bias && out, "null bias_add buffer");
+    AXIS_REQUIRE(rows >= 1 && width >= 1, "bias_add extents must be positive");
+    const bool v = width % 4 == 0 && all_aligned({a, bias, out, relu_out});
+    return launch_map(device, BiasAdd{a, bias, out, relu_out, FastDiv(1), width}, rows * width, v,
+                      "bias_add");
+}
+
+int axis_bias_gradient(axis_device device, const float *gradient, const float *relu_input,
+                       float *masked_out, float *out, int64_t rows, int64_t width) {
+    AXIS_ENTER(device);
+    AXIS_REQUIRE(gradient && out, "null bias_gradient buffer");
+    AXIS_REQUIRE(!relu_input || masked_out, "a masked bias gradient needs masked_out");
+    AXIS_REQUIRE(rows >= 1 && width >= 1, "bias_gradient extents must be positive");
+    const int64_t chunks = (rows + axis::kGroupedChunk - 1) / axis::kGroupedChunk;
+    const int64_t column_blocks = (width + kBlock - 1) / kBlock;
+    AXIS_REQUIRE(chunks * column_blocks < INT32_MAX, "bias_gradient too large");
+    axis::Scratch partial;
+    if (int s = partial.get(device, sizeof(float) * (size_t)(chunks * width))) return s;
+    const unsigned grid = (unsigned)(chunks * column_blocks);
+    if (relu_input)
+        column_chunk_kernel<true><<<grid, kBlock, 0, device->stream>>>(
+            gradient, relu_input, masked_out, partial.as<float>(), rows, width, column_blocks);
+    else
+        column_chunk_kernel<false><<<grid, kBlock, 0, device->stream>>>(
+            gradient, nullptr, nullptr, partial.as<float>(), rows, width, column_blocks);
+    if (int s = axis::launch_status("column_chunk_kernel")) return s;
+    column_combine_kernel<<<(unsigned)column_blocks, kBlock, 0, device->stream>>>(
+        partial.as<float>(), chunks, width, 1.0f, out);
+    return axis::launch_status("column_combine_kernel");
+}
+
+int axis_reduce_middle(axis_device device, const float *a, float *out, int64_t outer,
+                       int64_t reduce, int64_t inner, float factor) {
+    AXIS_ENTER(device);
+    AXIS_REQUIRE(a && out, "null reduce_middle buffer");
+    AXIS_REQUIRE(outer >= 1 && reduce >= 1 && inner >= 1, "reduce_middle extents must be positive");
+    reduce_middle_kernel<<<axis::blocks_for(outer * inner, kBlock, INT32_MAX), kBlock, 0,
+                           device->stream>>>(a, out, outer, reduce, inner, factor);
+    return axis::launch_status("reduce_middle_kernel");
+}
+
+int axis_broadcast_middle(axis_device device, const float *gradient, float *out, int64_t outer,
+                          int64_t reduce, int64_t inner, float factor) {
+    AXIS_ENTER(device);
+    AXIS_REQUIRE(gradient && out, "null broadcast_middle buffer");
+    AXIS_REQUIRE(outer >= 1 && reduce >= 1 && inner >= 1, "broadcast_middle extents must be positive");
+    const bool v = inner % 4 == 0 && all_aligned({gradient, out});
+    return launch_map(device, BroadcastMiddle{gradient, out, reduce, inner, factor},
+                      outer * reduce * inner, v, "broadcast_middle");
+}
+
+}  // extern "C"

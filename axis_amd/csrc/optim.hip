@@ -1,0 +1,201 @@
+// Adam / AdamW update (runtime/backend.rs:1023-1075, kernels adam_moment :2545-2556 and
+// adam_update :2558-2586) fused into one pass: read p, g, m, v and write p', m', v'
+// (28 bytes per parameter instead of the reference's three kernels and three zero-fills).
+// The expression order is the reference's, built with -ffp-contract=off, so the result is
+// bit-identical to a sequential restatement of the three kernels.  The multi-tensor entry
+// updates up to kMaxTensors tensors per launch, blocks split among them by size.
+#include "common.hpp"
+
+namespace {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int kBlock = 256;
+constexpr int kMaxTensors = 24;
+constexpr int kVecPerThread = 4;  // float4 vectors per thread per block-chunk
+
+struct AdamHyper {
+    float lr, b1, b2, one_minus_b1, one_minus_b2, c1, c2, eps, wd;
+};
+
+__device__ __forceinline__ void adam_one(float &p, float g, float &m, float &v, float lr,
+                                         const AdamHyper &h) {
+    const float m_next = h.b1 * m + h.one_minus_b1 * g;
+    const float gg = g * g;
+    const float v_next = h.b2 * v + h.one_minus_b2 * gg;
+    const float mh = m_next / h.c1;
+    const float vh = v_next / h.c2;
+    const float denom = sqrtf(vh) + h.eps;
+    const float step = mh / denom + h.wd * p;
+    p = p - lr * step;
+    m = m_next;
+    v = v_next;
+}
+
+struct AdamTensorArg {
+    float *value;
+    const float *gradient;
+    float *first;
+    float *second;
+    const float *rates;
+    int64_t len;
+    int64_t block_begin;  // first block index of this tensor
+    int32_t vec;          // 16-byte aligned and handled with float4
+};
+
+struct AdamMultiArgs {
+    AdamTensorArg t[kMaxTensors];
+    int32_t count;
+    AdamHyper h;
+};
+
+__global__ void __launch_bounds__(kBlock) adam_multi_kernel(AdamMultiArgs args) {
+    int ti = 0;
+    while (ti + 1 < args.count && (int64_t)blockIdx.x >= args.t[ti + 1].block_begin) ++ti;
+    const AdamTensorArg &t = args.t[ti];
+    const int64_t local_block = blockIdx.x - t.block_begin;
+    constexpr int64_t per_block = (int64_t)kBlock * kVecPerThread * 4;  // elements per block
+    const int64_t begin = local_block * per_block;
+    const int64_t end = begin + per_block < t.len ? begin + per_block : t.len;
+    const AdamHyper h = args.h;
+    if (t.vec && !t.rates) {
+        // whole float4 vectors, lanes striding by the block so each access coalesces
+        const int64_t vbegin = begin / 4, vend = end / 4;
+        floatx4 *pv = reinterpret_cast<floatx4 *>(t.value);
+        const floatx4 *gv = reinterpret_cast<const floatx4 *>(t.gradient);
+        floatx4 *mv = reinterpret_cast<floatx4 *>(t.first);
+        floatx4 *vv = reinterpret_cast<floatx4 *>(t.second);
+#pragma unroll
+        for (int u = 0; u < kVecPerThread; ++u) {
+            const int64_t i = vbegin + threadIdx.x + (int64_t)u * kBlock;
+            if (i < vend) {
+                floatx4 p = pv[i], g = gv[i], m = mv[i], v = vv[i];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    float pc = p[c], mc = m[c], vc = v[c];
+                    adam_one(pc, g[c], mc, vc, h.lr, h);
+                    p[c] = pc;
+                    m[c] = mc;
+                    v[c] = vc;
+                }
+                pv[i] = p;
+                mv[i] = m;
+                vv[i] = v;
+            }
+        }
+        for (int64_t i = vend * 4 + threadIdx.x; i < end; i += kBlock) {
+            float p = t.value[i], m = t.first[i], v = t.second[i];
+            adam_one(p, t.gradient[i], m, v, h.lr, h);
+            t.value[i] = p;
+            t.first[i] = m;
+            t.second[i] = v;
+        }
+    } else {
+        for (int64_t i = begin + threadIdx.x; i < end; i += kBlock) {
+            float p = t.value[i], m = t.first[i], v = t.second[i];
+            adam_one(p, t.gradient[i], m, v, t.rates ? t.rates[i] : h.lr, h);
+            t.value[i] = p;
+            t.first[i] = m;
+            t.second[i] = v;
+        }
+    }
+}
+
+// Out-of-place single tensor (outputs may alias inputs).
+__global__ void __launch_bounds__(kBlock) adam_kernel(const float *__restrict__ value,
+                                                      const float *__restrict__ gradient,
+                                                      const float *__restrict__ first,
+                                                      const float *__restrict__ second,
+                                                      const float *__restrict__ rates, int64_t len,
+                                                      AdamHyper h, float *out_value, float *out_first,
+                                                      float *out_second) {
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < len;
+         i += (int64_t)gridDim.x * kBlock) {
+        float p = value[i], m = first[i], v = second[i];
+        adam_one(p, gradient[i], m, v, rates ? rates[i] : h.lr, h);
+        out_value[i] = p;
+        out_first[i] = m;
+        out_second[i] = v;
+    }
+}
+
+AdamHyper hyper(float lr, float b1, float b2, float c1, float c2, float eps, float wd) {
+    AdamHyper h;
+    h.lr = lr;
+    h.b1 = b1;
+    h.b2 = b2;
+    h.one_minus_b1 = 1.0f - b1;
+    h.one_minus_b2 = 1.0f - b2;
+    h.c1 = c1;
+    h.c2 = c2;
+    h.eps = eps;
+    h.wd = wd;
+    return h;
+}
+
+}  // namespace
+
+extern "C" {
+
+int axis_adam(axis_device device, const float *value, const float *gradient, const float *first,
+              const float *second, const float *learning_rates, int64_t len, float learning_rate,
+              float beta1, float beta2, float correction1, float correction2, float epsilon,
+              float weight_decay, float *out_value, float *out_first, float *out_second) {
+    AXIS_ENTER(device);
+    AXIS_REQUIRE(len >= 0, "negative length");
+    if (len == 0) return AXIS_OK;
+    AXIS_REQUIRE(value && gradient && first && second && out_value && out_first && out_second,
+                 "null adam buffer");
+    const AdamHyper h = hyper(learning_rate, beta1, beta2, correction1, correction2, epsilon,
+                              weight_decay);
+    adam_kernel<<<axis::blocks_for(len, kBlock, (int64_t)device->multiprocessors * 16), kBlock, 0,
+                  device->stream>>>(value, gradient, first, second, learning_rates, len, h,
+                                    out_value, out_first, out_second);
+    return axis::launch_status("adam_kernel");
+}
+
+int axis_adam_multi(axis_device device, const axis_adam_tensor *tensors, int32_t count,
+                    float learning_rate, float beta1, float beta2, float correction1,
+                    float correction2, float epsilon, float weight_decay) {
+    AXIS_ENTER(device);
+    AXIS_REQUIRE(count >= 0 && (count == 0 || tensors), "bad adam_multi tensor list");
+    for (int32_t i = 0; i < count; ++i) {
+        const axis_adam_tensor &t = tensors[i];
+        AXIS_REQUIRE(t.len >= 0, "negative adam tensor length");
+        AXIS_REQUIRE(t.len == 0 || (t.value && t.gradient && t.first && t.second),
+                     "null adam tensor buffer");
+    }
+    const AdamHyper h = hyper(learning_rate, beta1, beta2, correction1, correction2, epsilon,
+                              weight_decay);
+    constexpr int64_t per_block = (int64_t)kBlock * kVecPerThread * 4;
+    int32_t i = 0;
+    while (i < count) {
+        AdamMultiArgs args{};
+        args.h = h;
+        int64_t blocks = 0;
+        int32_t n = 0;
+        for (; i < count && n < kMaxTensors; ++i) {
+            const axis_adam_tensor &t = tensors[i];
+            if (t.len == 0) continue;
+            AdamTensorArg &a = args.t[n++];
+            a.value = t.value;
+            a.gradient = t.gradient;
+            a.first = t.first;
+            a.second = t.second;
+            a.rates = t.learning_rates;
+            a.len = t.len;
+            a.block_begin = blocks;
+            a.vec = axis::aligned16(t.value) && axis::aligned16(t.gradient) &&
+                    axis::aligned16(t.first) && axis::aligned16(t.second);
+            blocks += (t.len + per_block - 1) / per_block;
+        }
+        if (n == 0) continue;
+        AXIS_REQUIRE(blocks < INT32_MAX, "adam_multi launch too large");
+        args.count = n;
+        adam_multi_kernel<<<(unsigned)blocks, kBlock, 0, device->stream>>>(args);
+        if (int s = axis::launch_status("adam_multi_kernel")) return s;
+    }
+    return AXIS_OK;
+}
+
+}  // extern "C"

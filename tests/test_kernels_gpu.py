@@ -1,0 +1,374 @@
+"""Parity of every C-ABI entry (include/axis_hip.h) against the CPU oracle on the same inputs.
+
+Index and byte work (im2col, winners, argmax) and every kernel that keeps the reference's
+evaluation order (col2im, CSR sums, elementwise, Adam) must be bit-identical; GEMMs and the
+softmax family are checked to the stated fp32 tolerance.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from axis_amd import hip
+from axis_amd.hip import F32, I32, I64, VP
+from tests.conftest import close
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    return hip.Device(0)
+
+
+def up(dev, a, dtype=np.float32):
+    return dev.upload(np.ascontiguousarray(a, dtype=dtype))
+
+
+def rel_err(actual, expected):
+    e = np.asarray(expected, np.float64)
+    return float(np.abs(np.asarray(actual, np.float64) - e).max() / max(np.abs(e).max(), 1e-30))
+
+
+# ---------------------------------------------------------------- contractions
+
+GEMM_SHAPES = [(1, 1, 1, 1), (1, 7, 5, 9), (2, 33, 27, 64), (1, 130, 129, 131), (3, 64, 64, 64),
+               (1, 256, 256, 1000), (1, 300, 576, 128), (1, 2048, 27, 64), (1, 40000, 27, 64),
+               (1, 512, 1152, 256)]
+
+
+@pytest.mark.parametrize("batch,m,k,n", GEMM_SHAPES)
+def test_matmul_family(dev, oracle, batch, m, k, n):
+    rng = np.random.default_rng(batch * 1000 + m + k + n)
+    a = rng.standard_normal(batch * m * k).astype(np.float32)
+    b = rng.standard_normal(batch * k * n).astype(np.float32)
+    g = rng.standard_normal(batch * m * n).astype(np.float32)
+    da, db, dg = up(dev, a), up(dev, b), up(dev, g)
+    out = dev.empty(batch * m * n)
+    dev.call("axis_matmul", da.vp, db.vp, out.vp, I64(batch), I64(m), I64(k), I64(n))
+    assert rel_err(dev.read(out, batch * m * n), oracle.matmul(a, b, batch, m, k, n)) < 1e-5
+    out = dev.empty(batch * m * k)
+    dev.call("axis_matmul_left_backward", dg.vp, db.vp, out.vp, I64(batch), I64(m), I64(k), I64(n))
+    assert rel_err(dev.read(out, batch * m * k), oracle.matmul_left_backward(g, b, batch, m, k, n)) < 1e-5
+    out = dev.empty(batch * k * n)
+    dev.call("axis_matmul_right_backward", da.vp, dg.vp, out.vp, I64(batch), I64(m), I64(k), I64(n))
+    assert rel_err(dev.read(out, batch * k * n), oracle.matmul_right_backward(a, g, batch, m, k, n)) < 1e-5
+
+
+def test_matmul_rejects_bad_extents(dev):
+    buf = dev.empty(4)
+    with pytest.raises(hip.AxisError, match="positive"):
+        dev.call("axis_matmul", buf.vp, buf.vp, buf.vp, I64(1), I64(0), I64(1), I64(1))
+
+
+# ---------------------------------------------------------------- unfold / col2im
+
+def _spec(oracle, u):
+    s = hip.UnfoldSpec()
+    ctypes.memmove(ctypes.byref(s), ctypes.byref(u.spec), ctypes.sizeof(s))
+    return s
+
+
+UNFOLD_CASES = [
+    # dims, layout order, channels, group, kernel, stride, padding, fill
+    ([("batch", 2), ("channel", 3), ("height", 9), ("width", 7)], None, 1, [3, 3], [1, 1], [1, 1], 0.0),
+    ([("batch", 2), ("height", 8), ("width", 8), ("channel", 16)], None, 1, [3, 3], [1, 1], [1, 1], 0.0),
+    ([("batch", 2), ("height", 9), ("width", 7), ("channel", 4)], None, 4, [2, 2], [2, 2], [0, 0], float("-inf")),
+    ([("batch", 3), ("channel", 4), ("height", 6), ("width", 5)], ["width", "batch", "channel", "height"], 2,
+     [3, 2], [2, 1], [2, 1], 0.0),
+]
+
+
+@pytest.mark.parametrize("case", range(len(UNFOLD_CASES)))
+def test_unfold_and_col2im_bit_exact(dev, oracle, case):
+    dims, order, groups, kernel, stride, padding, fill = UNFOLD_CASES[case]
+    strides = oracle.layout_for(dims, order) if order else oracle.contiguous(dims)
+    cin = dict(dims)["channel"]
+    group = ("channel", cin) if groups == cin and fill != 0.0 else ("group", groups)
+    u = oracle.unfold_spec(dims, strides, "channel", ["height", "width"], group,
+                           ("patch", cin // groups * kernel[0] * kernel[1]), kernel, stride, padding, fill)
+    rng = np.random.default_rng(case)
+    x = rng.standard_normal(oracle.shape_len(dims)).astype(np.float32)
+    spec = _spec(oracle, u)
+    dx = up(dev, x)
+    out = dev.empty(spec.output_len)
+    dev.call("axis_unfold", dx.vp, out.vp, ctypes.byref(spec))
+    assert np.array_equal(dev.read(out, spec.output_len), oracle.unfold2d(x, u))
+    y = rng.standard_normal(spec.output_len).astype(np.float32)
+    dy = up(dev, y)
+    back = dev.empty(spec.input_len)
+    dev.call("axis_unfold_backward", dy.vp, back.vp, ctypes.byref(spec))
+    assert np.array_equal(dev.read(back, spec.input_len), oracle.unfold2d_backward(y, u, len(x)))
+
+
+def test_unfold_conv2_shape_bit_exact(dev, oracle):
+    # conv2 geometry of the 3-block CNN at batch 8 (NHWC input, 64 channels)
+    dims = [("batch", 8), ("height", 32), ("width", 32), ("c", 64)]
+    u = oracle.unfold_spec(dims, oracle.contiguous(dims), "c", ["height", "width"], ("group", 1),
+                           ("patch", 576), [3, 3], [1, 1], [1, 1], 0.0)
+    x = np.random.default_rng(9).standard_normal(oracle.shape_len(dims)).astype(np.float32)
+    spec = _spec(oracle, u)
+    dx, out = up(dev, x), dev.empty(spec.output_len)
+    dev.call("axis_unfold", dx.vp, out.vp, ctypes.byref(spec))
+    patches = dev.read(out, spec.output_len)
+    assert np.array_equal(patches, oracle.unfold2d(x, u))
+    back = dev.empty(spec.input_len)
+    dev.call("axis_unfold_backward", out.vp, back.vp, ctypes.byref(spec))
+    assert np.array_equal(dev.read(back, spec.input_len), oracle.unfold2d_backward(patches, u, len(x)))
+
+
+# ---------------------------------------------------------------- CSR plans
+
+def _plan(dev, plan, uncapped=False):
+    handle = ctypes.c_void_p()
+    right = plan.right.ctypes.data_as(VP) if len(plan.right) else None
+    dev.call("axis_plan_create", plan.offsets.ctypes.data_as(VP), plan.left.ctypes.data_as(VP), right,
+             I64(len(plan.offsets) - 1), ctypes.c_int(1 if uncapped else 0), ctypes.byref(handle))
+    return handle
+
+
+def test_grouped_sum_and_product_bit_exact(dev, oracle):
+    rng = np.random.default_rng(4)
+    a = rng.standard_normal(5000).astype(np.float32)
+    b = rng.standard_normal(5000).astype(np.float32)
+    groups = [[(int(rng.integers(5000)), int(rng.integers(5000))) for _ in range(n)]
+              for n in (0, 1, 511, 512, 513, 1300, 7)]
+    plan = oracle.plan_groups(groups, product=True)
+    h = _plan(dev, plan)
+    da, db = up(dev, a), up(dev, b)
+    out = dev.empty(len(groups))
+    dev.call("axis_grouped", da.vp, None, h, F32(0.5), out.vp)
+    assert np.array_equal(dev.read(out, len(groups)), oracle.grouped(a, None, plan, 0.5))
+    dev.call("axis_grouped", da.vp, db.vp, h, F32(1.0), out.vp)
+    assert np.array_equal(dev.read(out, len(groups)), oracle.grouped(a, b, plan, 1.0))
+    dev.call("axis_plan_destroy", h)
+
+
+def test_plan_cap_is_enforced(dev, oracle):
+    offsets = np.array([0, 16_777_217], np.int32)
+    left = np.zeros(16_777_217, np.int32)
+    handle = ctypes.c_void_p()
+    with pytest.raises(hip.AxisError, match="16777216"):
+        dev.call("axis_plan_create", offsets.ctypes.data_as(VP), left.ctypes.data_as(VP), None,
+                 I64(1), ctypes.c_int(0), ctypes.byref(handle))
+
+
+def test_grouped_minimum_pool_winners_bit_exact(dev, oracle):
+    rng = np.random.default_rng(5)
+    dims = [("batch", 2), ("height", 6), ("width", 6), ("c", 8)]
+    x = rng.integers(-3, 3, oracle.shape_len(dims)).astype(np.float32)  # many ties
+    x[::17] = np.inf
+    x[::23] = np.nan
+    u = oracle.unfold_spec(dims, oracle.contiguous(dims), "c", ["height", "width"], ("c", 8),
+                           ("pool", 9), [3, 3], [2, 2], [1, 1], float("-inf"))
+    q = oracle.scale(oracle.unfold2d(x, u), -1.0)
+    out_dims, fwd, rev = oracle.min_plans(u.shape, u.strides, "pool")
+    ref, ref_mask, ref_w = oracle.grouped_minimum(q, fwd, rev)
+    hf, hr = _plan(dev, fwd), _plan(dev, rev)
+    dq = up(dev, q)
+    n_out = len(fwd.offsets) - 1
+    out, winners, mask = dev.empty(n_out), dev.empty(n_out, np.int32), dev.empty(len(q))
+    dev.call("axis_grouped_minimum", dq.vp, I64(len(q)), hf, hr, out.vp, winners.vp, mask.vp)
+    got = dev.read(out, n_out)
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    assert np.array_equal(got[~np.isnan(got)], ref[~np.isnan(ref)])
+    assert np.array_equal(dev.read(winners, n_out, np.int32), ref_w)
+    assert np.array_equal(dev.read(mask, len(q)), ref_mask)
+
+
+# ---------------------------------------------------------------- elementwise
+
+@pytest.mark.parametrize("n", [1, 7, 4096, 100003])
+def test_elementwise_bit_exact(dev, oracle, n):
+    rng = np.random.default_rng(n)
+    a = rng.standard_normal(n).astype(np.float32)
+    a[: min(n, 3)] = [0.0, -0.0, 1.0][: min(n, 3)]
+    b = rng.standard_normal(n).astype(np.float32) + 3.0
+    da, db, out = up(dev, a), up(dev, b), dev.empty(n)
+    dev.call("axis_relu", da.vp, out.vp, I64(n))
+    assert np.array_equal(dev.read(out, n), oracle.relu(a))
+    dev.call("axis_relu_backward", db.vp, da.vp, out.vp, I64(n))
+    assert np.array_equal(dev.read(out, n), oracle.relu_backward(b, a))
+    dev.call("axis_mask_gradient", db.vp, da.vp, out.vp, I64(n))
+    assert np.array_equal(dev.read(out, n), oracle.mask_gradient(b, a))
+    dev.call("axis_scale", da.vp, F32(-0.37), out.vp, I64(n))
+    assert np.array_equal(dev.read(out, n), oracle.scale(a, -0.37))
+    for op in range(4):
+        dev.call("axis_binary", da.vp, db.vp, I32(op), out.vp, I64(n))
+        assert np.array_equal(dev.read(out, n), oracle.binary(a, b, op)), op
+    dev.call("axis_inverse_sqrt", db.vp, F32(1e-3), out.vp, I64(n))
+    assert np.array_equal(dev.read(out, n), oracle.inverse_sqrt(b, 1e-3))
+    s = up(dev, np.array([1.7], np.float32))
+    dev.call("axis_multiply_scalar", da.vp, s.vp, out.vp, I64(n))
+    assert np.array_equal(dev.read(out, n), oracle.multiply_scalar(a, [1.7]))
+    one = dev.empty(1)
+    dev.call("axis_sum_squares", da.vp, I64(n), one.vp)
+    close("sum_squares", dev.read(one, 1), oracle.sum_squares(a), rtol=1e-5)
+
+
+def test_select_axis_permutation_and_broadcast(dev, oracle):
+    rng = np.random.default_rng(6)
+    dims = [("a", 3), ("b", 4), ("c", 5)]
+    x = rng.standard_normal(60).astype(np.float32)
+    # permutation to [c, a, b] order: metadata per target dim (extent, input_stride, output_stride)
+    md = np.array([5, 1, 12, 3, 20, 4, 4, 5, 1], np.int32)
+    dx, out = up(dev, x), dev.empty(60)
+    dev.call("axis_select_axis", dx.vp, out.vp, md.ctypes.data_as(VP), I32(3), I32(0), I64(60))
+    got = dev.read(out, 60)
+    assert np.array_equal(got, oracle.select_axis(x, md, 3, 0, 60))
+    assert np.array_equal(got, x.reshape(3, 4, 5).transpose(2, 0, 1).reshape(-1))
+    back = dev.empty(60)
+    bmd = np.array([3, 20, 4, 4, 5, 1, 5, 1, 12], np.int32)
+    dev.call("axis_select_axis_backward", out.vp, back.vp, bmd.ctypes.data_as(VP), I32(3), I32(0), I64(60))
+    assert np.array_equal(dev.read(back, 60), oracle.select_axis_backward(got, bmd, 3, 0, 60))
+    bias = rng.standard_normal(7).astype(np.float32)
+    bmd2 = oracle.broadcast_metadata([("o", 7)], [1], [("r", 11), ("o", 7)])
+    db, out2 = up(dev, bias), dev.empty(77)
+    dev.call("axis_select_axis", db.vp, out2.vp, np.array(bmd2, np.int32).ctypes.data_as(VP), I32(2),
+             I32(0), I64(77))
+    assert np.array_equal(dev.read(out2, 77), np.tile(bias, 11))
+
+
+# ---------------------------------------------------------------- softmax / cross-entropy
+
+@pytest.mark.parametrize("rows,width", [(2, 3), (256, 1000), (5, 2049)])
+def test_softmax_cross_entropy(dev, oracle, rows, width):
+    rng = np.random.default_rng(rows)
+    z = (rng.standard_normal(rows * width) * 4).astype(np.float32)
+    _, y = oracle.one_hot_labels(7, rows, width)
+    y = y.reshape(-1)
+    dz, dy = up(dev, z), up(dev, y)
+    p, loss = dev.empty(rows * width), dev.empty(rows)
+    dev.call("axis_softmax", dz.vp, p.vp, I64(rows), I64(width))
+    pr = dev.read(p, rows * width)
+    close("softmax", pr, oracle.softmax(z, rows, width), atol=1e-7, rtol=2e-6)
+    dev.call("axis_categorical_cross_entropy", dz.vp, dy.vp, loss.vp, I64(rows), I64(width))
+    close("CE", dev.read(loss, rows), oracle.categorical_cross_entropy(z, y, rows, width), rtol=2e-6)
+    p2, l2 = dev.empty(rows * width), dev.empty(rows)
+    dev.call("axis_softmax_cross_entropy", dz.vp, dy.vp, p2.vp, l2.vp, I64(rows), I64(width))
+    assert np.array_equal(dev.read(p2, rows * width), pr)
+    close("fused CE", dev.read(l2, rows), oracle.categorical_cross_entropy(z, y, rows, width), rtol=2e-6)
+    g = rng.standard_normal(rows).astype(np.float32)
+    dg, out = up(dev, g), dev.empty(rows * width)
+    dev.call("axis_categorical_cross_entropy_backward", dg.vp, p.vp, dy.vp, out.vp, I64(rows), I64(width))
+    assert np.array_equal(dev.read(out, rows * width),
+                          oracle.categorical_cross_entropy_backward(g, pr, y, rows, width))
+    gw = rng.standard_normal(rows * width).astype(np.float32)
+    dgw = up(dev, gw)
+    dev.call("axis_softmax_backward", dgw.vp, p.vp, out.vp, I64(rows), I64(width))
+    close("softmax backward", dev.read(out, rows * width), oracle.softmax_backward(gw, pr, rows, width),
+          atol=1e-6, rtol=1e-5)
+
+
+# ---------------------------------------------------------------- Adam
+
+@pytest.mark.parametrize("n", [1, 5, 4096, 65537])
+def test_adam_bit_exact(dev, oracle, n):
+    rng = np.random.default_rng(n + 1)
+    p = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    g = (rng.standard_normal(n) * 1e-3).astype(np.float32)
+    m = (rng.standard_normal(n) * 1e-4).astype(np.float32)
+    v = np.abs(rng.standard_normal(n) * 1e-6).astype(np.float32)
+    c1, c2 = 1 - oracle.powi(0.9, 4), 1 - oracle.powi(0.999, 4)
+    ref = oracle.adam(p, g, m, v, 1e-3, 0.9, 0.999, c1, c2, 1e-8, 0.01)
+    dp, dg, dm, dv = up(dev, p), up(dev, g), up(dev, m), up(dev, v)
+    op, om, ov = dev.empty(n), dev.empty(n), dev.empty(n)
+    dev.call("axis_adam", dp.vp, dg.vp, dm.vp, dv.vp, None, I64(n), F32(1e-3), F32(0.9), F32(0.999),
+             F32(c1), F32(c2), F32(1e-8), F32(0.01), op.vp, om.vp, ov.vp)
+    for got, exp in zip((op, om, ov), ref):
+        assert np.array_equal(dev.read(got, n), exp)
+    # in place, multi-tensor
+    t = hip.AdamTensor(dp.ptr, dg.ptr, dm.ptr, dv.ptr, None, n)
+    arr = (hip.AdamTensor * 2)(t, hip.AdamTensor(None, None, None, None, None, 0))
+    dev.call("axis_adam_multi", arr, I32(2), F32(1e-3), F32(0.9), F32(0.999), F32(c1), F32(c2),
+             F32(1e-8), F32(0.01))
+    for got, exp in zip((dp, dm, dv), ref):
+        assert np.array_equal(dev.read(got, n), exp)
+
+
+def test_adam_multi_many_tensors(dev, oracle):
+    rng = np.random.default_rng(11)
+    sizes = [3, 64, 1000, 4097, 1, 123457] * 5  # 30 tensors: spans two launches
+    tensors, host = [], []
+    for s in sizes:
+        arrs = [(rng.standard_normal(s) * 0.1).astype(np.float32) for _ in range(3)]
+        arrs.append(np.abs(arrs[2]) * 0.01)
+        bufs = [up(dev, a) for a in arrs]
+        host.append(arrs)
+        tensors.append(bufs)
+    arr = (hip.AdamTensor * len(sizes))(*[hip.AdamTensor(b[0].ptr, b[1].ptr, b[2].ptr, b[3].ptr, None, s)
+                                          for b, s in zip(tensors, sizes)])
+    dev.call("axis_adam_multi", arr, I32(len(sizes)), F32(0.01), F32(0.9), F32(0.999), F32(0.1),
+             F32(0.001), F32(1e-8), F32(0.0))
+    for (p, g, m, v), bufs, s in zip(host, tensors, sizes):
+        ref = oracle.adam(p, g, m, v, 0.01, 0.9, 0.999, 0.1, 0.001, 1e-8, 0.0)
+        assert np.array_equal(dev.read(bufs[0], s), ref[0])
+        assert np.array_equal(dev.read(bufs[2], s), ref[1])
+
+
+# ---------------------------------------------------------------- fused entries
+
+@pytest.mark.parametrize("rows,width", [(1, 1), (600, 2), (1030, 64), (777, 130)])
+def test_bias_entries_bit_exact(dev, oracle, rows, width):
+    rng = np.random.default_rng(rows)
+    a = rng.standard_normal(rows * width).astype(np.float32)
+    bias = rng.standard_normal(width).astype(np.float32)
+    g = rng.standard_normal(rows * width).astype(np.float32)
+    da, db, dg = up(dev, a), up(dev, bias), up(dev, g)
+    out, act = dev.empty(rows * width), dev.empty(rows * width)
+    dev.call("axis_bias_add", da.vp, db.vp, out.vp, act.vp, I64(rows), I64(width))
+    z = oracle.binary(a, np.tile(bias, rows), 0)
+    assert np.array_equal(dev.read(out, rows * width), z)
+    assert np.array_equal(dev.read(act, rows * width), oracle.relu(z))
+    gb = dev.empty(width)
+    dev.call("axis_bias_gradient", dg.vp, None, None, gb.vp, I64(rows), I64(width))
+    assert np.array_equal(dev.read(gb, width), oracle.bias_gradient(g, rows, width))
+    masked = dev.empty(rows * width)
+    dev.call("axis_bias_gradient", dg.vp, out.vp, masked.vp, gb.vp, I64(rows), I64(width))
+    gm = oracle.relu_backward(g, z)
+    assert np.array_equal(dev.read(masked, rows * width), gm)
+    assert np.array_equal(dev.read(gb, width), oracle.bias_gradient(gm, rows, width))
+
+
+@pytest.mark.parametrize("kernel,stride,padding", [([2, 2], [2, 2], [0, 0]), ([3, 3], [1, 1], [1, 1]),
+                                                   ([3, 2], [2, 1], [1, 0])])
+def test_max_pool_entries_match_generic_path(dev, oracle, kernel, stride, padding):
+    rng = np.random.default_rng(sum(kernel) + sum(stride))
+    b, h, w, c = 2, 7, 9, 6
+    x = rng.integers(-2, 3, b * h * w * c).astype(np.float32)  # ties everywhere
+    x[::31] = np.nan
+    dims = [("batch", b), ("height", h), ("width", w), ("c", c)]
+    u = oracle.unfold_spec(dims, oracle.contiguous(dims), "c", ["height", "width"], ("c", c),
+                           ("pool", kernel[0] * kernel[1]), kernel, stride, padding, float("-inf"))
+    q = oracle.scale(oracle.unfold2d(x, u), -1.0)
+    out_dims, fwd, rev = oracle.min_plans(u.shape, u.strides, "pool")
+    mn, mask, _ = oracle.grouped_minimum(q, fwd, rev)
+    ref = oracle.scale(mn, -1.0)
+    n_out = len(ref)
+    gout = rng.standard_normal(n_out).astype(np.float32)
+    gg = oracle.mask_gradient(oracle.grouped(oracle.scale(gout, -1.0), None, rev, 1.0), mask)
+    ref_dx = oracle.unfold2d_backward(oracle.scale(gg, -1.0), u, len(x))
+    k, s, p = (I32 * 2)(*kernel), (I32 * 2)(*stride), (I32 * 2)(*padding)
+    dx, out, arg = up(dev, x), dev.empty(n_out), dev.empty(n_out, np.uint8)
+    dev.call("axis_max_pool2d", dx.vp, out.vp, arg.vp, I64(b), I32(h), I32(w), I64(c), k, s, p)
+    got = dev.read(out, n_out)
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    assert np.array_equal(got[~np.isnan(ref)], ref[~np.isnan(ref)])
+    dg, back = up(dev, gout), dev.empty(len(x))
+    dev.call("axis_max_pool2d_backward", dg.vp, arg.vp, back.vp, I64(b), I32(h), I32(w), I64(c), k, s, p)
+    assert np.array_equal(dev.read(back, len(x)), ref_dx)
+
+
+def test_reduce_and_broadcast_middle_bit_exact(dev, oracle):
+    rng = np.random.default_rng(12)
+    outer, red, inner = 3, 1100, 5
+    a = rng.standard_normal(outer * red * inner).astype(np.float32)
+    dims = [("o", outer), ("r", red), ("i", inner)]
+    _, fwd, rev, factor = oracle.reduction_plans(dims, oracle.contiguous(dims), ["r"], mean=True)
+    da, out = up(dev, a), dev.empty(outer * inner)
+    dev.call("axis_reduce_middle", da.vp, out.vp, I64(outer), I64(red), I64(inner), F32(factor))
+    got = dev.read(out, outer * inner)
+    assert np.array_equal(got, oracle.grouped(a, None, fwd, factor))
+    back = dev.empty(len(a))
+    dev.call("axis_broadcast_middle", out.vp, back.vp, I64(outer), I64(red), I64(inner), F32(factor))
+    assert np.array_equal(dev.read(back, len(a)), oracle.grouped(got, None, rev, factor))
