@@ -78,7 +78,7 @@ def build_host(jobs: int = 8) -> str | None:
     suffix = sysconfig.get_config_var("EXT_SUFFIX")
     target = os.path.join(HERE, "_axis" + suffix)
     py_inc = sysconfig.get_paths()["include"]
-    flags = ["-O2", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",
+    flags = ["-O2", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function", "-ffp-contract=off",
              f"-I{pybind11.get_include()}", f"-I{py_inc}", f"-I{os.path.join(ROOT, 'include')}",
              f"-I{HOST}", "-fvisibility=hidden"]
     os.makedirs(BUILD, exist_ok=True)

@@ -6,6 +6,7 @@
 
 #include <cstdint>
 #include <map>
+#include <vector>
 #include <string>
 #include <unordered_map>
 
@@ -21,6 +22,14 @@ struct axis_device_s {
     size_t in_use = 0;
     size_t cached = 0;
     int multiprocessors = 256;
+    // launch timing (axis_timing_*): event pairs and work per family
+    bool timing = false;
+    struct Timed {
+        hipEvent_t start, stop;
+        double work;
+    };
+    std::map<std::string, std::vector<Timed>> timed;
+    std::vector<hipEvent_t> spare_events;
 };
 
 struct axis_plan_s {
@@ -69,6 +78,17 @@ inline unsigned blocks_for(int64_t work, int per_block, int64_t cap = 1 << 20) {
     if (b > cap) b = cap;
     return static_cast<unsigned>(b);
 }
+
+// Brackets one launch of a timed family with events on the device's stream (no-op unless
+// timing is enabled).
+struct TimedLaunch {
+    axis_device device;
+    const char *family;
+    double work;
+    hipEvent_t start = nullptr;
+    TimedLaunch(axis_device d, const char *f, double w);
+    ~TimedLaunch();
+};
 
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 

@@ -78,6 +78,33 @@ void release(axis_device device, void *ptr) {
     device->live.erase(it);
 }
 
+namespace {
+hipEvent_t take_event(axis_device device) {
+    if (!device->spare_events.empty()) {
+        hipEvent_t e = device->spare_events.back();
+        device->spare_events.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+}  // namespace
+
+TimedLaunch::TimedLaunch(axis_device d, const char *f, double w) : device(d), family(f), work(w) {
+    if (!device->timing) return;
+    start = take_event(device);
+    if (start) (void)hipEventRecord(start, device->stream);
+}
+
+TimedLaunch::~TimedLaunch() {
+    if (!start) return;
+    hipEvent_t stop = take_event(device);
+    if (!stop) return;
+    (void)hipEventRecord(stop, device->stream);
+    device->timed[family].push_back({start, stop, work});
+}
+
 }  // namespace axis
 
 namespace {
@@ -127,6 +154,12 @@ int axis_device_destroy(axis_device device) {
     AXIS_HIP(hipStreamSynchronize(device->stream));
     for (auto &kv : device->free_blocks) (void)hipFree(kv.second);
     for (auto &kv : device->live) (void)hipFree(kv.first);
+    for (auto &kv : device->timed)
+        for (auto &t : kv.second) {
+            (void)hipEventDestroy(t.start);
+            (void)hipEventDestroy(t.stop);
+        }
+    for (hipEvent_t e : device->spare_events) (void)hipEventDestroy(e);
     (void)hipStreamDestroy(device->stream);
     delete device;
     return AXIS_OK;
@@ -209,6 +242,47 @@ int axis_fill(axis_device device, float *out, float value, int64_t len) {
     AXIS_REQUIRE(out, "null output");
     fill_kernel<<<axis::blocks_for(len, 256, 8192), 256, 0, device->stream>>>(out, value, len);
     return axis::launch_status("fill_kernel");
+}
+
+int axis_timing_enable(axis_device device, int enabled) {
+    AXIS_ENTER(device);
+    device->timing = enabled != 0;
+    return AXIS_OK;
+}
+
+int axis_timing_reset(axis_device device) {
+    AXIS_ENTER(device);
+    AXIS_HIP(hipStreamSynchronize(device->stream));
+    for (auto &kv : device->timed)
+        for (auto &t : kv.second) {
+            device->spare_events.push_back(t.start);
+            device->spare_events.push_back(t.stop);
+        }
+    device->timed.clear();
+    return AXIS_OK;
+}
+
+int axis_timing_read(axis_device device, const char *family, int64_t *launches, double *milliseconds,
+                     double *work) {
+    AXIS_ENTER(device);
+    AXIS_REQUIRE(family, "null timing family");
+    AXIS_HIP(hipStreamSynchronize(device->stream));
+    int64_t n = 0;
+    double ms = 0.0, w = 0.0;
+    auto it = device->timed.find(family);
+    if (it != device->timed.end()) {
+        for (auto &t : it->second) {
+            float elapsed = 0.0f;
+            AXIS_HIP(hipEventElapsedTime(&elapsed, t.start, t.stop));
+            ms += elapsed;
+            w += t.work;
+            ++n;
+        }
+    }
+    if (launches) *launches = n;
+    if (milliseconds) *milliseconds = ms;
+    if (work) *work = w;
+    return AXIS_OK;
 }
 
 int axis_plan_create(axis_device device, const int32_t *offsets, const int32_t *left,

@@ -274,6 +274,7 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out) {
     }
     if (batch * splits > 65535)
         return axis::fail(AXIS_ERROR_INVALID, "matmul batch too large for one launch");
+    axis::TimedLaunch timed(device, "gemm", 2.0 * (double)batch * (double)p.m * (double)p.n * (double)p.k);
     dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n), static_cast<unsigned>(batch * splits));
     if (big)
         launch_vec<128, 128, 2, 2, XR, YR>(p, grid, device->stream, vx, vy);

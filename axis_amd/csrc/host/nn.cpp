@@ -1,0 +1,291 @@
+// Parameters and the hot-path modules: Linear (model/nn.rs:186-295), Conv2d
+// (model/convolution.rs:38-305), MaxPool2d (convolution.rs:1334-1556), ReLU and Sequential
+// (nn.rs:1885-1896, :3731-3790).
+#include <atomic>
+#include <cmath>
+
+#include "axis.hpp"
+
+namespace axis {
+
+namespace {
+std::atomic<uint64_t> next_parameter{1};
+}
+
+// ------------------------------------------------------------------ Parameter (nn.rs:14-65)
+
+Parameter Parameter::make(const Tensor &tensor) {
+    Parameter p;
+    p.s = std::make_shared<ParamState>();
+    p.s->id = next_parameter.fetch_add(1);
+    p.s->version = std::make_shared<uint64_t>(0);
+    p.s->tensor = tensor.parameter_leaf(p.s->version);
+    return p;
+}
+
+void Parameter::set_values(const std::vector<float> &values) const {
+    Tensor current = tensor();
+    replace(Tensor::from_slice(values, current.shape().dims, current.device()));
+}
+
+void Parameter::replace(const Tensor &t) const {
+    *s->version += 1;
+    s->tensor = t.parameter_leaf(s->version);
+}
+
+std::vector<Parameter> Module::parameters() {
+    std::vector<Parameter> out;
+    for (auto &kv : named_parameters()) out.push_back(kv.second);
+    return out;
+}
+
+Parameter Module::parameter(const std::string &name) {
+    std::optional<Parameter> found;
+    for (auto &kv : named_parameters()) {
+        if (kv.first != name) continue;
+        if (found) raise("ambiguous parameter path \"" + name + "\"");
+        found = kv.second;
+    }
+    if (!found) raise("unknown parameter \"" + name + "\"; build the model before accessing parameters");
+    return *found;
+}
+
+void Module::zero_grad() {
+    for (auto &p : parameters()) p.zero_grad();
+}
+
+// ------------------------------------------------------------------ Linear
+
+Linear::Linear(const Axis &input_axis, const Dim &out)
+    : input(input_axis),
+      input_role(input_axis.role("linear_input")),
+      output_role(out.axis.role("linear_output")),
+      output(out) {}
+
+Shape Linear::output_shape(const Shape &in) {
+    int64_t extent = in.extent(input);
+    if (bound && std::get<0>(*bound) != extent) raise("Linear input extent differs from its built extent");
+    std::vector<Dim> dims;
+    for (auto &d : in.dims)
+        if (d.axis != input) dims.push_back(d);
+    dims.push_back(output);
+    return Shape::make(dims);
+}
+
+Shape Linear::build(const Shape &in, const Device &device, uint64_t seed) {
+    Shape shape = output_shape(in);
+    if (bound) {
+        if (!std::get<1>(*bound).tensor().device().same(device))
+            raise("Linear is already built on a different Device");
+        return shape;
+    }
+    int64_t extent = in.extent(input);
+    Shape weight_shape = Shape::make({Dim{input_role, extent}, Dim{output_role, output.extent}});
+    const float scale = std::sqrt(6.0f / (float)(extent + output.extent));
+    auto values = xorshift_unit_stream(seed, weight_shape.len);
+    for (auto &v : values) v = (v * 2.0f - 1.0f) * scale;
+    Parameter weight = Parameter::make(Tensor::from_slice(values, weight_shape.dims, device));
+    std::optional<Parameter> b;
+    if (bias)
+        b = Parameter::make(Tensor::from_slice(std::vector<float>((size_t)output.extent, 0.0f),
+                                               {Dim{output_role, output.extent}}, device));
+    bound = std::make_tuple(extent, weight, b);
+    return shape;
+}
+
+Tensor Linear::forward(const Tensor &x) {
+    output_shape(x.shape());
+    if (!bound) raise("Linear must be built before forward");
+    auto &[extent, weight, b] = *bound;
+    (void)extent;
+    Tensor projected = x.rename(input, input_role).contract(weight.tensor(), {input_role});
+    if (b) projected = projected.add(b->tensor());
+    return projected.rename(output_role, output.axis);
+}
+
+std::vector<std::pair<std::string, Parameter>> Linear::named_parameters() {
+    std::vector<std::pair<std::string, Parameter>> out;
+    if (!bound) return out;
+    out.emplace_back("weight", std::get<1>(*bound));
+    if (std::get<2>(*bound)) out.emplace_back("bias", *std::get<2>(*bound));
+    return out;
+}
+
+// ------------------------------------------------------------------ Conv2d
+
+Conv2d::Conv2d(const Axis &input_axis, const Dim &out, const std::vector<Axis> &spatial_axes,
+               const std::vector<int64_t> &kernel_extents)
+    : input(input_axis),
+      group(input_axis.role("conv_group")),
+      patch(input_axis.role("conv_patch_in_group")),
+      output_in_group(out.axis.role("conv_output_in_group")),
+      output_role(out.axis.role("conv_output")),
+      output(out),
+      spatial(spatial_axes),
+      kernel(kernel_extents) {
+    if (spatial.size() != 2 || kernel.size() != 2) raise("Conv2d needs two spatial axes and kernel extents");
+}
+
+Shape Conv2d::output_shape(const Shape &in) {
+    for (size_t i = 0; i < 2; ++i)
+        if (spatial[i] == input || (i == 1 && spatial[0] == spatial[1]))
+            raise("Conv2d requires distinct input-channel and spatial axes");
+    int64_t channels = in.extent(input);
+    if (groups <= 0 || channels % groups || output.extent % groups)
+        raise("Conv2d channels and outputs must be divisible by groups");
+    if (kernel[0] <= 0 || kernel[1] <= 0 || stride[0] <= 0 || stride[1] <= 0)
+        raise("Conv2d kernel and stride must be positive");
+    int64_t out_sp[2];
+    for (int i = 0; i < 2; ++i) {
+        int64_t padded = in.extent(spatial[i]) + 2 * padding[i];
+        if (kernel[i] > padded) raise("Conv2d kernel must fit the padded spatial axes");
+        out_sp[i] = (padded - kernel[i]) / stride[i] + 1;
+    }
+    int64_t patch_extent = channels / groups * kernel[0] * kernel[1];
+    if (bound) {
+        if (bound->channels != channels) raise("Conv2d input channels differ from its built extent");
+        if (bound->patch != patch_extent || bound->output_in_group != output.extent / groups)
+            raise("Conv2d group geometry differs from its built parameters");
+    }
+    std::vector<Dim> dims;
+    for (auto &d : in.dims) {
+        if (d.axis == input) continue;
+        if (d.axis == spatial[0])
+            dims.push_back(Dim{d.axis, out_sp[0]});
+        else if (d.axis == spatial[1])
+            dims.push_back(Dim{d.axis, out_sp[1]});
+        else
+            dims.push_back(d);
+    }
+    dims.push_back(output);
+    return Shape::make(dims);
+}
+
+Shape Conv2d::build(const Shape &in, const Device &device, uint64_t seed) {
+    Shape shape = output_shape(in);
+    if (bound) {
+        if (!bound->weight.tensor().device().same(device))
+            raise("Conv2d is already built on a different Device");
+        return shape;
+    }
+    int64_t channels = in.extent(input);
+    int64_t patch_extent = channels / groups * kernel[0] * kernel[1];
+    int64_t out_in_group = output.extent / groups;
+    Shape weight_shape = Shape::make(
+        {Dim{group, groups}, Dim{patch, patch_extent}, Dim{output_in_group, out_in_group}});
+    // convolution.rs:176-186: xavier-uniform from an inline xorshift stream
+    uint64_t rng = seed > 1 ? seed : 1;
+    const float scale = std::sqrt(6.0f / (float)(patch_extent + out_in_group));
+    std::vector<float> values((size_t)weight_shape.len);
+    for (auto &v : values) {
+        rng ^= rng << 13;
+        rng ^= rng >> 7;
+        rng ^= rng << 17;
+        v = (((float)(rng >> 40) / (float)(1u << 24)) * 2.0f - 1.0f) * scale;
+    }
+    Bound b{channels, patch_extent, out_in_group,
+            Parameter::make(Tensor::from_slice(values, weight_shape.dims, device)), std::nullopt};
+    if (bias)
+        b.bias = Parameter::make(Tensor::from_slice(std::vector<float>((size_t)output.extent, 0.0f),
+                                                    {Dim{output_role, output.extent}}, device));
+    bound = b;
+    return shape;
+}
+
+Tensor Conv2d::forward(const Tensor &x) {
+    output_shape(x.shape());
+    if (!bound) raise("Conv2d must be built before forward");
+    Tensor projected = x.unfold_grouped(input, spatial, Dim{group, groups}, Dim{patch, bound->patch},
+                                        kernel, stride, padding, 0.0f)
+                           .contract(bound->weight.tensor(), {patch})
+                           .merge({group, output_in_group}, output_role);
+    if (bound->bias) projected = projected.add(bound->bias->tensor());
+    return projected.rename(output_role, output.axis);
+}
+
+std::vector<std::pair<std::string, Parameter>> Conv2d::named_parameters() {
+    std::vector<std::pair<std::string, Parameter>> out;
+    if (!bound) return out;
+    out.emplace_back("weight", bound->weight);
+    if (bound->bias) out.emplace_back("bias", *bound->bias);
+    return out;
+}
+
+// ------------------------------------------------------------------ MaxPool2d
+
+MaxPool2d::MaxPool2d(const Axis &channel_axis, const std::vector<Axis> &spatial_axes,
+                     const std::vector<int64_t> &kernel_extents)
+    : channels(channel_axis),
+      patch(channel_axis.role("pool_patch")),
+      spatial(spatial_axes),
+      kernel(kernel_extents),
+      stride(kernel_extents) {
+    if (spatial.size() != 2 || kernel.size() != 2) raise("MaxPool2d needs two spatial axes and kernel extents");
+}
+
+// Spatial axes keep their position at the pooled extent; the channel axis is appended.
+Shape MaxPool2d::output_shape(const Shape &in) {
+    in.extent(channels);
+    std::vector<Dim> dims;
+    for (auto &d : in.dims) {
+        if (d.axis == channels) continue;
+        bool found = false;
+        for (int i = 0; i < 2; ++i) {
+            if (d.axis != spatial[i]) continue;
+            int64_t padded = d.extent + 2 * padding[i];
+            if (kernel[i] <= 0 || stride[i] <= 0) raise("MaxPool2d kernel and stride must be positive");
+            if (kernel[i] > padded) raise("MaxPool2d kernel exceeds the padded spatial extent");
+            dims.push_back(Dim{d.axis, (padded - kernel[i]) / stride[i] + 1});
+            found = true;
+        }
+        if (!found) dims.push_back(d);
+    }
+    dims.push_back(Dim{channels, in.extent(channels)});
+    return Shape::make(dims);
+}
+
+Tensor MaxPool2d::forward(const Tensor &x) {
+    Shape expected = output_shape(x.shape());
+    Tensor out = x.max_pool2d(channels, spatial, kernel, stride, padding);
+    if (!(out.shape() == expected)) {
+        // The fused path keeps the input's axis order; present the reference's order.
+        std::vector<Axis> order = expected.axes();
+        Tensor aligned = out.with_layout(order);
+        std::vector<Dim> dims = expected.dims;
+        return Tensor::node(expected, Layout::contiguous(expected), aligned.value(), aligned.device(),
+                            {Edge{aligned, Rule{}}}, false);
+    }
+    return out;
+}
+
+// ------------------------------------------------------------------ Sequential
+
+Shape Sequential::output_shape(const Shape &in) {
+    Shape s = in;
+    for (auto &l : layers) s = l->output_shape(s);
+    return s;
+}
+
+Shape Sequential::build(const Shape &in, const Device &device, uint64_t seed) {
+    output_shape(in);
+    Shape s = in;
+    for (size_t i = 0; i < layers.size(); ++i) s = layers[i]->build(s, device, seed + i);
+    return s;
+}
+
+Tensor Sequential::forward(const Tensor &x) {
+    output_shape(x.shape());
+    Tensor v = x;
+    for (auto &l : layers) v = l->forward(v);
+    return v;
+}
+
+std::vector<std::pair<std::string, Parameter>> Sequential::named_parameters() {
+    std::vector<std::pair<std::string, Parameter>> out;
+    for (size_t i = 0; i < layers.size(); ++i)
+        for (auto &kv : layers[i]->named_parameters())
+            out.emplace_back(std::to_string(i) + "." + kv.first, kv.second);
+    return out;
+}
+
+}  // namespace axis

@@ -1,0 +1,209 @@
+"""Benchmark of the training hot path on one MI355X.
+
+Workload: one training step of the 3-block CNN -- three blocks of
+conv3x3/s1/p1 (3->64->128->256) + ReLU + 2x2 max-pool, global mean over [height, width], Linear
+256->1000, mean softmax cross-entropy -- forward, backward and one Adam(1e-3) update, fp32, batch
+256, input [256, 3, 64, 64] uniform[0,1) (seed 1), labels from seed 2, He-normal weights (seeds
+10..13), zero biases.  The step runs through the C++ host layer (named-axis Tensor, tape, Trainer)
+on libaxis_hip; inputs are resident in HBM before the timed region.
+
+Prints one JSON line:  images/sec for the whole job, the GEMM family's achieved fp32 MFMA rate
+(HIP events on the library's stream around every GEMM launch inside the timed region) against
+MI355X's 157.3 TFLOP/s, and the CPU oracle timed on this host on a bounded sample.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+BASELINE_METRIC = "images/sec (3-block CNN, bs256, fp32 fwd+bwd+Adam); % of fp32 MFMA peak"
+FP32_MFMA_PEAK_TFLOPS = 157.3
+HBM_PEAK_GBS = 8000.0
+
+BATCH, SIZE, CLASSES, CHANNELS = 256, 64, 1000, (3, 64, 128, 256)
+
+
+def cnn_gemm_flops(batch=BATCH, size=SIZE, classes=CLASSES, ch=CHANNELS) -> float:
+    """Algorithmic GEMM flops of one step: forward, wgrad for every layer, dgrad for every layer
+    but conv1 (its input carries no gradient)."""
+    total, hw = 0.0, size
+    for j in range(3):
+        m, k, n = batch * hw * hw, ch[j] * 9, ch[j + 1]
+        passes = 3 if j > 0 else 2
+        total += passes * 2.0 * m * k * n
+        hw //= 2
+    total += 3 * 2.0 * batch * ch[3] * classes
+    return total
+
+
+def build_step(ax, device, x_host, y_host, params):
+    bt, c0, h, w = ax.Axis("batch"), ax.Axis("channel"), ax.Axis("height"), ax.Axis("width")
+    cs = [c0] + [ax.Axis(f"c{j + 1}") for j in range(3)]
+    cls = ax.Axis("class")
+    layers = []
+    for j in range(3):
+        layers += [ax.Conv2d(cs[j], cs[j + 1].of(CHANNELS[j + 1]), [h, w], [3, 3]).padding([1, 1]),
+                   ax.ReLU(), ax.MaxPool2d(cs[j + 1], [h, w], [2, 2])]
+    features = ax.Sequential(layers)
+    features.build(ax.Shape([bt.of(BATCH), c0.of(3), h.of(SIZE), w.of(SIZE)]), device, 1)
+    head = ax.Linear(cs[3], cls.of(CLASSES))
+    head.build(ax.Shape([bt.of(BATCH), cs[3].of(CHANNELS[3])]), device, 4)
+    model = ax.Sequential([features, head])
+    for j in range(3):
+        model.parameter(f"0.{3 * j}.weight").set_values(params[f"conv{j}.weight"])
+        model.parameter(f"0.{3 * j}.bias").set_values(params[f"conv{j}.bias"])
+    model.parameter("1.weight").set_values(params["linear.weight"])
+    model.parameter("1.bias").set_values(params["linear.bias"])
+    x = ax.Tensor.from_slice(x_host, [bt.of(BATCH), c0.of(3), h.of(SIZE), w.of(SIZE)], device)
+    y = ax.Tensor.from_slice(y_host, [bt.of(BATCH), cls.of(CLASSES)], device)
+    trainer = ax.Trainer(ax.Adam(1e-3))
+
+    def loss_fn(_model):
+        pooled = features.forward(x).mean([h, w])
+        return head.forward(pooled).categorical_cross_entropy_with_logits(y, cls).mean([bt])
+
+    def step():
+        return trainer.step(model, loss_fn)
+
+    return step
+
+
+def synthetic_inputs():
+    """BASELINE config 4 inputs from the reference's xorshift stream (host C++ generator)."""
+    import axis_amd
+    ax = axis_amd.host()
+    x = ax.uniform_host_values(1, BATCH * 3 * SIZE * SIZE, 0.0, 1.0)
+    u = ax.xorshift_unit_stream(2, BATCH)
+    labels = np.minimum(np.floor(u.astype(np.float64) * CLASSES).astype(np.int64), CLASSES - 1)
+    y = np.zeros((BATCH, CLASSES), np.float32)
+    y[np.arange(BATCH), labels] = 1.0
+    params = {}
+    for j in range(3):
+        fan_in = CHANNELS[j] * 9
+        std = float(np.sqrt(np.float32(2.0) / np.float32(fan_in), dtype=np.float32))
+        params[f"conv{j}.weight"] = ax.normal_host_values(10 + j, fan_in * CHANNELS[j + 1], 0.0, std)
+        params[f"conv{j}.bias"] = np.zeros(CHANNELS[j + 1], np.float32)
+    std = float(np.sqrt(np.float32(2.0) / np.float32(CHANNELS[3]), dtype=np.float32))
+    params["linear.weight"] = ax.normal_host_values(13, CHANNELS[3] * CLASSES, 0.0, std)
+    params["linear.bias"] = np.zeros(CLASSES, np.float32)
+    return x, y.reshape(-1), params
+
+
+def cpu_baseline(sample_batch: int):
+    """The CPU oracle (oracle/, a restatement of the reference's step) on `sample_batch` images of
+    the same workload, timed on this host's cores; images/s scales linearly with batch."""
+    from oracle import oracle
+    oracle.build()
+    threads = oracle.threads()
+    oracle.cnn_step(2, SIZE, CLASSES, 1e-3, CHANNELS)  # load the library, touch the code paths
+    start = time.perf_counter()
+    oracle.cnn_step(sample_batch, SIZE, CLASSES, 1e-3, CHANNELS)
+    elapsed = time.perf_counter() - start
+    return {"value": round(sample_batch / elapsed, 3), "unit": "images/sec", "cores": threads,
+            "kind": "port",
+            "sample": f"one fwd+bwd+Adam step of the same 3-block CNN at batch {sample_batch} "
+                      f"(64x64x3, fp64-accumulated GEMMs, OpenMP), {elapsed:.2f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample-batch", type=int, default=32)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: this build has no multi-GPU path "
+              f"(--gpus {args.gpus} requested)", file=sys.stderr)
+        sys.exit(2)
+
+    import axis_amd
+    from axis_amd import hip
+    ax = axis_amd.host()
+    device = ax.Device.hip(0)
+    x, y, params = synthetic_inputs()
+    step = build_step(ax, device, x, y, params)
+    lib = hip.load()
+
+    for _ in range(args.warmup):
+        step()
+    device.synchronize()
+
+    # The host layer's device handle: timing is toggled through the same C ABI.
+    dev_handle = _device_handle(device)
+    lib.axis_timing_reset(dev_handle)
+    lib.axis_timing_enable(dev_handle, 1)
+    device.synchronize()
+    start = time.perf_counter()
+    for _ in range(args.steps):
+        _, loss = step()
+    device.synchronize()
+    elapsed = time.perf_counter() - start
+    lib.axis_timing_enable(dev_handle, 0)
+    launches, ms, work = ctypes.c_int64(), ctypes.c_double(), ctypes.c_double()
+    hip.check(lib.axis_timing_read(dev_handle, b"gemm", ctypes.byref(launches), ctypes.byref(ms),
+                                   ctypes.byref(work)), "axis_timing_read")
+
+    ms_per_step = elapsed * 1000.0 / args.steps
+    value = BATCH * args.steps / elapsed
+    gemm_tflops = work.value / (ms.value * 1e-3) / 1e12 if ms.value > 0 else 0.0
+    per_launch_flops = work.value / max(launches.value, 1)
+    result = {
+        "metric": BASELINE_METRIC,
+        "value": round(value, 2),
+        "unit": "images/sec",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (reference xorshift stream: uniform inputs, one-hot labels, He-normal weights)",
+        "config": {"workload": "3-block CNN training step (conv3x3 3-64-128-256 + ReLU + maxpool2, "
+                               "GAP, Linear 256-1000, softmax CE, Adam 1e-3)",
+                   "global_batch": BATCH, "image": [3, SIZE, SIZE], "classes": CLASSES,
+                   "parallelism": "single GPU"},
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "gemm family (conv/linear fwd, dgrad, wgrad; fp32 v_mfma_f32_32x32x2)",
+            "achieved": round(gemm_tflops, 3),
+            "peak": FP32_MFMA_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(gemm_tflops / FP32_MFMA_PEAK_TFLOPS, 4),
+            "traffic": None,
+            "launches_per_step": launches.value / args.steps,
+            "gemm_ms_per_step": round(ms.value / args.steps, 4),
+            "flops_per_launch": per_launch_flops,
+            "flops_per_step": cnn_gemm_flops(),
+        },
+        "loss": float(loss.item()),
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(args.cpu_sample_batch)
+    print(json.dumps(result))
+
+
+def _device_handle(device):
+    """The axis_device behind a host-layer Device (its stream pointer identifies the handle)."""
+    import axis_amd
+    ax = axis_amd.host()
+    return ctypes.c_void_p(ax.device_handle(device))
+
+
+if __name__ == "__main__":
+    main()

@@ -68,6 +68,15 @@ int axis_copy(axis_device device, void *dst, const void *src, size_t bytes);
 /* Device::zeros_buffer (backend.rs:385-392) generalised to any fill value. */
 int axis_fill(axis_device device, float *out, float value, int64_t len);
 
+/* Launch timing, off by default.  While enabled, every launch of a kernel family is bracketed
+ * by HIP events on the handle's stream.  axis_timing_read synchronizes and returns, for the
+ * family ("gemm": matmul, left and right backward), the launches since the last reset, their
+ * summed duration and their summed algorithmic work (2*batch*m*k*n flops). */
+int axis_timing_enable(axis_device device, int enabled);
+int axis_timing_reset(axis_device device);
+int axis_timing_read(axis_device device, const char *family, int64_t *launches, double *milliseconds,
+                     double *work);
+
 /* ------------------------------------------------------------------ contractions */
 
 /* Device::matmul (backend.rs:934-957): out[b] = a[b] . b[b]; a [batch,m,k], b [batch,k,n],
