@@ -285,14 +285,36 @@ __global__ void __launch_bounds__(kBlock) column_chunk_kernel(const float *__res
     partial[q * width + c] = sum;
 }
 
+// Stage two: one block per column.  The block stages the column's chunk partials through LDS
+// (parallel, coalesced across chunks of the same column block) and one lane adds them in chunk
+// order, so the association is the reference's ((0 + p0) + p1) + ... exactly.
+constexpr int kCombineStage = 4096;
+
 __global__ void __launch_bounds__(kBlock) column_combine_kernel(const float *__restrict__ partial,
                                                                 int64_t chunks, int64_t width,
                                                                 float scale, float *__restrict__ out) {
-    const int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-    if (c >= width) return;
+    __shared__ __attribute__((aligned(16))) float staged[kCombineStage];
+    const int64_t c = blockIdx.x;
     float sum = 0.0f;
-    for (int64_t q = 0; q < chunks; ++q) sum = sum + partial[q * width + c];
-    out[c] = sum * scale;
+    for (int64_t base = 0; base < chunks; base += kCombineStage) {
+        const int n = (int)(chunks - base < kCombineStage ? chunks - base : kCombineStage);
+        for (int i = threadIdx.x; i < n; i += kBlock) staged[i] = partial[(base + i) * width + c];
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const floatx4 *v = reinterpret_cast<const floatx4 *>(staged);
+            int i = 0;
+            for (; i + 4 <= n; i += 4) {
+                const floatx4 q = v[i / 4];
+                sum = sum + q[0];
+                sum = sum + q[1];
+                sum = sum + q[2];
+                sum = sum + q[3];
+            }
+            for (; i < n; ++i) sum = sum + staged[i];
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[c] = sum * scale;
 }
 
 // out[o][i] = factor * sum_r a[o][r][i] in the reference's chunked order.
@@ -459,8 +481,8 @@ int axis_bias_gradient(axis_device device, const float *gradient, const float *r
         column_chunk_kernel<false><<<grid, kBlock, 0, device->stream>>>(
             gradient, nullptr, nullptr, partial.as<float>(), rows, width, column_blocks);
     if (int s = axis::launch_status("column_chunk_kernel")) return s;
-    column_combine_kernel<<<(unsigned)column_blocks, kBlock, 0, device->stream>>>(
-        partial.as<float>(), chunks, width, 1.0f, out);
+    column_combine_kernel<<<(unsigned)width, kBlock, 0, device->stream>>>(partial.as<float>(), chunks,
+                                                                        width, 1.0f, out);
     return axis::launch_status("column_combine_kernel");
 }
 

@@ -194,16 +194,21 @@ __global__ void __launch_bounds__(WM *WN * 64)
         }
 }
 
-// Sum of reduction slices in slice order: out[e] = ((0 + s0) + s1) + ...
-__global__ void split_sum_kernel(const float *__restrict__ partial, float *__restrict__ out,
-                                 int64_t len, int32_t splits, int64_t split_stride) {
-    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (; i < len; i += stride) {
-        float s = 0.f;
-        for (int32_t k = 0; k < splits; ++k) s += partial[k * split_stride + i];
-        out[i] = s;
-    }
+// Sum of reduction slices: lane group g (of 4) adds slices g, g+4, g+8, ... in order, then the
+// four group sums are added in group order -- a fixed association for a given slice count, so
+// the result is deterministic and independent of scheduling.
+__global__ void __launch_bounds__(256) split_sum_kernel(const float *__restrict__ partial,
+                                                        float *__restrict__ out, int64_t len,
+                                                        int32_t splits, int64_t split_stride) {
+    __shared__ float acc[4][64];
+    const int lane = threadIdx.x & 63, group = threadIdx.x >> 6;
+    const int64_t i = (int64_t)blockIdx.x * 64 + lane;
+    float s = 0.f;
+    if (i < len)
+        for (int32_t k = group; k < splits; k += 4) s += partial[k * split_stride + i];
+    acc[group][lane] = s;
+    __syncthreads();
+    if (group == 0 && i < len) out[i] = ((acc[0][lane] + acc[1][lane]) + acc[2][lane]) + acc[3][lane];
 }
 
 template <int BM, int BN, int WM, int WN, bool XR, bool YR, int VX, int VY>
@@ -242,7 +247,7 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out) {
     // Split the reduction when the tiles alone cannot fill the chip.
     int64_t splits = 1;
     if (tiles < 2 * cus && p.k >= 8 * BK * 8) {
-        splits = (4 * cus + tiles - 1) / tiles;
+        splits = std::min<int64_t>((4 * cus + tiles - 1) / tiles, 2 * cus);
         splits = std::min<int64_t>(splits, p.k / (BK * 8));
         splits = std::max<int64_t>(splits, 1);
     }
@@ -283,7 +288,7 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out) {
     int status = axis::launch_status("gemm_kernel");
     if (status) return status;
     if (splits > 1) {
-        split_sum_kernel<<<axis::blocks_for(out_len, 256, 16384), 256, 0, device->stream>>>(
+        split_sum_kernel<<<axis::blocks_for(out_len, 64, INT32_MAX), 256, 0, device->stream>>>(
             partial.as<float>(), out, out_len, static_cast<int32_t>(splits), out_len);
         status = axis::launch_status("split_sum_kernel");
     }

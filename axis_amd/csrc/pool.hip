@@ -2,85 +2,172 @@
 // -min(-unfold(x, fill=-inf)) (model/convolution.rs:1357-1370, Tensor::min tensor.rs:2880-2946,
 // grouped_minimum backend.rs:3019-3056) in one pass, emitting the window-local winner as a byte,
 // and its backward (Rule::Minimum gather + mask, then unfold's col2im, tensor.rs:5679-5683 and
-// backend.rs:1795-1889) as one gather pass per input element.
+// backend.rs:1795-1889).
 //
-// Lanes run along the channel axis, so every load and store is unit-stride across the wave.
+// Lanes run along the channel axis (4 channels per lane when the channel extent allows), so
+// every load and store is unit-stride across the wave; index decode is 32-bit multiply-high.
+// Non-overlapping windows (stride == kernel, no padding, exact tiling) take a scatter-form
+// backward -- one lane per output writes its window -- which equals the gather sum exactly: each
+// input receives exactly one term, written as 0.0f + g like the sum the reference starts at +0.0.
 #include <cfloat>
 
 #include "common.hpp"
+#include "fastdiv.hpp"
 
 namespace {
 
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 constexpr uint8_t kNoWinner = 255;
 
 struct PoolArgs {
-    int64_t outer, channels;
-    int32_t height, width, out_h, out_w;
+    int32_t channels, height, width, out_h, out_w;
     int32_t ky, kx, sy, sx, py, px;
+    uint32_t total;          // lanes in the launch (vectors of VEC channels)
+    FastDiv cvec, ow, oh;    // decode of an output-vector index
+    FastDiv iw, ih;          // decode of an input-vector index
+    FastDiv sy_div, sx_div;
 };
 
+template <int VEC>
+struct Vec {
+    float v[VEC];
+};
+
+template <int VEC>
+__device__ __forceinline__ void load_vec(const float *p, float (&v)[VEC]) {
+    if constexpr (VEC == 4) {
+        const floatx4 x = *reinterpret_cast<const floatx4 *>(p);
+        v[0] = x[0], v[1] = x[1], v[2] = x[2], v[3] = x[3];
+    } else {
+        v[0] = p[0];
+    }
+}
+
+template <int VEC>
+__device__ __forceinline__ void store_vec(float *p, const float (&v)[VEC]) {
+    if constexpr (VEC == 4) {
+        floatx4 x = {v[0], v[1], v[2], v[3]};
+        *reinterpret_cast<floatx4 *>(p) = x;
+    } else {
+        p[0] = v[0];
+    }
+}
+
+template <int VEC>
 __global__ void __launch_bounds__(256) max_pool2d_kernel(const float *__restrict__ in,
                                                          float *__restrict__ out,
                                                          uint8_t *__restrict__ argmax, PoolArgs a) {
-    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int64_t total = a.outer * a.out_h * a.out_w * a.channels;
-    if (idx >= total) return;
-    const int64_t c = idx % a.channels;
-    int64_t rest = idx / a.channels;
-    const int32_t ox = (int32_t)(rest % a.out_w);
-    rest /= a.out_w;
-    const int32_t oy = (int32_t)(rest % a.out_h);
-    const int64_t o = rest / a.out_h;
-    const float *base = in + o * a.height * a.width * a.channels + c;
-    float best = -INFINITY;
-    int winner = kNoWinner;
+    const uint32_t t = blockIdx.x * 256u + threadIdx.x;
+    if (t >= a.total) return;
+    const uint32_t cv = a.cvec.mod(t);
+    uint32_t rest = a.cvec.div(t);
+    const int32_t ox = (int32_t)a.ow.mod(rest);
+    rest = a.ow.div(rest);
+    const int32_t oy = (int32_t)a.oh.mod(rest);
+    const uint32_t o = a.oh.div(rest);
+    const int32_t c = (int32_t)cv * VEC;
+    const float *base = in + (int64_t)o * a.height * a.width * a.channels + c;
+    float best[VEC];
+    int winner[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) best[e] = -INFINITY, winner[e] = kNoWinner;
     for (int32_t ky = 0; ky < a.ky; ++ky) {
         const int32_t iy = oy * a.sy + ky - a.py;
         if (iy < 0 || iy >= a.height) continue;
         for (int32_t kx = 0; kx < a.kx; ++kx) {
             const int32_t ix = ox * a.sx + kx - a.px;
             if (ix < 0 || ix >= a.width) continue;
-            const float v = base[((int64_t)iy * a.width + ix) * a.channels];
-            // first strictly greater finite value in window order (ky major, kx minor)
-            if (v >= -FLT_MAX && v <= FLT_MAX && v > best) {
-                best = v;
-                winner = ky * a.kx + kx;
+            float v[VEC];
+            load_vec<VEC>(base + ((int64_t)iy * a.width + ix) * a.channels, v);
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) {
+                // first strictly greater finite value in window order (ky major, kx minor)
+                if (v[e] >= -FLT_MAX && v[e] <= FLT_MAX && v[e] > best[e]) {
+                    best[e] = v[e];
+                    winner[e] = ky * a.kx + kx;
+                }
             }
         }
     }
-    out[idx] = winner == kNoWinner ? __builtin_nanf("") : best;
-    argmax[idx] = (uint8_t)winner;
+    float r[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) r[e] = winner[e] == kNoWinner ? __builtin_nanf("") : best[e];
+    store_vec<VEC>(out + (int64_t)t * VEC, r);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) argmax[(int64_t)t * VEC + e] = (uint8_t)winner[e];
 }
 
+// Non-overlapping windows: one lane per output vector writes its whole window.
+template <int VEC>
+__global__ void __launch_bounds__(256) max_pool2d_backward_tiled_kernel(
+    const float *__restrict__ gradient, const uint8_t *__restrict__ argmax, float *__restrict__ out,
+    PoolArgs a) {
+    const uint32_t t = blockIdx.x * 256u + threadIdx.x;
+    if (t >= a.total) return;
+    const uint32_t cv = a.cvec.mod(t);
+    uint32_t rest = a.cvec.div(t);
+    const int32_t ox = (int32_t)a.ow.mod(rest);
+    rest = a.ow.div(rest);
+    const int32_t oy = (int32_t)a.oh.mod(rest);
+    const uint32_t o = a.oh.div(rest);
+    const int32_t c = (int32_t)cv * VEC;
+    float g[VEC];
+    int w[VEC];
+    load_vec<VEC>(gradient + (int64_t)t * VEC, g);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) w[e] = argmax[(int64_t)t * VEC + e];
+    float *base = out + (int64_t)o * a.height * a.width * a.channels + c;
+    for (int32_t ky = 0; ky < a.ky; ++ky) {
+        const int32_t iy = oy * a.ky + ky;
+        for (int32_t kx = 0; kx < a.kx; ++kx) {
+            const int32_t ix = ox * a.kx + kx;
+            const int k = ky * a.kx + kx;
+            float r[VEC];
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) r[e] = w[e] == k ? 0.0f + g[e] : 0.0f;
+            store_vec<VEC>(base + ((int64_t)iy * a.width + ix) * a.channels, r);
+        }
+    }
+}
+
+// General windows: one lane per input vector gathers the windows it won, ky major, kx minor.
+template <int VEC>
 __global__ void __launch_bounds__(256) max_pool2d_backward_kernel(const float *__restrict__ gradient,
                                                                   const uint8_t *__restrict__ argmax,
                                                                   float *__restrict__ out, PoolArgs a) {
-    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int64_t total = a.outer * a.height * a.width * a.channels;
-    if (idx >= total) return;
-    const int64_t c = idx % a.channels;
-    int64_t rest = idx / a.channels;
-    const int32_t ix = (int32_t)(rest % a.width);
-    rest /= a.width;
-    const int32_t iy = (int32_t)(rest % a.height);
-    const int64_t o = rest / a.height;
-    const int64_t obase = o * a.out_h * a.out_w * a.channels + c;
-    float sum = 0.0f;
+    const uint32_t t = blockIdx.x * 256u + threadIdx.x;
+    if (t >= a.total) return;
+    const uint32_t cv = a.cvec.mod(t);
+    uint32_t rest = a.cvec.div(t);
+    const int32_t ix = (int32_t)a.iw.mod(rest);
+    rest = a.iw.div(rest);
+    const int32_t iy = (int32_t)a.ih.mod(rest);
+    const uint32_t o = a.ih.div(rest);
+    const int32_t c = (int32_t)cv * VEC;
+    const int64_t obase = (int64_t)o * a.out_h * a.out_w * a.channels + c;
+    float sum[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) sum[e] = 0.0f;
     for (int32_t ky = 0; ky < a.ky; ++ky) {
         const int32_t padded_y = iy + a.py - ky;
-        if (padded_y < 0 || padded_y % a.sy != 0) continue;
-        const int32_t oy = padded_y / a.sy;
-        if (oy >= a.out_h) continue;
+        if (padded_y < 0) continue;
+        const int32_t oy = (int32_t)a.sy_div.div((uint32_t)padded_y);
+        if (oy * a.sy != padded_y || oy >= a.out_h) continue;
         for (int32_t kx = 0; kx < a.kx; ++kx) {
             const int32_t padded_x = ix + a.px - kx;
-            if (padded_x < 0 || padded_x % a.sx != 0) continue;
-            const int32_t ox = padded_x / a.sx;
-            if (ox >= a.out_w) continue;
-            const int64_t w = obase + ((int64_t)oy * a.out_w + ox) * a.channels;
-            if (argmax[w] == ky * a.kx + kx) sum += gradient[w];
+            if (padded_x < 0) continue;
+            const int32_t ox = (int32_t)a.sx_div.div((uint32_t)padded_x);
+            if (ox * a.sx != padded_x || ox >= a.out_w) continue;
+            const int64_t wpos = obase + ((int64_t)oy * a.out_w + ox) * a.channels;
+            const int k = ky * a.kx + kx;
+            float g[VEC];
+            load_vec<VEC>(gradient + wpos, g);
+#pragma unroll
+            for (int e = 0; e < VEC; ++e)
+                if (argmax[wpos + e] == k) sum[e] += g[e];
         }
     }
-    out[idx] = sum;
+    store_vec<VEC>(out + (int64_t)t * VEC, sum);
 }
 
 int pool_args(int64_t outer, int32_t height, int32_t width, int64_t channels, const int32_t *kernel,
@@ -96,8 +183,9 @@ int pool_args(int64_t outer, int32_t height, int32_t width, int64_t channels, co
                  "pool padding must be at most half the kernel extent");
     AXIS_REQUIRE(height + 2 * padding[0] >= kernel[0] && width + 2 * padding[1] >= kernel[1],
                  "pool kernel exceeds the padded spatial extent");
-    a->outer = outer;
-    a->channels = channels;
+    AXIS_REQUIRE(outer * height * width * channels <= INT32_MAX, "pool input exceeds the 32-bit index range");
+    AXIS_REQUIRE(channels <= INT32_MAX, "too many channels");
+    a->channels = (int32_t)channels;
     a->height = height;
     a->width = width;
     a->out_h = (height + 2 * padding[0] - kernel[0]) / stride[0] + 1;
@@ -108,6 +196,12 @@ int pool_args(int64_t outer, int32_t height, int32_t width, int64_t channels, co
     a->sx = stride[1];
     a->py = padding[0];
     a->px = padding[1];
+    a->ow = FastDiv((uint32_t)a->out_w);
+    a->oh = FastDiv((uint32_t)a->out_h);
+    a->iw = FastDiv((uint32_t)width);
+    a->ih = FastDiv((uint32_t)height);
+    a->sy_div = FastDiv((uint32_t)stride[0]);
+    a->sx_div = FastDiv((uint32_t)stride[1]);
     return AXIS_OK;
 }
 
@@ -122,9 +216,17 @@ int axis_max_pool2d(axis_device device, const float *input, float *out, uint8_t 
     AXIS_REQUIRE(input && out && argmax, "null max_pool2d buffer");
     PoolArgs a{};
     if (int s = pool_args(outer, height, width, channels, kernel, stride, padding, &a)) return s;
-    const int64_t total = outer * a.out_h * a.out_w * channels;
-    max_pool2d_kernel<<<axis::blocks_for(total, 256, INT32_MAX), 256, 0, device->stream>>>(
-        input, out, argmax, a);
+    const bool vec = channels % 4 == 0 && axis::aligned16(input) && axis::aligned16(out) &&
+                     (reinterpret_cast<uintptr_t>(argmax) & 3u) == 0;
+    const int v = vec ? 4 : 1;
+    a.cvec = FastDiv((uint32_t)(channels / v));
+    a.total = (uint32_t)(outer * a.out_h * a.out_w * (channels / v));
+    if (vec)
+        max_pool2d_kernel<4><<<axis::blocks_for(a.total, 256, INT32_MAX), 256, 0, device->stream>>>(
+            input, out, argmax, a);
+    else
+        max_pool2d_kernel<1><<<axis::blocks_for(a.total, 256, INT32_MAX), 256, 0, device->stream>>>(
+            input, out, argmax, a);
     return axis::launch_status("max_pool2d_kernel");
 }
 
@@ -136,9 +238,29 @@ int axis_max_pool2d_backward(axis_device device, const float *gradient, const ui
     AXIS_REQUIRE(gradient && argmax && out, "null max_pool2d_backward buffer");
     PoolArgs a{};
     if (int s = pool_args(outer, height, width, channels, kernel, stride, padding, &a)) return s;
-    const int64_t total = outer * (int64_t)height * width * channels;
-    max_pool2d_backward_kernel<<<axis::blocks_for(total, 256, INT32_MAX), 256, 0, device->stream>>>(
-        gradient, argmax, out, a);
+    const bool vec = channels % 4 == 0 && axis::aligned16(gradient) && axis::aligned16(out) &&
+                     (reinterpret_cast<uintptr_t>(argmax) & 3u) == 0;
+    const int v = vec ? 4 : 1;
+    a.cvec = FastDiv((uint32_t)(channels / v));
+    const bool tiled = stride[0] == kernel[0] && stride[1] == kernel[1] && padding[0] == 0 &&
+                       padding[1] == 0 && height % kernel[0] == 0 && width % kernel[1] == 0;
+    if (tiled) {
+        a.total = (uint32_t)(outer * a.out_h * a.out_w * (channels / v));
+        if (vec)
+            max_pool2d_backward_tiled_kernel<4><<<axis::blocks_for(a.total, 256, INT32_MAX), 256, 0,
+                                                  device->stream>>>(gradient, argmax, out, a);
+        else
+            max_pool2d_backward_tiled_kernel<1><<<axis::blocks_for(a.total, 256, INT32_MAX), 256, 0,
+                                                  device->stream>>>(gradient, argmax, out, a);
+        return axis::launch_status("max_pool2d_backward_tiled_kernel");
+    }
+    a.total = (uint32_t)(outer * height * width * (channels / v));
+    if (vec)
+        max_pool2d_backward_kernel<4><<<axis::blocks_for(a.total, 256, INT32_MAX), 256, 0,
+                                        device->stream>>>(gradient, argmax, out, a);
+    else
+        max_pool2d_backward_kernel<1><<<axis::blocks_for(a.total, 256, INT32_MAX), 256, 0,
+                                        device->stream>>>(gradient, argmax, out, a);
     return axis::launch_status("max_pool2d_backward_kernel");
 }
 

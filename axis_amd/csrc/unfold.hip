@@ -6,6 +6,8 @@
 // 32-bit (the tensor layer bounds both lengths below 2^31).  col2im keeps the reference's
 // summation order -- ky outer, kx inner, starting from +0.0 -- so its result is bit-identical to
 // a sequential restatement, and it needs no atomics.
+#include <algorithm>
+
 #include "common.hpp"
 #include "fastdiv.hpp"
 
@@ -92,6 +94,118 @@ __global__ void __launch_bounds__(256) unfold2d_backward_kernel(const float *__r
     out[i] = sum;
 }
 
+// Patches of a channel-innermost input laid out [rows = batch*oh*ow][patch = (c, ky, kx)] (the
+// convolution case with one group): a block stages the kh*kw*channels window values of `rows`
+// output pixels in LDS, read with lanes along the channel axis (unit stride), then writes each
+// pixel's patch row contiguously.  Same values as unfold2d_kernel, position for position.
+struct Im2colArgs {
+    int32_t rows, channels, window, patch;  // patch = channels * window
+    int32_t out_h, out_w, height, width;
+    int32_t kernel_x, stride_y, stride_x, padding_y, padding_x;
+    int32_t rows_per_block;
+    int64_t batch_stride, y_stride, x_stride;  // input strides (channel stride is 1)
+    FastDiv c_div, window_div, ow_div, oh_div, kx_div, patch_div;
+    float fill;
+};
+
+__global__ void __launch_bounds__(256) im2col_channels_last_kernel(const float *__restrict__ input,
+                                                                   float *__restrict__ out,
+                                                                   Im2colArgs a) {
+    extern __shared__ float tile[];  // [rows_per_block][window][channels + 1]
+    const int32_t pitch = a.channels + 1;
+    const int32_t row0 = blockIdx.x * a.rows_per_block;
+    const int32_t rows = min(a.rows_per_block, a.rows - row0);
+    const uint32_t staged = (uint32_t)(rows * a.window * a.channels);
+    for (uint32_t idx = threadIdx.x; idx < staged; idx += 256) {
+        const uint32_t c = a.c_div.mod(idx);
+        const uint32_t rest = a.c_div.div(idx);
+        const uint32_t pos = a.window_div.mod(rest);
+        const uint32_t r = a.window_div.div(rest);
+        const uint32_t pixel = (uint32_t)row0 + r;
+        const int32_t ox = (int32_t)a.ow_div.mod(pixel);
+        const uint32_t rest2 = a.ow_div.div(pixel);
+        const int32_t oy = (int32_t)a.oh_div.mod(rest2);
+        const int64_t b = a.oh_div.div(rest2);
+        const int32_t kx = (int32_t)a.kx_div.mod(pos);
+        const int32_t ky = (int32_t)a.kx_div.div(pos);
+        const int32_t iy = oy * a.stride_y + ky - a.padding_y;
+        const int32_t ix = ox * a.stride_x + kx - a.padding_x;
+        const bool valid = iy >= 0 && iy < a.height && ix >= 0 && ix < a.width;
+        tile[(r * a.window + pos) * pitch + c] =
+            valid ? input[b * a.batch_stride + iy * a.y_stride + ix * a.x_stride + c] : a.fill;
+    }
+    __syncthreads();
+    const uint32_t written = (uint32_t)(rows * a.patch);
+    float *dst = out + (int64_t)row0 * a.patch;
+    for (uint32_t idx = threadIdx.x; idx < written; idx += 256) {
+        const uint32_t k = a.patch_div.mod(idx);
+        const uint32_t r = a.patch_div.div(idx);
+        const uint32_t pos = a.window_div.mod(k);
+        const uint32_t c = a.window_div.div(k);
+        dst[idx] = tile[(r * a.window + pos) * pitch + c];
+    }
+}
+
+// Recognise the convolution layout of unfold_spec's output: one group, patch innermost, then
+// ox, oy and at most one other (batch) dimension, over a channel-innermost input.
+bool channels_last_im2col(const axis_unfold_spec *s, Im2colArgs *a) {
+    const int32_t kh = s->kernel[0], kw = s->kernel[1];
+    const int32_t oh = s->output_spatial[0], ow = s->output_spatial[1];
+    int32_t channels = -1;
+    for (int d = 0; d < s->input_rank; ++d)
+        if (s->backward_metadata[4 * d + 3] == 1) channels = s->backward_metadata[4 * d];
+    if (channels < 1 || s->channels_per_group != channels || s->input_special_strides[0] != 1)
+        return false;
+    const int64_t patch = (int64_t)channels * kh * kw;
+    int64_t batch = 1, batch_stride = 0;
+    int others = 0;
+    for (int d = 0; d < s->output_rank; ++d) {
+        const int32_t *md = s->forward_metadata + 4 * d;
+        switch (md[3]) {
+        case 0:
+            if (++others > 1 || md[1] != patch * ow * oh) return false;
+            batch = md[0];
+            batch_stride = md[2];
+            break;
+        case 1: if (md[1] != patch * ow) return false; break;
+        case 2: if (md[1] != patch) return false; break;
+        case 3: if (md[0] != 1) return false; break;
+        default: if (md[1] != 1 || md[0] != patch) return false; break;
+        }
+    }
+    const int64_t rows = batch * oh * ow;
+    if (rows * patch != s->output_len || rows > INT32_MAX) return false;
+    int rows_per_block = (int)std::max<int64_t>(1, 4096 / patch);
+    while (rows_per_block > 1 && (int64_t)rows_per_block * kh * kw * (channels + 1) * 4 > 48 * 1024)
+        --rows_per_block;
+    if ((int64_t)rows_per_block * kh * kw * (channels + 1) * 4 > 64 * 1024) return false;
+    a->rows = (int32_t)rows;
+    a->channels = channels;
+    a->window = kh * kw;
+    a->patch = (int32_t)patch;
+    a->out_h = oh;
+    a->out_w = ow;
+    a->height = s->input_spatial[0];
+    a->width = s->input_spatial[1];
+    a->kernel_x = kw;
+    a->stride_y = s->stride[0];
+    a->stride_x = s->stride[1];
+    a->padding_y = s->padding[0];
+    a->padding_x = s->padding[1];
+    a->rows_per_block = rows_per_block;
+    a->batch_stride = batch_stride;
+    a->y_stride = s->input_special_strides[1];
+    a->x_stride = s->input_special_strides[2];
+    a->c_div = FastDiv((uint32_t)channels);
+    a->window_div = FastDiv((uint32_t)(kh * kw));
+    a->ow_div = FastDiv((uint32_t)ow);
+    a->oh_div = FastDiv((uint32_t)oh);
+    a->kx_div = FastDiv((uint32_t)kw);
+    a->patch_div = FastDiv((uint32_t)patch);
+    a->fill = s->fill;
+    return true;
+}
+
 int validate(const axis_unfold_spec *s) {
     AXIS_REQUIRE(s, "null unfold spec");
     AXIS_REQUIRE(s->spatial_rank == 2, "unfold supports exactly two spatial axes on this backend");
@@ -145,6 +259,13 @@ int axis_unfold(axis_device device, const float *input, float *out, const axis_u
     AXIS_ENTER(device);
     if (int st = validate(spec)) return st;
     AXIS_REQUIRE(input && out, "null unfold buffer");
+    Im2colArgs fast{};
+    if (channels_last_im2col(spec, &fast)) {
+        const unsigned blocks = (unsigned)((fast.rows + fast.rows_per_block - 1) / fast.rows_per_block);
+        const size_t lds = (size_t)fast.rows_per_block * fast.window * (fast.channels + 1) * sizeof(float);
+        im2col_channels_last_kernel<<<blocks, 256, lds, device->stream>>>(input, out, fast);
+        return axis::launch_status("im2col_channels_last_kernel");
+    }
     UnfoldArgs a = common_args(spec);
     a.dims.rank = spec->output_rank;
     for (int d = 0; d < spec->output_rank; ++d) {
