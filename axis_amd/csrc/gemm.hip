@@ -211,21 +211,21 @@ __global__ void __launch_bounds__(256) split_sum_kernel(const float *__restrict_
     if (group == 0 && i < len) out[i] = ((acc[0][lane] + acc[1][lane]) + acc[2][lane]) + acc[3][lane];
 }
 
-template <int BM, int BN, int WM, int WN, bool XR, bool YR, int VX, int VY>
+template <int BM, int BN, int BK, int WM, int WN, bool XR, bool YR, int VX, int VY>
 void launch_config(const GemmParams &p, dim3 grid, hipStream_t stream) {
-    gemm_kernel<BM, BN, 16, WM, WN, XR, YR, VX, VY><<<grid, WM * WN * 64, 0, stream>>>(p);
+    gemm_kernel<BM, BN, BK, WM, WN, XR, YR, VX, VY><<<grid, WM * WN * 64, 0, stream>>>(p);
 }
 
-template <int BM, int BN, int WM, int WN, bool XR, bool YR>
+template <int BM, int BN, int BK, int WM, int WN, bool XR, bool YR>
 void launch_vec(const GemmParams &p, dim3 grid, hipStream_t stream, bool vx, bool vy) {
     if (vx && vy)
-        launch_config<BM, BN, WM, WN, XR, YR, 4, 4>(p, grid, stream);
+        launch_config<BM, BN, BK, WM, WN, XR, YR, 4, 4>(p, grid, stream);
     else if (vx)
-        launch_config<BM, BN, WM, WN, XR, YR, 4, 1>(p, grid, stream);
+        launch_config<BM, BN, BK, WM, WN, XR, YR, 4, 1>(p, grid, stream);
     else if (vy)
-        launch_config<BM, BN, WM, WN, XR, YR, 1, 4>(p, grid, stream);
+        launch_config<BM, BN, BK, WM, WN, XR, YR, 1, 4>(p, grid, stream);
     else
-        launch_config<BM, BN, WM, WN, XR, YR, 1, 1>(p, grid, stream);
+        launch_config<BM, BN, BK, WM, WN, XR, YR, 1, 1>(p, grid, stream);
 }
 
 // Vector loads need the contiguous extent, the other stride and the base to be 4-aligned.
@@ -235,11 +235,11 @@ bool vec_ok(const float *base, int64_t contiguous_extent, int64_t other_stride) 
 
 template <bool XR, bool YR>
 int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out) {
-    constexpr int BK = 16;
     const int64_t cus = device->multiprocessors;
-    // Large tiles when the output is big enough to keep every CU busy with them.
-    const bool big = p.m >= 128 && p.n >= 128 &&
-                     ((p.m + 127) / 128) * ((p.n + 127) / 128) * batch >= 2 * cus;
+    // Large tiles whenever both output extents fill them; a reduction split restores the block
+    // count when the output alone has too few tiles.  Large tiles run 32 deep per LDS stage.
+    const bool big = p.m >= 128 && p.n >= 128;
+    const int BK = big ? 32 : 16;
     const int bm = big ? 128 : 64, bn = big ? 128 : 64;
     p.tiles_m = static_cast<int32_t>((p.m + bm - 1) / bm);
     p.tiles_n = static_cast<int32_t>((p.n + bn - 1) / bn);
@@ -282,9 +282,9 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out) {
     axis::TimedLaunch timed(device, "gemm", 2.0 * (double)batch * (double)p.m * (double)p.n * (double)p.k);
     dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n), static_cast<unsigned>(batch * splits));
     if (big)
-        launch_vec<128, 128, 2, 2, XR, YR>(p, grid, device->stream, vx, vy);
+        launch_vec<128, 128, 32, 2, 2, XR, YR>(p, grid, device->stream, vx, vy);
     else
-        launch_vec<64, 64, 2, 2, XR, YR>(p, grid, device->stream, vx, vy);
+        launch_vec<64, 64, 16, 2, 2, XR, YR>(p, grid, device->stream, vx, vy);
     int status = axis::launch_status("gemm_kernel");
     if (status) return status;
     if (splits > 1) {

@@ -841,6 +841,7 @@ void Tensor::backward() const {
     double started = now_seconds();
     std::vector<Tensor> order;
     std::unordered_set<uint64_t> seen;
+    std::unordered_map<uint64_t, int> uses;  // edges that read each node
     std::vector<std::pair<Tensor, bool>> stack{{*this, false}};
     while (!stack.empty()) {
         auto [node_t, expanded] = stack.back();
@@ -855,10 +856,16 @@ void Tensor::backward() const {
             raise("parameter changed between forward and backward");
         stack.push_back({node_t, true});
         if (node_t.n->edges)
-            for (auto &e : *node_t.n->edges) stack.push_back({e.input, false});
+            for (auto &e : *node_t.n->edges) {
+                ++uses[e.input.id()];
+                stack.push_back({e.input, false});
+            }
     }
     const Device &dev = device();
     std::unordered_map<uint64_t, Buffer> adjoints;
+    // Bias gradients produced together with a ReLU backward (one pass over the activation), keyed
+    // by the bias-add node whose BiasBroadcast edge they answer.
+    std::unordered_map<uint64_t, Buffer> fused_bias;
     adjoints[id()] = dev.filled(1, 1.0f);
     std::vector<std::pair<Tensor, Buffer>> leaves;
     for (auto it = order.rbegin(); it != order.rend(); ++it) {
@@ -876,7 +883,28 @@ void Tensor::backward() const {
                 case Rule::Zero: c = dev.zeros_buffer(r.n); break;
                 case Rule::Scale: c = dev.scale(g, r.factor); break;
                 case Rule::Multiply: c = dev.binary(g, r.a, 2); break;
-                case Rule::Relu: c = dev.relu_backward(g, r.a); break;
+                case Rule::Relu: {
+                    // relu(bias_add(z, b)) whose add feeds nothing else: mask the gradient and sum
+                    // the bias gradient in one pass (same values, same summation order).
+                    const auto &x = e.input.n;
+                    const Rule *bias_rule = nullptr;
+                    if (uses[x->id] == 1 && x->edges && x->edges->size() == 2) {
+                        const Rule &r0 = (*x->edges)[0].rule, &r1 = (*x->edges)[1].rule;
+                        if (r0.kind == Rule::Identity && r1.kind == Rule::BiasBroadcast) bias_rule = &r1;
+                        if (r1.kind == Rule::Identity && r0.kind == Rule::BiasBroadcast) bias_rule = &r0;
+                    }
+                    if (bias_rule && bias_rule->outer * bias_rule->inner == g->floats()) {
+                        c = dev.alloc(g->floats());
+                        Buffer db = dev.alloc(bias_rule->inner);
+                        check(axis_bias_gradient(dev.h(), g->f32(), r.a->f32(), c->f32(), db->f32(),
+                                                 bias_rule->outer, bias_rule->inner),
+                              "bias_gradient");
+                        fused_bias[x->id] = db;
+                    } else {
+                        c = dev.relu_backward(g, r.a);
+                    }
+                    break;
+                }
                 case Rule::CategoricalCrossEntropy:
                     c = dev.alloc(r.m * r.n);
                     check(axis_categorical_cross_entropy_backward(dev.h(), g->f32(), r.a->f32(),
@@ -893,12 +921,19 @@ void Tensor::backward() const {
                 }
                 case Rule::Unfold: c = dev.unfold_backward(g, *r.spec); break;
                 case Rule::Select: c = dev.select_axis_backward(g, r.metadata, r.n); break;
-                case Rule::BiasBroadcast:
+                case Rule::BiasBroadcast: {
+                    auto fused = fused_bias.find(nd.id());
+                    if (fused != fused_bias.end()) {
+                        c = fused->second;
+                        fused_bias.erase(fused);
+                        break;
+                    }
                     c = dev.alloc(r.inner);
                     check(axis_bias_gradient(dev.h(), g->f32(), nullptr, nullptr, c->f32(), r.outer,
                                              r.inner),
                           "bias_gradient");
                     break;
+                }
                 case Rule::MeanMiddle:
                     c = dev.alloc(r.outer * r.reduce * r.inner);
                     check(axis_broadcast_middle(dev.h(), g->f32(), c->f32(), r.outer, r.reduce, r.inner,

