@@ -246,9 +246,9 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out) {
     const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n * batch;
     // Split the reduction when the tiles alone cannot fill the chip.
     int64_t splits = 1;
-    if (tiles < 2 * cus && p.k >= 8 * BK * 8) {
+    if (tiles < 2 * cus && p.k >= 8 * BK) {
         splits = std::min<int64_t>((4 * cus + tiles - 1) / tiles, 2 * cus);
-        splits = std::min<int64_t>(splits, p.k / (BK * 8));
+        splits = std::min<int64_t>(splits, p.k / (BK * 4));
         splits = std::max<int64_t>(splits, 1);
     }
     int64_t chunk = (p.k + splits - 1) / splits;

@@ -886,7 +886,12 @@ void Tensor::backward() const {
                 case Rule::Relu: {
                     // relu(bias_add(z, b)) whose add feeds nothing else: mask the gradient and sum
                     // the bias gradient in one pass (same values, same summation order).
-                    const auto &x = e.input.n;
+                    // Look through renames (single Identity edge, same buffer) to the add node.
+                    std::shared_ptr<Node> x = e.input.n;
+                    while (uses[x->id] == 1 && x->edges && x->edges->size() == 1 &&
+                           (*x->edges)[0].rule.kind == Rule::Identity &&
+                           (*x->edges)[0].input.n->value == x->value)
+                        x = (*x->edges)[0].input.n;
                     const Rule *bias_rule = nullptr;
                     if (uses[x->id] == 1 && x->edges && x->edges->size() == 2) {
                         const Rule &r0 = (*x->edges)[0].rule, &r1 = (*x->edges)[1].rule;

@@ -192,6 +192,9 @@ int axis_adam_multi(axis_device device, const axis_adam_tensor *tensors, int32_t
         if (n == 0) continue;
         AXIS_REQUIRE(blocks < INT32_MAX, "adam_multi launch too large");
         args.count = n;
+        double bytes = 0.0;  // algorithmic: read p, g, m, v (+ rate), write p, m, v
+        for (int32_t t = 0; t < n; ++t) bytes += (args.t[t].rates ? 32.0 : 28.0) * (double)args.t[t].len;
+        axis::TimedLaunch timed(device, "adam", bytes);
         adam_multi_kernel<<<(unsigned)blocks, kBlock, 0, device->stream>>>(args);
         if (int s = axis::launch_status("adam_multi_kernel")) return s;
     }

@@ -117,6 +117,168 @@ def cpu_baseline(sample_batch: int):
                       f"(64x64x3, fp64-accumulated GEMMs, OpenMP), {elapsed:.2f} s"}
 
 
+def _timing(lib, handle, family):
+    from axis_amd import hip
+    launches, ms, work = ctypes.c_int64(), ctypes.c_double(), ctypes.c_double()
+    hip.check(lib.axis_timing_read(handle, family.encode(), ctypes.byref(launches), ctypes.byref(ms),
+                                   ctypes.byref(work)), "axis_timing_read")
+    return launches.value, ms.value, work.value
+
+
+def bench_matmul(args):
+    """dX = dY W^T and dW = X^T dY for X, W, dY [4096, 4096] and for the
+    skinny case X [8192, 784], W [784, 1024], all N(0, 1) from seeds 21, 22, 23."""
+    import axis_amd
+    from axis_amd import hip
+    ax = axis_amd.host()
+    dev = hip.Device(0)
+    lib = hip.load()
+    results = {}
+    for name, (m, k, n) in {"square_4096": (4096, 4096, 4096), "skinny_8192x784x1024": (8192, 784, 1024)}.items():
+        x = dev.upload(ax.normal_host_values(21, m * k, 0.0, 1.0))
+        w = dev.upload(ax.normal_host_values(22, k * n, 0.0, 1.0))
+        dy = dev.upload(ax.normal_host_values(23, m * n, 0.0, 1.0))
+        dx, dw = dev.empty(m * k), dev.empty(k * n)
+        I = ctypes.c_int64
+        for _ in range(args.warmup):
+            dev.call("axis_matmul_left_backward", dy.vp, w.vp, dx.vp, I(1), I(m), I(k), I(n))
+            dev.call("axis_matmul_right_backward", x.vp, dy.vp, dw.vp, I(1), I(m), I(k), I(n))
+        dev.synchronize()
+        row = {}
+        for op, call in (("dgrad", lambda: dev.call("axis_matmul_left_backward", dy.vp, w.vp, dx.vp, I(1), I(m), I(k), I(n))),
+                         ("wgrad", lambda: dev.call("axis_matmul_right_backward", x.vp, dy.vp, dw.vp, I(1), I(m), I(k), I(n)))):
+            lib.axis_timing_reset(dev.handle)
+            lib.axis_timing_enable(dev.handle, 1)
+            for _ in range(args.steps):
+                call()
+            lib.axis_timing_enable(dev.handle, 0)
+            launches, ms, work = _timing(lib, dev.handle, "gemm")
+            tflops = work / (ms * 1e-3) / 1e12
+            row[op] = {"ms": round(ms / launches, 4), "tflops": round(tflops, 2),
+                       "frac": round(tflops / FP32_MFMA_PEAK_TFLOPS, 4)}
+        results[name] = row
+    total = [v for r in results.values() for v in r.values()]
+    avg = sum(v["tflops"] for v in total) / len(total)
+    print(json.dumps({"metric": "fp32 matmul backward TFLOP/s (dgrad + wgrad)", "value": round(avg, 2),
+                      "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+                      "higher_is_better": True, "dtype": "fp32", "data": "synthetic N(0,1), seeds 21-23",
+                      "config": {"workload": "BASELINE config 2: isolated matmul backward"},
+                      "roofline": {"bound": "mfma", "achieved": round(avg, 2), "peak": FP32_MFMA_PEAK_TFLOPS,
+                                   "unit": "TFLOP/s", "frac": round(avg / FP32_MFMA_PEAK_TFLOPS, 4)},
+                      "results": results}))
+
+
+def bench_adam(args):
+    """fused Adam over 16 tensors of 4,194,304 fp32 parameters; p ~ N(0, 0.02)
+    (seeds 100+i), g ~ N(0, 1e-3) (seeds 200+i), m = v = 0, three warm-up steps, then timed steps."""
+    import axis_amd
+    from axis_amd import hip
+    ax = axis_amd.host()
+    dev = hip.Device(0)
+    lib = hip.load()
+    n, count = 4_194_304, 16
+    bufs = []
+    for i in range(count):
+        p = dev.upload(ax.normal_host_values(100 + i, n, 0.0, 0.02))
+        g = dev.upload(ax.normal_host_values(200 + i, n, 0.0, 1e-3))
+        m, v = dev.empty(n), dev.empty(n)
+        dev.call("axis_fill", m.vp, ctypes.c_float(0.0), ctypes.c_int64(n))
+        dev.call("axis_fill", v.vp, ctypes.c_float(0.0), ctypes.c_int64(n))
+        bufs.append((p, g, m, v))
+    arr = (hip.AdamTensor * count)(*[hip.AdamTensor(p.ptr, g.ptr, m.ptr, v.ptr, None, n) for p, g, m, v in bufs])
+    ax_powi = ax.powi
+
+    def step(t):
+        c1, c2 = 1.0 - ax_powi(0.9, t), 1.0 - ax_powi(0.999, t)
+        dev.call("axis_adam_multi", arr, ctypes.c_int32(count), ctypes.c_float(1e-3), ctypes.c_float(0.9),
+                 ctypes.c_float(0.999), ctypes.c_float(c1), ctypes.c_float(c2), ctypes.c_float(1e-8),
+                 ctypes.c_float(0.0))
+
+    t = 0
+    for _ in range(3 + args.warmup):
+        t += 1
+        step(t)
+    dev.synchronize()
+    lib.axis_timing_reset(dev.handle)
+    lib.axis_timing_enable(dev.handle, 1)
+    start = time.perf_counter()
+    for _ in range(args.steps):
+        t += 1
+        step(t)
+    dev.synchronize()
+    elapsed = time.perf_counter() - start
+    lib.axis_timing_enable(dev.handle, 0)
+    launches, ms, work = _timing(lib, dev.handle, "adam")
+    gbs = work / (ms * 1e-3) / 1e9
+    print(json.dumps({"metric": "fused Adam GB/s (16 x 4M fp32 params, 28 B/param)", "value": round(gbs, 1),
+                      "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+                      "ms_per_step": round(ms / args.steps, 4), "wall_ms_per_step": round(elapsed * 1e3 / args.steps, 4),
+                      "higher_is_better": True, "dtype": "fp32", "data": "synthetic, seeds 100-115 / 200-215",
+                      "config": {"workload": "BASELINE config 3: Adam over 64Mi params in 16 tensors"},
+                      "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                   "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}}))
+
+
+def bench_muon(args):
+    """wide MLP 4096-8192-8192-4096-1000, batch 4096, inputs N(0,1), labels
+    over 1000 classes, He-normal weights; forward, backward, Muon (momentum 0.95, Nesterov, five
+    Newton-Schulz steps) on the four weight matrices and AdamW (wd 0) on the biases."""
+    import axis_amd
+    from axis_amd import hip
+    ax = axis_amd.host()
+    device = ax.Device.hip(0)
+    lib = hip.load()
+    sizes, batch = (4096, 8192, 8192, 4096, 1000), 4096
+    bt = ax.Axis("batch")
+    feats = [ax.Axis(f"f{i}") for i in range(len(sizes))]
+    layers = []
+    for j in range(len(sizes) - 1):
+        layers.append(ax.Linear(feats[j], feats[j + 1].of(sizes[j + 1])))
+        if j < len(sizes) - 2:
+            layers.append(ax.ReLU())
+    model = ax.Sequential(layers)
+    model.build(ax.Shape([bt.of(batch), feats[0].of(sizes[0])]), device, 7)
+    for j in range(len(sizes) - 1):
+        std = float(np.sqrt(np.float32(2.0) / np.float32(sizes[j]), dtype=np.float32))
+        model.parameter(f"{2 * j}.weight").set_values(ax.normal_host_values(10 + j, sizes[j] * sizes[j + 1], 0.0, std))
+    x = ax.Tensor.from_slice(ax.normal_host_values(1, batch * sizes[0], 0.0, 1.0), [bt.of(batch), feats[0].of(sizes[0])], device)
+    u = ax.xorshift_unit_stream(2, batch)
+    labels = np.minimum(np.floor(u.astype(np.float64) * 1000).astype(np.int64), 999)
+    yh = np.zeros((batch, 1000), np.float32)
+    yh[np.arange(batch), labels] = 1.0
+    y = ax.Tensor.from_slice(yh.reshape(-1), [bt.of(batch), feats[-1].of(1000)], device)
+    selected = [ax.MuonMatrix.axis_linear(model.parameter(f"{2 * j}.weight")) for j in range(len(sizes) - 1)]
+    trainer = ax.Trainer(ax.MuonWithAuxAdamW(selected, 0.02, 1e-3, 0.0))
+
+    def loss_fn(m):
+        return m.forward(x).categorical_cross_entropy_with_logits(y, feats[-1]).mean([bt])
+
+    for _ in range(args.warmup):
+        trainer.step(model, loss_fn)
+    device.synchronize()
+    handle = ctypes.c_void_p(ax.device_handle(device))
+    lib.axis_timing_reset(handle)
+    lib.axis_timing_enable(handle, 1)
+    start = time.perf_counter()
+    for _ in range(args.steps):
+        _, loss = trainer.step(model, loss_fn)
+    device.synchronize()
+    elapsed = time.perf_counter() - start
+    lib.axis_timing_enable(handle, 0)
+    launches, ms, work = _timing(lib, handle, "gemm")
+    tflops = work / (ms * 1e-3) / 1e12
+    print(json.dumps({"metric": "wide-MLP Muon training step (ms/step); GEMM % of fp32 MFMA peak",
+                      "value": round(elapsed * 1e3 / args.steps, 3), "unit": "ms/step", "n_gpus": 1,
+                      "steps": args.steps, "warmup": args.warmup, "higher_is_better": False, "dtype": "fp32",
+                      "data": "synthetic N(0,1) inputs, seeds 1/2/10-13",
+                      "config": {"workload": "BASELINE config 5: MLP 4096-8192-8192-4096-1000, bs4096, MuonWithAuxAdamW"},
+                      "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": FP32_MFMA_PEAK_TFLOPS,
+                                   "unit": "TFLOP/s", "frac": round(tflops / FP32_MFMA_PEAK_TFLOPS, 4),
+                                   "gemm_ms_per_step": round(ms / args.steps, 3),
+                                   "gemm_tflop_per_step": round(work / args.steps / 1e12, 3)},
+                      "loss": float(loss.item())}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -124,11 +286,16 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-batch", type=int, default=256)
+    ap.add_argument("--workload", choices=["cnn", "matmul", "adam", "muon"], default="cnn",
+                    help="cnn: the headline metric (BASELINE config 4); the others are configs 2, 3, 5")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path "
               f"(--gpus {args.gpus} requested)", file=sys.stderr)
         sys.exit(2)
+    if args.workload != "cnn":
+        {"matmul": bench_matmul, "adam": bench_adam, "muon": bench_muon}[args.workload](args)
+        return
 
     import axis_amd
     from axis_amd import hip

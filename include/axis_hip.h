@@ -70,8 +70,9 @@ int axis_fill(axis_device device, float *out, float value, int64_t len);
 
 /* Launch timing, off by default.  While enabled, every launch of a kernel family is bracketed
  * by HIP events on the handle's stream.  axis_timing_read synchronizes and returns, for the
- * family ("gemm": matmul, left and right backward), the launches since the last reset, their
- * summed duration and their summed algorithmic work (2*batch*m*k*n flops). */
+ * family, the launches since the last reset, their summed duration and their summed algorithmic
+ * work: "gemm" (matmul, left and right backward; 2*batch*m*k*n flops each) and "adam"
+ * (axis_adam_multi; 28 bytes per parameter, 32 with per-element rates). */
 int axis_timing_enable(axis_device device, int enabled);
 int axis_timing_reset(axis_device device);
 int axis_timing_read(axis_device device, const char *family, int64_t *launches, double *milliseconds,

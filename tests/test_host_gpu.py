@@ -336,12 +336,12 @@ def test_cnn_small_batch_step_matches_oracle(ax, device, oracle):
         zero = np.zeros_like(p0)
         exact = oracle.adam(p0, g, zero, zero, 1e-3, 0.9, 0.999, c1, c2, 1e-8, 0.0)[0]
         assert np.array_equal(v, exact), theirs
-        # Against the whole oracle step: Adam's first update is lr * g / (|g| + eps), so an element
-        # whose gradient is near zero amplifies any rounding difference in g; compare every
-        # element whose gradient is at least 1e-3 of the tensor's largest.
+        # Against the whole oracle step: Adam's first update is lr * g / (|g| + eps), which turns a
+        # rounding difference in a gradient of comparable size into an O(lr) step difference;
+        # compare every element whose gradient agrees with the oracle's to 1% or better.
         gr = np.asarray(ref["grads"][theirs], np.float64)
-        sure = np.abs(gr) >= 1e-3 * np.abs(gr).max()
-        assert sure.mean() > 0.5, (theirs, sure.mean())
+        sure = np.abs(gr) >= 100.0 * np.abs(np.asarray(g, np.float64) - gr) + 1e-12
+        assert sure.mean() > 0.9, (theirs, sure.mean())
         assert rel_max(v[sure], ref["params"][theirs][sure]) < 1e-5, theirs
 
 
