@@ -59,28 +59,40 @@ __global__ void __launch_bounds__(kBlock) adam_multi_kernel(AdamMultiArgs args) 
     const int64_t end = begin + per_block < t.len ? begin + per_block : t.len;
     const AdamHyper h = args.h;
     if (t.vec && !t.rates) {
-        // whole float4 vectors, lanes striding by the block so each access coalesces
+        // Whole float4 vectors, lanes striding by the block so each access coalesces.  Every load
+        // of the thread's kVecPerThread vectors is issued before any arithmetic (16 loads in
+        // flight per lane), and the streams bypass cache residency (each byte is touched once).
         const int64_t vbegin = begin / 4, vend = end / 4;
-        floatx4 *pv = reinterpret_cast<floatx4 *>(t.value);
-        const floatx4 *gv = reinterpret_cast<const floatx4 *>(t.gradient);
-        floatx4 *mv = reinterpret_cast<floatx4 *>(t.first);
-        floatx4 *vv = reinterpret_cast<floatx4 *>(t.second);
+        floatx4 *__restrict__ pv = reinterpret_cast<floatx4 *>(t.value);
+        const floatx4 *__restrict__ gv = reinterpret_cast<const floatx4 *>(t.gradient);
+        floatx4 *__restrict__ mv = reinterpret_cast<floatx4 *>(t.first);
+        floatx4 *__restrict__ vv = reinterpret_cast<floatx4 *>(t.second);
+        floatx4 P[kVecPerThread], G[kVecPerThread], M[kVecPerThread], V[kVecPerThread];
 #pragma unroll
         for (int u = 0; u < kVecPerThread; ++u) {
             const int64_t i = vbegin + threadIdx.x + (int64_t)u * kBlock;
             if (i < vend) {
-                floatx4 p = pv[i], g = gv[i], m = mv[i], v = vv[i];
+                P[u] = __builtin_nontemporal_load(pv + i);
+                G[u] = __builtin_nontemporal_load(gv + i);
+                M[u] = __builtin_nontemporal_load(mv + i);
+                V[u] = __builtin_nontemporal_load(vv + i);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kVecPerThread; ++u) {
+            const int64_t i = vbegin + threadIdx.x + (int64_t)u * kBlock;
+            if (i < vend) {
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
-                    float pc = p[c], mc = m[c], vc = v[c];
-                    adam_one(pc, g[c], mc, vc, h.lr, h);
-                    p[c] = pc;
-                    m[c] = mc;
-                    v[c] = vc;
+                    float pc = P[u][c], mc = M[u][c], vc = V[u][c];
+                    adam_one(pc, G[u][c], mc, vc, h.lr, h);
+                    P[u][c] = pc;
+                    M[u][c] = mc;
+                    V[u][c] = vc;
                 }
-                pv[i] = p;
-                mv[i] = m;
-                vv[i] = v;
+                __builtin_nontemporal_store(P[u], pv + i);
+                __builtin_nontemporal_store(M[u], mv + i);
+                __builtin_nontemporal_store(V[u], vv + i);
             }
         }
         for (int64_t i = vend * 4 + threadIdx.x; i < end; i += kBlock) {
