@@ -1,32 +1,52 @@
 // fp32 GEMM family on CDNA4 matrix cores (v_mfma_f32_32x32x2_f32) for the reference's
 // matmul / matmul_left_backward / matmul_right_backward (runtime/backend.rs:934-1021,
-// kernels :2190-2290).
+// kernels :2190-2290), and implicit-GEMM convolution entries that compute the reference's
+// unfold -> contract (forward), contract-backward -> unfold_backward (dgrad) and
+// unfold -> contract-backward (wgrad) without materialising the patch matrix.
 //
-// One kernel template computes C[i][j] = sum_r X(i,r) Y(r,j) for a batch of row-major C,
-// with each operand either contiguous along the reduction (r) or along its output dimension:
+// One kernel template computes C[i][j] = sum_r X(i,r) Y(r,j) for a batch of row-major C.
+// Dense operands are contiguous along the reduction (r) or along their output dimension:
 //   matmul      : X = a [m,k] (r-contiguous),        Y = b [k,n] (j-contiguous)
 //   left_bwd    : X = gradient [m,n] (r-contiguous), Y = rhs [k,n] read as rhs^T (r-contiguous)
 //   right_bwd   : X = lhs [m,k] read as lhs^T (i-contiguous), Y = gradient [m,n] (j-contiguous)
+// Convolution X operands gather from a channel-innermost tensor [batch, h, w, c]:
+//   rows mode   : X(i = output pixel, r = (ky*kw + kx)*c + channel)   (forward, dgrad)
+//   cols mode   : X(i = (ky*kw + kx)*c + channel, r = output pixel)   (wgrad)
+// with zero outside the padded input.  Reordering the reduction as (ky, kx, channel) makes every
+// gathered vector contiguous in memory; the weights are permuted to match (a few KB).
+//
 // Tiles are staged through LDS as [r][i] / [r][j] so every MFMA operand read is a unit-stride
 // LDS access across the wave.  The next K tile is prefetched into registers while the current
 // one feeds the MFMAs.  When the output has too few tiles to fill 256 CUs, the reduction is
-// split into slices whose partial tiles are summed afterwards in slice order (deterministic,
+// split into slices whose partial tiles are summed afterwards in a fixed order (deterministic,
 // no atomics).
 #include <algorithm>
+#include <type_traits>
 
 #include "common.hpp"
+#include "fastdiv.hpp"
 
 namespace {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
+// Geometry of a gathered convolution operand (tensor [batch, height, width, channels]).
+struct ConvGeom {
+    const float *src;
+    int32_t height, width, channels;  // gathered tensor
+    int32_t out_h, out_w;             // output pixel grid the reduction/rows enumerate
+    int32_t kw, sy, sx, py, px;
+    FastDiv c_div, kw_div, ow_div, oh_div;
+};
+
 struct GemmParams {
     const float *x;
     const float *y;
     float *c;
+    const float *bias;         // added to every row of C (length n), or null
     int64_t m, n, k;           // C is [m, n]; reduction length k
-    int64_t x_si, x_sr;        // X(i, r) = x[i * x_si + r * x_sr]
+    int64_t x_si, x_sr;        // dense X(i, r) = x[i * x_si + r * x_sr]
     int64_t y_sr, y_sj;        // Y(r, j) = y[r * y_sr + j * y_sj]
     int64_t x_batch, y_batch;  // batch strides (elements)
     int64_t c_batch;           // batch stride of the output (or of one slice of partials)
@@ -34,64 +54,45 @@ struct GemmParams {
     int64_t k_chunk;           // reduction length per slice (multiple of the tile depth)
     int32_t splits;
     int32_t tiles_m, tiles_n;
+    ConvGeom conv;
 };
 
-// Stage one BK x BT tile of an operand into registers.  OUTER is the operand's output-dimension
-// extent (m for X, n for Y).  RCONTIG: the operand is contiguous along r.
+template <int VEC>
+__device__ __forceinline__ void load_into(float *reg, const float *src, bool valid) {
+    if constexpr (VEC == 4) {
+        floatx4 v = {0.f, 0.f, 0.f, 0.f};
+        if (valid) v = *reinterpret_cast<const floatx4 *>(src);
+        reg[0] = v[0];
+        reg[1] = v[1];
+        reg[2] = v[2];
+        reg[3] = v[3];
+    } else {
+        reg[0] = valid ? src[0] : 0.f;
+    }
+}
+
+// LDS staging shared by every loader: [r][t] layout with a pitch that keeps both the fill and
+// the MFMA operand reads free of bank conflicts.
 template <int BT, int BK, int NT, bool RCONTIG, int VEC>
-struct TileLoader {
+struct Staging {
     static constexpr int kElems = BT * BK / NT;  // floats per thread
     static constexpr int kVecs = kElems / VEC;
-    static constexpr int LD = RCONTIG ? BT + 2 : BT + 4;  // LDS row pitch ([r][t] layout)
-
+    static constexpr int LD = RCONTIG ? BT + 2 : BT + 4;
+    static constexpr int kPer = RCONTIG ? BK / VEC : BT / VEC;  // vectors per contiguous line
     float reg[kElems];
-
-    // s_t: stride along the output dimension; s_r: stride along r.
-    __device__ __forceinline__ void load(const float *__restrict__ base, int64_t s_t, int64_t s_r,
-                                         int64_t t0, int64_t r0, int64_t t_end, int64_t r_end,
-                                         int tid) {
-#pragma unroll
-        for (int e = 0; e < kVecs; ++e) {
-            int idx = tid + e * NT;
-            int tt, rr;
-            if (RCONTIG) {
-                constexpr int per = BK / VEC;
-                rr = (idx % per) * VEC;
-                tt = idx / per;
-            } else {
-                constexpr int per = BT / VEC;
-                tt = (idx % per) * VEC;
-                rr = idx / per;
-            }
-            int64_t gt = t0 + tt, gr = r0 + rr;
-            bool valid = gt < t_end && gr < r_end;
-            if (VEC == 4) {
-                floatx4 v = {0.f, 0.f, 0.f, 0.f};
-                if (valid) v = *reinterpret_cast<const floatx4 *>(base + gt * s_t + gr * s_r);
-                reg[e * 4 + 0] = v[0];
-                reg[e * 4 + 1] = v[1];
-                reg[e * 4 + 2] = v[2];
-                reg[e * 4 + 3] = v[3];
-            } else {
-                reg[e] = valid ? base[gt * s_t + gr * s_r] : 0.f;
-            }
-        }
-    }
 
     __device__ __forceinline__ void store(float *__restrict__ lds, int tid) const {
 #pragma unroll
         for (int e = 0; e < kVecs; ++e) {
-            int idx = tid + e * NT;
+            const int idx = tid + e * NT;
             if (RCONTIG) {
-                constexpr int per = BK / VEC;
-                int rr = (idx % per) * VEC;
-                int tt = idx / per;
+                const int rr = (idx % kPer) * VEC;
+                const int tt = idx / kPer;
 #pragma unroll
                 for (int c = 0; c < VEC; ++c) lds[(rr + c) * LD + tt] = reg[e * VEC + c];
             } else {
-                constexpr int per = BT / VEC;
-                int tt = (idx % per) * VEC;
-                int rr = idx / per;
+                const int tt = (idx % kPer) * VEC;
+                const int rr = idx / kPer;
                 if (VEC == 4) {
                     floatx4 v = {reg[e * 4 + 0], reg[e * 4 + 1], reg[e * 4 + 2], reg[e * 4 + 3]};
                     *reinterpret_cast<floatx4 *>(lds + rr * LD + tt) = v;
@@ -103,14 +104,134 @@ struct TileLoader {
     }
 };
 
-template <int BM, int BN, int BK, int WM, int WN, bool XR, bool YR, int VX, int VY>
+// Dense operand: element (t, r) at base[t * s_t + r * s_r].
+template <int BT, int BK, int NT, bool RCONTIG, int VEC>
+struct DenseLoader : Staging<BT, BK, NT, RCONTIG, VEC> {
+    using S = Staging<BT, BK, NT, RCONTIG, VEC>;
+    const float *base;
+    int64_t s_t, s_r, t0, t_end;
+
+    __device__ __forceinline__ void init(const float *b, int64_t st, int64_t sr, int64_t t_begin,
+                                         int64_t t_limit) {
+        base = b, s_t = st, s_r = sr, t0 = t_begin, t_end = t_limit;
+    }
+    __device__ __forceinline__ void load(const ConvGeom &, int64_t r0, int64_t r_end, int tid) {
+#pragma unroll
+        for (int e = 0; e < S::kVecs; ++e) {
+            const int idx = tid + e * NT;
+            int tt, rr;
+            if (RCONTIG) {
+                rr = (idx % S::kPer) * VEC;
+                tt = idx / S::kPer;
+            } else {
+                tt = (idx % S::kPer) * VEC;
+                rr = idx / S::kPer;
+            }
+            const int64_t gt = t0 + tt, gr = r0 + rr;
+            load_into<VEC>(this->reg + e * VEC, base + gt * s_t + gr * s_r, gt < t_end && gr < r_end);
+        }
+    }
+};
+
+// Convolution operand, rows mode: t = output pixel, r = (ky*kw + kx)*channels + channel.
+template <int BT, int BK, int NT, int VEC>
+struct ConvRowsLoader : Staging<BT, BK, NT, true, VEC> {
+    using S = Staging<BT, BK, NT, true, VEC>;
+    int64_t pixel_base[S::kVecs];  // offset of (b, 0, 0, 0); -1 past the last row
+    int32_t iy0[S::kVecs], ix0[S::kVecs];
+    int rr;
+
+    __device__ __forceinline__ void init(const ConvGeom &geom, int64_t t0, int64_t t_end, int tid) {
+        rr = (tid % S::kPer) * VEC;  // NT is a multiple of kPer, so rr is the same for every e
+#pragma unroll
+        for (int e = 0; e < S::kVecs; ++e) {
+            const int64_t gt = t0 + (tid + e * NT) / S::kPer;
+            if (gt < t_end) {
+                const uint32_t pix = (uint32_t)gt;
+                const uint32_t q = geom.ow_div.div(pix);
+                const int32_t ox = (int32_t)(pix - q * (uint32_t)geom.out_w);
+                const uint32_t b = geom.oh_div.div(q);
+                const int32_t oy = (int32_t)(q - b * (uint32_t)geom.out_h);
+                pixel_base[e] = (int64_t)b * geom.height * geom.width * geom.channels;
+                iy0[e] = oy * geom.sy - geom.py;
+                ix0[e] = ox * geom.sx - geom.px;
+            } else {
+                pixel_base[e] = -1;
+                iy0[e] = ix0[e] = 0;
+            }
+        }
+    }
+    __device__ __forceinline__ void load(const ConvGeom &geom, int64_t r0, int64_t r_end, int) {
+        const int64_t gr = r0 + rr;
+        const bool r_ok = gr < r_end;
+        int32_t c = 0, ky = 0, kx = 0;
+        if (r_ok) {
+            const uint32_t pos = geom.c_div.div((uint32_t)gr);
+            c = (int32_t)((uint32_t)gr - pos * (uint32_t)geom.channels);
+            ky = (int32_t)geom.kw_div.div(pos);
+            kx = (int32_t)pos - ky * geom.kw;
+        }
+#pragma unroll
+        for (int e = 0; e < S::kVecs; ++e) {
+            const int32_t iy = iy0[e] + ky, ix = ix0[e] + kx;
+            const bool valid = r_ok && pixel_base[e] >= 0 && iy >= 0 && iy < geom.height && ix >= 0 &&
+                               ix < geom.width;
+            const int64_t off = valid ? pixel_base[e] + ((int64_t)iy * geom.width + ix) * geom.channels + c : 0;
+            load_into<VEC>(this->reg + e * VEC, geom.src + off, valid);
+        }
+    }
+};
+
+// Convolution operand, cols mode: t = (ky*kw + kx)*channels + channel, r = output pixel.
+template <int BT, int BK, int NT, int VEC>
+struct ConvColsLoader : Staging<BT, BK, NT, false, VEC> {
+    using S = Staging<BT, BK, NT, false, VEC>;
+    int32_t c, ky, kx;
+    bool t_ok;
+    int row0;
+
+    __device__ __forceinline__ void init(const ConvGeom &geom, int64_t t0, int64_t t_end, int tid) {
+        const int64_t gt = t0 + (tid % S::kPer) * VEC;
+        t_ok = gt < t_end;
+        const uint32_t pos = geom.c_div.div((uint32_t)(t_ok ? gt : 0));
+        c = (int32_t)((uint32_t)(t_ok ? gt : 0) - pos * (uint32_t)geom.channels);
+        ky = (int32_t)geom.kw_div.div(pos);
+        kx = (int32_t)pos - ky * geom.kw;
+        row0 = tid / S::kPer;
+    }
+    __device__ __forceinline__ void load(const ConvGeom &geom, int64_t r0, int64_t r_end, int) {
+#pragma unroll
+        for (int e = 0; e < S::kVecs; ++e) {
+            const int64_t gr = r0 + row0 + e * (NT / S::kPer);
+            bool valid = t_ok && gr < r_end;
+            int64_t off = 0;
+            if (valid) {
+                const uint32_t pix = (uint32_t)gr;
+                const uint32_t q = geom.ow_div.div(pix);
+                const int32_t ox = (int32_t)(pix - q * (uint32_t)geom.out_w);
+                const uint32_t b = geom.oh_div.div(q);
+                const int32_t oy = (int32_t)(q - b * (uint32_t)geom.out_h);
+                const int32_t iy = oy * geom.sy + ky - geom.py, ix = ox * geom.sx + kx - geom.px;
+                valid = iy >= 0 && iy < geom.height && ix >= 0 && ix < geom.width;
+                off = (int64_t)b * geom.height * geom.width * geom.channels +
+                      ((int64_t)iy * geom.width + ix) * geom.channels + c;
+            }
+            load_into<VEC>(this->reg + e * VEC, geom.src + (valid ? off : 0), valid);
+        }
+    }
+};
+
+// XMODE: 0 dense X, 1 convolution rows mode, 2 convolution cols mode.
+template <int BM, int BN, int BK, int WM, int WN, bool XR, bool YR, int VX, int VY, int XMODE>
 __global__ void __launch_bounds__(WM *WN * 64)
     gemm_kernel(GemmParams p) {
     constexpr int NT = WM * WN * 64;
     constexpr int TM = BM / WM, TN = BN / WN;
     constexpr int FM = TM / 32, FN = TN / 32;
-    using LX = TileLoader<BM, BK, NT, XR, VX>;
-    using LY = TileLoader<BN, BK, NT, YR, VY>;
+    using LX = std::conditional_t<XMODE == 0, DenseLoader<BM, BK, NT, XR, VX>,
+                                  std::conditional_t<XMODE == 1, ConvRowsLoader<BM, BK, NT, VX>,
+                                                     ConvColsLoader<BM, BK, NT, VX>>>;
+    using LY = DenseLoader<BN, BK, NT, YR, VY>;
     __shared__ float xs[BK * LX::LD];
     __shared__ float ys[BK * LY::LD];
 
@@ -127,9 +248,6 @@ __global__ void __launch_bounds__(WM *WN * 64)
     const int64_t r_begin = (int64_t)split * p.k_chunk;
     const int64_t r_end = r_begin + p.k_chunk < p.k ? r_begin + p.k_chunk : p.k;
 
-    const float *x = p.x + batch * p.x_batch;
-    const float *y = p.y + batch * p.y_batch;
-
     floatx16 acc[FM][FN];
 #pragma unroll
     for (int a = 0; a < FM; ++a)
@@ -140,9 +258,14 @@ __global__ void __launch_bounds__(WM *WN * 64)
 
     LX lx;
     LY ly;
+    if constexpr (XMODE == 0)
+        lx.init(p.x + batch * p.x_batch, p.x_si, p.x_sr, i0, p.m);
+    else
+        lx.init(p.conv, i0, p.m, tid);
+    ly.init(p.y + batch * p.y_batch, p.y_sj, p.y_sr, j0, p.n);
     if (r_begin < r_end) {
-        lx.load(x, p.x_si, p.x_sr, i0, r_begin, p.m, r_end, tid);
-        ly.load(y, p.y_sj, p.y_sr, j0, r_begin, p.n, r_end, tid);
+        lx.load(p.conv, r_begin, r_end, tid);
+        ly.load(p.conv, r_begin, r_end, tid);
         lx.store(xs, tid);
         ly.store(ys, tid);
     }
@@ -153,8 +276,8 @@ __global__ void __launch_bounds__(WM *WN * 64)
     for (int64_t r0 = r_begin; r0 < r_end; r0 += BK) {
         const bool more = r0 + BK < r_end;
         if (more) {
-            lx.load(x, p.x_si, p.x_sr, i0, r0 + BK, p.m, r_end, tid);
-            ly.load(y, p.y_sj, p.y_sr, j0, r0 + BK, p.n, r_end, tid);
+            lx.load(p.conv, r0 + BK, r_end, tid);
+            ly.load(p.conv, r0 + BK, r_end, tid);
         }
 #pragma unroll
         for (int kk = 0; kk < BK; kk += 2) {
@@ -178,28 +301,33 @@ __global__ void __launch_bounds__(WM *WN * 64)
     }
 
     // Accumulator layout of the 32x32 block: lane -> column l32; register v -> row
-    // 8*(v/4) + 4*(lane/32) + (v%4).
+    // 8*(v/4) + 4*(lane/32) + (v%4).  The bias (one value per column) is added only when the
+    // reduction is not split; split sums add it once at the end.
     float *c = p.c + batch * p.c_batch + (int64_t)split * p.c_split;
+    const bool with_bias = p.bias != nullptr && p.splits == 1;
 #pragma unroll
     for (int a = 0; a < FM; ++a)
 #pragma unroll
         for (int b = 0; b < FN; ++b) {
             const int64_t col = j0 + wn * TN + b * 32 + l32;
             if (col >= p.n) continue;
+            const float add = with_bias ? p.bias[col] : 0.0f;
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const int64_t row = i0 + wm * TM + a * 32 + (v >> 2) * 8 + half * 4 + (v & 3);
-                if (row < p.m) c[row * p.n + col] = acc[a][b][v];
+                if (row < p.m) c[row * p.n + col] = with_bias ? acc[a][b][v] + add : acc[a][b][v];
             }
         }
 }
 
 // Sum of reduction slices: lane group g (of 4) adds slices g, g+4, g+8, ... in order, then the
 // four group sums are added in group order -- a fixed association for a given slice count, so
-// the result is deterministic and independent of scheduling.
+// the result is deterministic and independent of scheduling.  The bias, when present, is added
+// to the total.
 __global__ void __launch_bounds__(256) split_sum_kernel(const float *__restrict__ partial,
                                                         float *__restrict__ out, int64_t len,
-                                                        int32_t splits, int64_t split_stride) {
+                                                        int32_t splits, int64_t split_stride,
+                                                        const float *__restrict__ bias, int64_t n) {
     __shared__ float acc[4][64];
     const int lane = threadIdx.x & 63, group = threadIdx.x >> 6;
     const int64_t i = (int64_t)blockIdx.x * 64 + lane;
@@ -208,24 +336,62 @@ __global__ void __launch_bounds__(256) split_sum_kernel(const float *__restrict_
         for (int32_t k = group; k < splits; k += 4) s += partial[k * split_stride + i];
     acc[group][lane] = s;
     __syncthreads();
-    if (group == 0 && i < len) out[i] = ((acc[0][lane] + acc[1][lane]) + acc[2][lane]) + acc[3][lane];
+    if (group == 0 && i < len) {
+        const float total = ((acc[0][lane] + acc[1][lane]) + acc[2][lane]) + acc[3][lane];
+        out[i] = bias ? total + bias[i % n] : total;
+    }
 }
 
-template <int BM, int BN, int BK, int WM, int WN, bool XR, bool YR, int VX, int VY>
+// Weight permutations between the reference's [(c, ky, kx), n] layout and the implicit-GEMM
+// orders.  mode 0: W'[(ky, kx, c), n] = W[(c, ky, kx), n]            (forward)
+//           mode 1: W''[(ky', kx', n), c] = W[(c, kh-1-ky', kw-1-kx'), n] (dgrad, flipped)
+//           mode 2: W[(c, ky, kx), n] = W'[(ky, kx, c), n]           (wgrad result back)
+__global__ void __launch_bounds__(256) conv_weight_permute_kernel(const float *__restrict__ src,
+                                                                  float *__restrict__ dst, int32_t c_in,
+                                                                  int32_t n_out, int32_t kh, int32_t kw,
+                                                                  int32_t mode) {
+    const int64_t total = (int64_t)c_in * kh * kw * n_out;
+    for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total;
+         idx += (int64_t)gridDim.x * 256) {
+        if (mode == 0) {
+            const int32_t n = (int32_t)(idx % n_out);
+            const int64_t r = idx / n_out;
+            const int32_t c = (int32_t)(r % c_in);
+            const int32_t pos = (int32_t)(r / c_in);
+            dst[idx] = src[((int64_t)c * kh * kw + pos) * n_out + n];
+        } else if (mode == 1) {
+            const int32_t c = (int32_t)(idx % c_in);
+            const int64_t r = idx / c_in;
+            const int32_t n = (int32_t)(r % n_out);
+            const int32_t pos = (int32_t)(r / n_out);
+            const int32_t ky = pos / kw, kx = pos % kw;
+            const int32_t flipped = (kh - 1 - ky) * kw + (kw - 1 - kx);
+            dst[idx] = src[((int64_t)c * kh * kw + flipped) * n_out + n];
+        } else {
+            const int32_t n = (int32_t)(idx % n_out);
+            const int64_t r = idx / n_out;
+            const int32_t pos = (int32_t)(r % (kh * kw));
+            const int32_t c = (int32_t)(r / (kh * kw));
+            dst[idx] = src[((int64_t)pos * c_in + c) * n_out + n];
+        }
+    }
+}
+
+template <int BM, int BN, int BK, int WM, int WN, bool XR, bool YR, int VX, int VY, int XMODE>
 void launch_config(const GemmParams &p, dim3 grid, hipStream_t stream) {
-    gemm_kernel<BM, BN, BK, WM, WN, XR, YR, VX, VY><<<grid, WM * WN * 64, 0, stream>>>(p);
+    gemm_kernel<BM, BN, BK, WM, WN, XR, YR, VX, VY, XMODE><<<grid, WM * WN * 64, 0, stream>>>(p);
 }
 
-template <int BM, int BN, int BK, int WM, int WN, bool XR, bool YR>
+template <int BM, int BN, int BK, int WM, int WN, bool XR, bool YR, int XMODE>
 void launch_vec(const GemmParams &p, dim3 grid, hipStream_t stream, bool vx, bool vy) {
     if (vx && vy)
-        launch_config<BM, BN, BK, WM, WN, XR, YR, 4, 4>(p, grid, stream);
+        launch_config<BM, BN, BK, WM, WN, XR, YR, 4, 4, XMODE>(p, grid, stream);
     else if (vx)
-        launch_config<BM, BN, BK, WM, WN, XR, YR, 4, 1>(p, grid, stream);
+        launch_config<BM, BN, BK, WM, WN, XR, YR, 4, 1, XMODE>(p, grid, stream);
     else if (vy)
-        launch_config<BM, BN, BK, WM, WN, XR, YR, 1, 4>(p, grid, stream);
+        launch_config<BM, BN, BK, WM, WN, XR, YR, 1, 4, XMODE>(p, grid, stream);
     else
-        launch_config<BM, BN, BK, WM, WN, XR, YR, 1, 1>(p, grid, stream);
+        launch_config<BM, BN, BK, WM, WN, XR, YR, 1, 1, XMODE>(p, grid, stream);
 }
 
 // Vector loads need the contiguous extent, the other stride and the base to be 4-aligned.
@@ -233,7 +399,7 @@ bool vec_ok(const float *base, int64_t contiguous_extent, int64_t other_stride) 
     return axis::aligned16(base) && contiguous_extent % 4 == 0 && other_stride % 4 == 0;
 }
 
-template <bool XR, bool YR>
+template <bool XR, bool YR, int XMODE>
 int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out) {
     const int64_t cus = device->multiprocessors;
     // Large tiles whenever both output extents fill them; a reduction split restores the block
@@ -259,8 +425,12 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out) {
     p.k_chunk = chunk;
     p.splits = static_cast<int32_t>(splits);
 
-    const bool vx = XR ? vec_ok(p.x, p.k, p.x_si) && p.x_batch % 4 == 0
-                       : vec_ok(p.x, p.m, p.x_sr) && p.x_batch % 4 == 0;
+    bool vx;
+    if constexpr (XMODE == 0)
+        vx = XR ? vec_ok(p.x, p.k, p.x_si) && p.x_batch % 4 == 0
+                : vec_ok(p.x, p.m, p.x_sr) && p.x_batch % 4 == 0;
+    else
+        vx = axis::aligned16(p.conv.src) && p.conv.channels % 4 == 0;
     const bool vy = YR ? vec_ok(p.y, p.k, p.y_sj) && p.y_batch % 4 == 0
                        : vec_ok(p.y, p.n, p.y_sr) && p.y_batch % 4 == 0;
 
@@ -282,14 +452,14 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out) {
     axis::TimedLaunch timed(device, "gemm", 2.0 * (double)batch * (double)p.m * (double)p.n * (double)p.k);
     dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n), static_cast<unsigned>(batch * splits));
     if (big)
-        launch_vec<128, 128, 32, 2, 2, XR, YR>(p, grid, device->stream, vx, vy);
+        launch_vec<128, 128, 32, 2, 2, XR, YR, XMODE>(p, grid, device->stream, vx, vy);
     else
-        launch_vec<64, 64, 16, 2, 2, XR, YR>(p, grid, device->stream, vx, vy);
+        launch_vec<64, 64, 16, 2, 2, XR, YR, XMODE>(p, grid, device->stream, vx, vy);
     int status = axis::launch_status("gemm_kernel");
     if (status) return status;
     if (splits > 1) {
         split_sum_kernel<<<axis::blocks_for(out_len, 64, INT32_MAX), 256, 0, device->stream>>>(
-            partial.as<float>(), out, out_len, static_cast<int32_t>(splits), out_len);
+            partial.as<float>(), out, out_len, static_cast<int32_t>(splits), out_len, p.bias, p.n);
         status = axis::launch_status("split_sum_kernel");
     }
     return status;
@@ -305,6 +475,71 @@ int check_dims(const void *a, const void *b, const void *out, int64_t batch, int
     AXIS_REQUIRE(m < (int64_t(1) << 31) / 2 && n < (int64_t(1) << 31) / 2,
                  "matmul output extent too large for one launch");
     return AXIS_OK;
+}
+
+struct ConvShape {
+    int64_t batch;
+    int32_t height, width, channels, out_channels, kh, kw, sy, sx, py, px, out_h, out_w;
+};
+
+int conv_shape(int64_t batch, int32_t height, int32_t width, int32_t channels, int32_t out_channels,
+               const int32_t *kernel, const int32_t *stride, const int32_t *padding, ConvShape *s) {
+    AXIS_REQUIRE(kernel && stride && padding, "null convolution geometry");
+    AXIS_REQUIRE(batch >= 1 && height >= 1 && width >= 1 && channels >= 1 && out_channels >= 1,
+                 "convolution extents must be positive");
+    AXIS_REQUIRE(kernel[0] >= 1 && kernel[1] >= 1 && stride[0] >= 1 && stride[1] >= 1 &&
+                     padding[0] >= 0 && padding[1] >= 0,
+                 "convolution kernel/stride must be positive and padding nonnegative");
+    AXIS_REQUIRE(height + 2 * padding[0] >= kernel[0] && width + 2 * padding[1] >= kernel[1],
+                 "convolution kernel exceeds the padded spatial extent");
+    s->batch = batch;
+    s->height = height;
+    s->width = width;
+    s->channels = channels;
+    s->out_channels = out_channels;
+    s->kh = kernel[0];
+    s->kw = kernel[1];
+    s->sy = stride[0];
+    s->sx = stride[1];
+    s->py = padding[0];
+    s->px = padding[1];
+    s->out_h = (height + 2 * padding[0] - kernel[0]) / stride[0] + 1;
+    s->out_w = (width + 2 * padding[1] - kernel[1]) / stride[1] + 1;
+    const int64_t in_len = batch * height * width * channels;
+    const int64_t out_len = batch * (int64_t)s->out_h * s->out_w * out_channels;
+    const int64_t patch = (int64_t)channels * kernel[0] * kernel[1];
+    AXIS_REQUIRE(in_len < INT32_MAX && out_len < INT32_MAX && batch * s->out_h * s->out_w < INT32_MAX &&
+                     patch * out_channels < INT32_MAX && batch * (int64_t)s->out_h * s->out_w * patch < (int64_t(1) << 40),
+                 "convolution too large for 32-bit pixel indexing");
+    return AXIS_OK;
+}
+
+ConvGeom geom(const float *src, int32_t height, int32_t width, int32_t channels, int32_t out_h,
+              int32_t out_w, int32_t kw, int32_t sy, int32_t sx, int32_t py, int32_t px) {
+    ConvGeom g{};
+    g.src = src;
+    g.height = height;
+    g.width = width;
+    g.channels = channels;
+    g.out_h = out_h;
+    g.out_w = out_w;
+    g.kw = kw;
+    g.sy = sy;
+    g.sx = sx;
+    g.py = py;
+    g.px = px;
+    g.c_div = FastDiv((uint32_t)channels);
+    g.kw_div = FastDiv((uint32_t)kw);
+    g.ow_div = FastDiv((uint32_t)out_w);
+    g.oh_div = FastDiv((uint32_t)out_h);
+    return g;
+}
+
+int permute_weight(axis_device device, const float *src, float *dst, const ConvShape &s, int mode) {
+    const int64_t total = (int64_t)s.channels * s.kh * s.kw * s.out_channels;
+    conv_weight_permute_kernel<<<axis::blocks_for(total, 256, 4096), 256, 0, device->stream>>>(
+        src, dst, s.channels, s.out_channels, s.kh, s.kw, mode);
+    return axis::launch_status("conv_weight_permute_kernel");
 }
 
 }  // namespace
@@ -327,7 +562,7 @@ int axis_matmul(axis_device device, const float *a, const float *b, float *out, 
     p.y_sj = 1;
     p.x_batch = m * k;
     p.y_batch = k * n;
-    return run_gemm<true, false>(device, p, batch, out);
+    return run_gemm<true, false, 0>(device, p, batch, out);
 }
 
 int axis_matmul_left_backward(axis_device device, const float *gradient, const float *rhs,
@@ -347,7 +582,7 @@ int axis_matmul_left_backward(axis_device device, const float *gradient, const f
     p.y_sj = n;
     p.x_batch = m * n;
     p.y_batch = k * n;
-    return run_gemm<true, true>(device, p, batch, out);
+    return run_gemm<true, true, 0>(device, p, batch, out);
 }
 
 int axis_matmul_right_backward(axis_device device, const float *lhs, const float *gradient,
@@ -367,7 +602,90 @@ int axis_matmul_right_backward(axis_device device, const float *lhs, const float
     p.y_sj = 1;
     p.x_batch = m * k;
     p.y_batch = m * n;
-    return run_gemm<false, false>(device, p, batch, out);
+    return run_gemm<false, false, 0>(device, p, batch, out);
+}
+
+int axis_conv2d_forward(axis_device device, const float *input, const float *weight,
+                        const float *bias, float *out, int64_t batch, int32_t height, int32_t width,
+                        int32_t channels, int32_t out_channels, const int32_t kernel[2],
+                        const int32_t stride[2], const int32_t padding[2]) {
+    AXIS_ENTER(device);
+    AXIS_REQUIRE(input && weight && out, "null convolution buffer");
+    ConvShape s{};
+    if (int st = conv_shape(batch, height, width, channels, out_channels, kernel, stride, padding, &s))
+        return st;
+    const int64_t patch = (int64_t)channels * s.kh * s.kw;
+    axis::Scratch permuted;
+    if (int st = permuted.get(device, sizeof(float) * (size_t)(patch * out_channels))) return st;
+    if (int st = permute_weight(device, weight, permuted.as<float>(), s, 0)) return st;
+    GemmParams p{};
+    p.x = input;
+    p.y = permuted.as<float>();
+    p.bias = bias;
+    p.m = batch * s.out_h * s.out_w;
+    p.n = out_channels;
+    p.k = patch;
+    p.y_sr = out_channels;
+    p.y_sj = 1;
+    p.conv = geom(input, height, width, channels, s.out_h, s.out_w, s.kw, s.sy, s.sx, s.py, s.px);
+    return run_gemm<true, false, 1>(device, p, 1, out);
+}
+
+int axis_conv2d_backward_data(axis_device device, const float *gradient, const float *weight,
+                              float *d_input, int64_t batch, int32_t height, int32_t width,
+                              int32_t channels, int32_t out_channels, const int32_t kernel[2],
+                              const int32_t stride[2], const int32_t padding[2]) {
+    AXIS_ENTER(device);
+    AXIS_REQUIRE(gradient && weight && d_input, "null convolution buffer");
+    ConvShape s{};
+    if (int st = conv_shape(batch, height, width, channels, out_channels, kernel, stride, padding, &s))
+        return st;
+    AXIS_REQUIRE(s.sy == 1 && s.sx == 1, "implicit convolution dgrad supports stride 1 only");
+    AXIS_REQUIRE(s.py <= s.kh - 1 && s.px <= s.kw - 1, "implicit convolution dgrad needs padding < kernel");
+    const int64_t patch = (int64_t)channels * s.kh * s.kw;
+    axis::Scratch flipped;
+    if (int st = flipped.get(device, sizeof(float) * (size_t)(patch * out_channels))) return st;
+    if (int st = permute_weight(device, weight, flipped.as<float>(), s, 1)) return st;
+    // d_input[b, y, x, c] = sum over (ky', kx', n) of gradient[b, y + ky' - (kh-1-py),
+    // x + kx' - (kw-1-px), n] * W[(c, kh-1-ky', kw-1-kx'), n]: a stride-1 convolution of the
+    // output gradient with the flipped, transposed kernel -- the reference's col2im of
+    // gradient . W^T, summed in a different (fp32) order.
+    GemmParams p{};
+    p.x = gradient;
+    p.y = flipped.as<float>();
+    p.m = batch * (int64_t)height * width;
+    p.n = channels;
+    p.k = (int64_t)s.kh * s.kw * out_channels;
+    p.y_sr = channels;
+    p.y_sj = 1;
+    p.conv = geom(gradient, s.out_h, s.out_w, out_channels, height, width, s.kw, 1, 1, s.kh - 1 - s.py,
+                  s.kw - 1 - s.px);
+    return run_gemm<true, false, 1>(device, p, 1, d_input);
+}
+
+int axis_conv2d_backward_weight(axis_device device, const float *input, const float *gradient,
+                                float *d_weight, int64_t batch, int32_t height, int32_t width,
+                                int32_t channels, int32_t out_channels, const int32_t kernel[2],
+                                const int32_t stride[2], const int32_t padding[2]) {
+    AXIS_ENTER(device);
+    AXIS_REQUIRE(input && gradient && d_weight, "null convolution buffer");
+    ConvShape s{};
+    if (int st = conv_shape(batch, height, width, channels, out_channels, kernel, stride, padding, &s))
+        return st;
+    const int64_t patch = (int64_t)channels * s.kh * s.kw;
+    axis::Scratch ordered;
+    if (int st = ordered.get(device, sizeof(float) * (size_t)(patch * out_channels))) return st;
+    GemmParams p{};
+    p.x = input;
+    p.y = gradient;
+    p.m = patch;
+    p.n = out_channels;
+    p.k = batch * (int64_t)s.out_h * s.out_w;
+    p.y_sr = out_channels;
+    p.y_sj = 1;
+    p.conv = geom(input, height, width, channels, s.out_h, s.out_w, s.kw, s.sy, s.sx, s.py, s.px);
+    if (int st = run_gemm<false, false, 2>(device, p, 1, ordered.as<float>())) return st;
+    return permute_weight(device, ordered.as<float>(), d_weight, s, 2);
 }
 
 }  // extern "C"

@@ -103,6 +103,13 @@ struct PoolGeometry {
     int32_t kernel[2] = {1, 1}, stride[2] = {1, 1}, padding[2] = {0, 0};
 };
 
+// A one-group convolution of a channel-innermost [batch, height, width, channels] input.
+struct ConvGeometry {
+    int64_t batch = 0;
+    int32_t height = 0, width = 0, channels = 0, out_channels = 0;
+    int32_t kernel[2] = {1, 1}, stride[2] = {1, 1}, padding[2] = {0, 0};
+};
+
 // Device (runtime/backend.rs:116-392): one GPU, one stream, out-of-place ops returning fresh
 // buffers, exactly the reference's method surface for the hot path.
 class Device {
@@ -153,8 +160,8 @@ struct Node;
 class Tensor;
 
 // One saved backward rule (algebra/tensor.rs:143-238), plus the rules of this backend's fused
-// lowerings (BiasBroadcast, MeanMiddle, MaxPool), each the exact derivative of the composition it
-// replaces.
+// lowerings (BiasBroadcast, MeanMiddle, MaxPool, ConvData, ConvWeight), each the exact
+// derivative of the composition it replaces.
 struct Rule {
     enum Kind {
         Identity,
@@ -172,6 +179,8 @@ struct Rule {
         BiasBroadcast,
         MeanMiddle,
         MaxPool,
+        ConvData,    // input gradient of an implicit-GEMM convolution (a = weight)
+        ConvWeight,  // weight gradient of an implicit-GEMM convolution (a = input)
     } kind = Identity;
     float factor = 1.0f;
     Buffer a, b;  // saved operands (rhs / lhs / probability / input / winners / argmax)
@@ -181,6 +190,7 @@ struct Rule {
     std::vector<int32_t> metadata;  // select_axis metadata
     int64_t outer = 0, reduce = 0, inner = 0;
     PoolGeometry pool;
+    ConvGeometry conv;
 };
 
 struct Edge;

@@ -193,8 +193,58 @@ Shape Conv2d::build(const Shape &in, const Device &device, uint64_t seed) {
 }
 
 Tensor Conv2d::forward(const Tensor &x) {
-    output_shape(x.shape());
+    Shape out_shape = output_shape(x.shape());
     if (!bound) raise("Conv2d must be built before forward");
+    // A one-group, stride-1 convolution of a contiguous [.., height, width, channels] input runs
+    // as implicit GEMM (no patch matrix) with the bias added in the epilogue; its rules are the
+    // derivatives of exactly that composition.  Every other geometry takes the reference's
+    // unfold -> contract -> merge -> add lowering below.
+    const Shape &in = x.shape();
+    const size_t r = in.rank();
+    const bool channels_last = r >= 3 && x.is_contiguous() && in.dims[r - 1].axis == input &&
+                               in.dims[r - 3].axis == spatial[0] && in.dims[r - 2].axis == spatial[1];
+    if (groups == 1 && channels_last && stride[0] == 1 && stride[1] == 1 &&
+        padding[0] <= kernel[0] - 1 && padding[1] <= kernel[1] - 1 && in.len < (int64_t(1) << 31) &&
+        out_shape.len < (int64_t(1) << 31)) {
+        ConvGeometry q;
+        q.channels = (int32_t)in.dims[r - 1].extent;
+        q.height = (int32_t)in.dims[r - 3].extent;
+        q.width = (int32_t)in.dims[r - 2].extent;
+        q.batch = in.len / ((int64_t)q.channels * q.height * q.width);
+        q.out_channels = (int32_t)output.extent;
+        for (int i = 0; i < 2; ++i) {
+            q.kernel[i] = (int32_t)kernel[i];
+            q.stride[i] = (int32_t)stride[i];
+            q.padding[i] = (int32_t)padding[i];
+        }
+        const Device &dev = x.device();
+        Tensor w = bound->weight.tensor();
+        Buffer out = dev.alloc(out_shape.len);
+        const float *bias_ptr = bound->bias ? bound->bias->tensor().value()->f32() : nullptr;
+        check(axis_conv2d_forward(dev.h(), x.value()->f32(), w.value()->f32(), bias_ptr, out->f32(),
+                                  q.batch, q.height, q.width, q.channels, q.out_channels, q.kernel,
+                                  q.stride, q.padding),
+              "conv2d_forward");
+        std::vector<Edge> edges;
+        Rule data;
+        data.kind = Rule::ConvData;
+        data.a = w.value();
+        data.conv = q;
+        edges.push_back(Edge{x, data});
+        Rule weight_rule;
+        weight_rule.kind = Rule::ConvWeight;
+        weight_rule.a = x.value();
+        weight_rule.conv = q;
+        edges.push_back(Edge{w, weight_rule});
+        if (bound->bias) {
+            Rule rb;
+            rb.kind = Rule::BiasBroadcast;
+            rb.outer = out_shape.len / output.extent;
+            rb.inner = output.extent;
+            edges.push_back(Edge{bound->bias->tensor(), rb});
+        }
+        return Tensor::node(out_shape, Layout::contiguous(out_shape), out, dev, std::move(edges), false);
+    }
     Tensor projected = x.unfold_grouped(input, spatial, Dim{group, groups}, Dim{patch, bound->patch},
                                         kernel, stride, padding, 0.0f)
                            .contract(bound->weight.tensor(), {patch})

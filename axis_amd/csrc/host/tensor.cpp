@@ -892,11 +892,13 @@ void Tensor::backward() const {
                            (*x->edges)[0].rule.kind == Rule::Identity &&
                            (*x->edges)[0].input.n->value == x->value)
                         x = (*x->edges)[0].input.n;
+                    // The add node's other edges all consume the same (masked) adjoint.
                     const Rule *bias_rule = nullptr;
-                    if (uses[x->id] == 1 && x->edges && x->edges->size() == 2) {
-                        const Rule &r0 = (*x->edges)[0].rule, &r1 = (*x->edges)[1].rule;
-                        if (r0.kind == Rule::Identity && r1.kind == Rule::BiasBroadcast) bias_rule = &r1;
-                        if (r1.kind == Rule::Identity && r0.kind == Rule::BiasBroadcast) bias_rule = &r0;
+                    if (uses[x->id] == 1 && x->edges) {
+                        int biases = 0;
+                        for (auto &xe : *x->edges)
+                            if (xe.rule.kind == Rule::BiasBroadcast) bias_rule = &xe.rule, ++biases;
+                        if (biases != 1) bias_rule = nullptr;
                     }
                     if (bias_rule && bias_rule->outer * bias_rule->inner == g->floats()) {
                         c = dev.alloc(g->floats());
@@ -945,6 +947,24 @@ void Tensor::backward() const {
                                                 r.factor),
                           "broadcast_middle");
                     break;
+                case Rule::ConvData: {
+                    const ConvGeometry &q = r.conv;
+                    c = dev.alloc(q.batch * q.height * q.width * q.channels);
+                    check(axis_conv2d_backward_data(dev.h(), g->f32(), r.a->f32(), c->f32(), q.batch,
+                                                    q.height, q.width, q.channels, q.out_channels,
+                                                    q.kernel, q.stride, q.padding),
+                          "conv2d_backward_data");
+                    break;
+                }
+                case Rule::ConvWeight: {
+                    const ConvGeometry &q = r.conv;
+                    c = dev.alloc((int64_t)q.channels * q.kernel[0] * q.kernel[1] * q.out_channels);
+                    check(axis_conv2d_backward_weight(dev.h(), r.a->f32(), g->f32(), c->f32(), q.batch,
+                                                      q.height, q.width, q.channels, q.out_channels,
+                                                      q.kernel, q.stride, q.padding),
+                          "conv2d_backward_weight");
+                    break;
+                }
                 case Rule::MaxPool: {
                     const PoolGeometry &p = r.pool;
                     c = dev.alloc(p.outer * p.height * p.width * p.channels);

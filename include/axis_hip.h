@@ -258,6 +258,29 @@ int axis_reduce_middle(axis_device device, const float *a, float *out, int64_t o
 /* Its Group-rule backward: out[o][r][i] = factor * gradient[o][i]. */
 int axis_broadcast_middle(axis_device device, const float *gradient, float *out, int64_t outer,
                           int64_t reduce, int64_t inner, float factor);
+/* Implicit-GEMM convolution of a channel-innermost input, one group: the reference's Conv2d
+ * lowering (convolution.rs:211-235: unfold -> contract -> merge -> + bias) without materialising
+ * the patch matrix.  input [batch, height, width, channels] contiguous; weight in the reference's
+ * layout [(channel, ky, kx), out_channels]; bias [out_channels] or NULL;
+ * out [batch, out_h, out_w, out_channels].  The patch reduction runs in (ky, kx, channel) order on
+ * fp32 MFMA, so results agree with the explicit path to fp32 tolerance. */
+int axis_conv2d_forward(axis_device device, const float *input, const float *weight,
+                        const float *bias, float *out, int64_t batch, int32_t height, int32_t width,
+                        int32_t channels, int32_t out_channels, const int32_t kernel[2],
+                        const int32_t stride[2], const int32_t padding[2]);
+/* Its input gradient (Rule::MatmulLeft then Rule::Unfold, tensor.rs:5650-5680): d_input
+ * [batch, height, width, channels] from gradient [batch, out_h, out_w, out_channels], computed as
+ * a stride-1 convolution with the flipped kernel (no col2im pass).  Stride 1 only. */
+int axis_conv2d_backward_data(axis_device device, const float *gradient, const float *weight,
+                              float *d_input, int64_t batch, int32_t height, int32_t width,
+                              int32_t channels, int32_t out_channels, const int32_t kernel[2],
+                              const int32_t stride[2], const int32_t padding[2]);
+/* Its weight gradient (Rule::MatmulRight over the patches): d_weight in the reference's layout
+ * [(channel, ky, kx), out_channels], deterministic split over output pixels. */
+int axis_conv2d_backward_weight(axis_device device, const float *input, const float *gradient,
+                                float *d_weight, int64_t batch, int32_t height, int32_t width,
+                                int32_t channels, int32_t out_channels, const int32_t kernel[2],
+                                const int32_t stride[2], const int32_t padding[2]);
 /* Softmax + categorical cross-entropy of [rows, width] logits in one pass (tensor.rs:1540-1543):
  * writes probability [rows, width] and per-row loss [rows]; each equals the separate entries. */
 int axis_softmax_cross_entropy(axis_device device, const float *logits, const float *targets,

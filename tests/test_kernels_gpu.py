@@ -372,3 +372,39 @@ def test_reduce_and_broadcast_middle_bit_exact(dev, oracle):
     back = dev.empty(len(a))
     dev.call("axis_broadcast_middle", out.vp, back.vp, I64(outer), I64(red), I64(inner), F32(factor))
     assert np.array_equal(dev.read(back, len(a)), oracle.grouped(got, None, rev, factor))
+
+
+# ---------------------------------------------------------------- implicit-GEMM convolution
+
+@pytest.mark.parametrize("b,h,w,c,n,k,s,p", [(2, 9, 7, 8, 16, 3, 1, 1), (3, 16, 16, 64, 128, 3, 1, 1),
+                                             (2, 11, 10, 5, 7, 3, 1, 0), (2, 9, 8, 12, 20, 3, 2, 1),
+                                             (1, 8, 8, 128, 256, 3, 1, 1), (2, 6, 6, 4, 8, 2, 1, 1)])
+def test_conv2d_entries_match_explicit_lowering(dev, oracle, b, h, w, c, n, k, s, p):
+    rng = np.random.default_rng(b * 100 + c)
+    x = rng.standard_normal(b * h * w * c).astype(np.float32)
+    weight = rng.standard_normal(c * k * k * n).astype(np.float32) * 0.1
+    bias = rng.standard_normal(n).astype(np.float32)
+    dims = [("batch", b), ("height", h), ("width", w), ("c", c)]
+    u = oracle.unfold_spec(dims, oracle.contiguous(dims), "c", ["height", "width"], ("group", 1),
+                           ("patch", c * k * k), [k, k], [s, s], [p, p], 0.0)
+    oh, ow = (h + 2 * p - k) // s + 1, (w + 2 * p - k) // s + 1
+    m = b * oh * ow
+    patches = oracle.unfold2d(x, u)
+    ref = oracle.binary(oracle.matmul(patches, weight, 1, m, c * k * k, n), np.tile(bias, m), 0)
+    geo = [(I32 * 2)(k, k), (I32 * 2)(s, s), (I32 * 2)(p, p)]
+    dx, dw, db, out = up(dev, x), up(dev, weight), up(dev, bias), dev.empty(m * n)
+    dev.call("axis_conv2d_forward", dx.vp, dw.vp, db.vp, out.vp, I64(b), I32(h), I32(w), I32(c), I32(n), *geo)
+    assert rel_err(dev.read(out, m * n), ref) < 1e-5
+    g = rng.standard_normal(m * n).astype(np.float32)
+    dg = up(dev, g)
+    gw = dev.empty(c * k * k * n)
+    dev.call("axis_conv2d_backward_weight", dx.vp, dg.vp, gw.vp, I64(b), I32(h), I32(w), I32(c), I32(n), *geo)
+    assert rel_err(dev.read(gw, c * k * k * n), oracle.matmul_right_backward(patches, g, 1, m, c * k * k, n)) < 1e-5
+    gx = dev.empty(b * h * w * c)
+    if s == 1:
+        dev.call("axis_conv2d_backward_data", dg.vp, dw.vp, gx.vp, I64(b), I32(h), I32(w), I32(c), I32(n), *geo)
+        ref_dx = oracle.unfold2d_backward(oracle.matmul_left_backward(g, weight, 1, m, c * k * k, n), u, len(x))
+        assert rel_err(dev.read(gx, len(x)), ref_dx) < 1e-5
+    else:
+        with pytest.raises(hip.AxisError, match="stride 1"):
+            dev.call("axis_conv2d_backward_data", dg.vp, dw.vp, gx.vp, I64(b), I32(h), I32(w), I32(c), I32(n), *geo)
