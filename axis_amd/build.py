@@ -30,6 +30,9 @@ HIP_FLAGS = [
 # Sources whose arithmetic must round exactly as written (no fused multiply-add contraction).
 EXACT = {"device.hip", "unfold.hip", "grouped.hip", "elementwise.hip", "pool.hip", "loss.hip",
          "optim.hip"}
+# Matrix-core kernels keep their accumulators in ordinary VGPRs: the MFMA VGPR form avoids the
+# per-iteration AGPR<->VGPR copies the default allocation inserts around the K loop.
+EXTRA = {"gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 HIP_SOURCES = ["device.hip", "gemm.hip", "unfold.hip", "grouped.hip", "elementwise.hip",
                "pool.hip", "loss.hip", "optim.hip"]
 
@@ -48,6 +51,7 @@ def _compile_hip(src):
     flags = list(HIP_FLAGS)
     if src in EXACT:
         flags.append("-ffp-contract=off")
+    flags += EXTRA.get(src, [])
     _run([HIPCC, *flags, "-c", os.path.join(CSRC, src), "-o", obj])
     return obj
 

@@ -8,6 +8,7 @@
 #include <cfloat>
 
 #include "common.hpp"
+#include "column_sum.hpp"
 #include "fastdiv.hpp"
 
 namespace {
@@ -259,16 +260,18 @@ struct BiasAdd {
 
 // Stage one of the bias gradient: partial[q][c] = sum of rows [512q, 512q+512) of column c,
 // sequentially; optionally masked by relu_input > 0 (and the masked gradient written out).
+// One lane per (chunk, column) pair, columns fastest, so narrow activations still fill blocks.
 template <bool MASK>
 __global__ void __launch_bounds__(kBlock) column_chunk_kernel(const float *__restrict__ g,
                                                               const float *__restrict__ relu_input,
                                                               float *__restrict__ masked_out,
                                                               float *__restrict__ partial,
                                                               int64_t rows, int64_t width,
-                                                              int64_t column_blocks) {
-    const int64_t q = blockIdx.x / column_blocks;
-    const int64_t c = (blockIdx.x % column_blocks) * kBlock + threadIdx.x;
-    if (c >= width) return;
+                                                              int64_t pairs) {
+    const int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (t >= pairs) return;
+    const int64_t q = t / width;
+    const int64_t c = t - q * width;
     const int64_t r0 = q * axis::kGroupedChunk;
     const int64_t r1 = r0 + axis::kGroupedChunk < rows ? r0 + axis::kGroupedChunk : rows;
     float sum = 0.0f;
@@ -283,38 +286,6 @@ __global__ void __launch_bounds__(kBlock) column_chunk_kernel(const float *__res
         sum = sum + v;
     }
     partial[q * width + c] = sum;
-}
-
-// Stage two: one block per column.  The block stages the column's chunk partials through LDS
-// (parallel, coalesced across chunks of the same column block) and one lane adds them in chunk
-// order, so the association is the reference's ((0 + p0) + p1) + ... exactly.
-constexpr int kCombineStage = 4096;
-
-__global__ void __launch_bounds__(kBlock) column_combine_kernel(const float *__restrict__ partial,
-                                                                int64_t chunks, int64_t width,
-                                                                float scale, float *__restrict__ out) {
-    __shared__ __attribute__((aligned(16))) float staged[kCombineStage];
-    const int64_t c = blockIdx.x;
-    float sum = 0.0f;
-    for (int64_t base = 0; base < chunks; base += kCombineStage) {
-        const int n = (int)(chunks - base < kCombineStage ? chunks - base : kCombineStage);
-        for (int i = threadIdx.x; i < n; i += kBlock) staged[i] = partial[(base + i) * width + c];
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            const floatx4 *v = reinterpret_cast<const floatx4 *>(staged);
-            int i = 0;
-            for (; i + 4 <= n; i += 4) {
-                const floatx4 q = v[i / 4];
-                sum = sum + q[0];
-                sum = sum + q[1];
-                sum = sum + q[2];
-                sum = sum + q[3];
-            }
-            for (; i < n; ++i) sum = sum + staged[i];
-        }
-        __syncthreads();
-    }
-    if (threadIdx.x == 0) out[c] = sum * scale;
 }
 
 // out[o][i] = factor * sum_r a[o][r][i] in the reference's chunked order.
@@ -469,20 +440,20 @@ int axis_bias_gradient(axis_device device, const float *gradient, const float *r
     AXIS_REQUIRE(!relu_input || masked_out, "a masked bias gradient needs masked_out");
     AXIS_REQUIRE(rows >= 1 && width >= 1, "bias_gradient extents must be positive");
     const int64_t chunks = (rows + axis::kGroupedChunk - 1) / axis::kGroupedChunk;
-    const int64_t column_blocks = (width + kBlock - 1) / kBlock;
-    AXIS_REQUIRE(chunks * column_blocks < INT32_MAX, "bias_gradient too large");
+    const int64_t pairs = chunks * width;
+    AXIS_REQUIRE(pairs / kBlock < INT32_MAX && width < INT32_MAX, "bias_gradient too large");
     axis::Scratch partial;
-    if (int s = partial.get(device, sizeof(float) * (size_t)(chunks * width))) return s;
-    const unsigned grid = (unsigned)(chunks * column_blocks);
+    if (int s = partial.get(device, sizeof(float) * (size_t)pairs)) return s;
+    const unsigned grid = axis::blocks_for(pairs, kBlock, INT32_MAX);
     if (relu_input)
         column_chunk_kernel<true><<<grid, kBlock, 0, device->stream>>>(
-            gradient, relu_input, masked_out, partial.as<float>(), rows, width, column_blocks);
+            gradient, relu_input, masked_out, partial.as<float>(), rows, width, pairs);
     else
         column_chunk_kernel<false><<<grid, kBlock, 0, device->stream>>>(
-            gradient, nullptr, nullptr, partial.as<float>(), rows, width, column_blocks);
+            gradient, nullptr, nullptr, partial.as<float>(), rows, width, pairs);
     if (int s = axis::launch_status("column_chunk_kernel")) return s;
-    column_combine_kernel<<<(unsigned)width, kBlock, 0, device->stream>>>(partial.as<float>(), chunks,
-                                                                        width, 1.0f, out);
+    axis::column_combine_kernel<<<(unsigned)width, 256, 0, device->stream>>>(partial.as<float>(), chunks,
+                                                                           width, 1.0f, out);
     return axis::launch_status("column_combine_kernel");
 }
 

@@ -13,7 +13,13 @@
 //   rows mode   : X(i = output pixel, r = (ky*kw + kx)*c + channel)   (forward, dgrad)
 //   cols mode   : X(i = (ky*kw + kx)*c + channel, r = output pixel)   (wgrad)
 // with zero outside the padded input.  Reordering the reduction as (ky, kx, channel) makes every
-// gathered vector contiguous in memory; the weights are permuted to match (a few KB).
+// gathered vector contiguous in memory when channels are innermost; the weights are permuted to
+// match (a few KB).  Any other input layout (e.g. channel-major [batch, c, h, w]) is gathered
+// element by element through its strides.
+//
+// The forward can end in a fused epilogue: bias, ReLU and a non-overlapping max pool over whole
+// windows, with the pool's window-local winner emitted as a byte.  The tile is staged in LDS so
+// every window is complete inside one block; the pre-activation never reaches HBM.
 //
 // Tiles are staged through LDS as [r][i] / [r][j] so every MFMA operand read is a unit-stride
 // LDS access across the wave.  The next K tile is prefetched into registers while the current
@@ -21,6 +27,7 @@
 // split into slices whose partial tiles are summed afterwards in a fixed order (deterministic,
 // no atomics).
 #include <algorithm>
+#include <cfloat>
 #include <type_traits>
 
 #include "common.hpp"
@@ -34,6 +41,8 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 // Geometry of a gathered convolution operand (tensor [batch, height, width, channels]).
 struct ConvGeom {
     const float *src;
+    int64_t ld_b;                     // element strides of batch, channel, row, column
+    int32_t ld_c, ld_h, ld_w;
     int32_t height, width, channels;  // gathered tensor
     int32_t out_h, out_w;             // output pixel grid the reduction/rows enumerate
     int32_t kw, sy, sx, py, px;
@@ -52,9 +61,14 @@ struct GemmParams {
     int64_t c_batch;           // batch stride of the output (or of one slice of partials)
     int64_t c_split;           // stride between reduction slices in the output (partials)
     int64_t k_chunk;           // reduction length per slice (multiple of the tile depth)
+    int64_t k_work;            // algorithmic reduction length for timing (k without padding), or 0
     int32_t splits;
     int32_t tiles_m, tiles_n;
     ConvGeom conv;
+    // Pooling epilogue: output rows are pixels of a [.., out_h, out_w] grid (out_w = pool_ow).
+    float *pooled;
+    uint8_t *argmax;
+    int32_t pool_h, pool_w, pool_ow;
 };
 
 template <int VEC>
@@ -146,19 +160,17 @@ struct ConvRowsLoader : Staging<BT, BK, NT, true, VEC> {
 #pragma unroll
         for (int e = 0; e < S::kVecs; ++e) {
             const int64_t gt = t0 + (tid + e * NT) / S::kPer;
-            if (gt < t_end) {
-                const uint32_t pix = (uint32_t)gt;
-                const uint32_t q = geom.ow_div.div(pix);
-                const int32_t ox = (int32_t)(pix - q * (uint32_t)geom.out_w);
-                const uint32_t b = geom.oh_div.div(q);
-                const int32_t oy = (int32_t)(q - b * (uint32_t)geom.out_h);
-                pixel_base[e] = (int64_t)b * geom.height * geom.width * geom.channels;
-                iy0[e] = oy * geom.sy - geom.py;
-                ix0[e] = ox * geom.sx - geom.px;
-            } else {
-                pixel_base[e] = -1;
-                iy0[e] = ix0[e] = 0;
-            }
+            // Rows past the end get base -1 and a far-out origin; computed branch-free so the
+            // per-row arrays stay in registers.
+            const bool live = gt < t_end;
+            const uint32_t pix = live ? (uint32_t)gt : 0u;
+            const uint32_t q = geom.ow_div.div(pix);
+            const int32_t ox = (int32_t)(pix - q * (uint32_t)geom.out_w);
+            const uint32_t b = geom.oh_div.div(q);
+            const int32_t oy = (int32_t)(q - b * (uint32_t)geom.out_h);
+            pixel_base[e] = live ? (int64_t)b * geom.ld_b : -1;
+            iy0[e] = oy * geom.sy - geom.py;
+            ix0[e] = ox * geom.sx - geom.px;
         }
     }
     __device__ __forceinline__ void load(const ConvGeom &geom, int64_t r0, int64_t r_end, int) {
@@ -176,7 +188,9 @@ struct ConvRowsLoader : Staging<BT, BK, NT, true, VEC> {
             const int32_t iy = iy0[e] + ky, ix = ix0[e] + kx;
             const bool valid = r_ok && pixel_base[e] >= 0 && iy >= 0 && iy < geom.height && ix >= 0 &&
                                ix < geom.width;
-            const int64_t off = valid ? pixel_base[e] + ((int64_t)iy * geom.width + ix) * geom.channels + c : 0;
+            const int64_t off =
+                valid ? pixel_base[e] + (int64_t)iy * geom.ld_h + (int64_t)ix * geom.ld_w + (int64_t)c * geom.ld_c
+                      : 0;
             load_into<VEC>(this->reg + e * VEC, geom.src + off, valid);
         }
     }
@@ -213,8 +227,8 @@ struct ConvColsLoader : Staging<BT, BK, NT, false, VEC> {
                 const int32_t oy = (int32_t)(q - b * (uint32_t)geom.out_h);
                 const int32_t iy = oy * geom.sy + ky - geom.py, ix = ox * geom.sx + kx - geom.px;
                 valid = iy >= 0 && iy < geom.height && ix >= 0 && ix < geom.width;
-                off = (int64_t)b * geom.height * geom.width * geom.channels +
-                      ((int64_t)iy * geom.width + ix) * geom.channels + c;
+                off = (int64_t)b * geom.ld_b + (int64_t)iy * geom.ld_h + (int64_t)ix * geom.ld_w +
+                      (int64_t)c * geom.ld_c;
             }
             load_into<VEC>(this->reg + e * VEC, geom.src + (valid ? off : 0), valid);
         }
@@ -222,7 +236,8 @@ struct ConvColsLoader : Staging<BT, BK, NT, false, VEC> {
 };
 
 // XMODE: 0 dense X, 1 convolution rows mode, 2 convolution cols mode.
-template <int BM, int BN, int BK, int WM, int WN, bool XR, bool YR, int VX, int VY, int XMODE>
+// EPI: 0 store C (+ bias), 1 bias + ReLU + max pool of whole windows (rows are output pixels).
+template <int BM, int BN, int BK, int WM, int WN, bool XR, bool YR, int VX, int VY, int XMODE, int EPI>
 __global__ void __launch_bounds__(WM *WN * 64)
     gemm_kernel(GemmParams p) {
     constexpr int NT = WM * WN * 64;
@@ -232,8 +247,12 @@ __global__ void __launch_bounds__(WM *WN * 64)
                                   std::conditional_t<XMODE == 1, ConvRowsLoader<BM, BK, NT, VX>,
                                                      ConvColsLoader<BM, BK, NT, VX>>>;
     using LY = DenseLoader<BN, BK, NT, YR, VY>;
-    __shared__ float xs[BK * LX::LD];
-    __shared__ float ys[BK * LY::LD];
+    constexpr int kStage = BK * LX::LD + BK * LY::LD;
+    constexpr int kPoolPitch = TN + 1;
+    constexpr int kEpilogue = EPI == 1 ? BM * kPoolPitch : 0;
+    __shared__ __attribute__((aligned(16))) float lds[kStage > kEpilogue ? kStage : kEpilogue];
+    float *const xs = lds;
+    float *const ys = lds + BK * LX::LD;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -303,21 +322,74 @@ __global__ void __launch_bounds__(WM *WN * 64)
     // Accumulator layout of the 32x32 block: lane -> column l32; register v -> row
     // 8*(v/4) + 4*(lane/32) + (v%4).  The bias (one value per column) is added only when the
     // reduction is not split; split sums add it once at the end.
-    float *c = p.c + batch * p.c_batch + (int64_t)split * p.c_split;
-    const bool with_bias = p.bias != nullptr && p.splits == 1;
+    if constexpr (EPI == 0) {
+        float *c = p.c + batch * p.c_batch + (int64_t)split * p.c_split;
+        const bool with_bias = p.bias != nullptr && p.splits == 1;
 #pragma unroll
-    for (int a = 0; a < FM; ++a)
+        for (int a = 0; a < FM; ++a)
 #pragma unroll
-        for (int b = 0; b < FN; ++b) {
-            const int64_t col = j0 + wn * TN + b * 32 + l32;
-            if (col >= p.n) continue;
-            const float add = with_bias ? p.bias[col] : 0.0f;
+            for (int b = 0; b < FN; ++b) {
+                const int64_t col = j0 + wn * TN + b * 32 + l32;
+                if (col >= p.n) continue;
+                const float add = with_bias ? p.bias[col] : 0.0f;
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int64_t row = i0 + wm * TM + a * 32 + (v >> 2) * 8 + half * 4 + (v & 3);
-                if (row < p.m) c[row * p.n + col] = with_bias ? acc[a][b][v] + add : acc[a][b][v];
+                for (int v = 0; v < 16; ++v) {
+                    const int64_t row = i0 + wm * TM + a * 32 + (v >> 2) * 8 + half * 4 + (v & 3);
+                    if (row < p.m) c[row * p.n + col] = with_bias ? acc[a][b][v] + add : acc[a][b][v];
+                }
+            }
+    } else {
+        // The block's BM rows are whole rows of pooling windows (the host guarantees
+        // BM % (pool_h * pool_ow) == 0 and an exact tiling), so every window is complete here.
+        // One column half (the waves with wn == h) at a time goes through LDS as
+        // relu(acc + bias); then all threads reduce windows: first strictly greater finite value
+        // in window order (ky major, kx minor), winner 255 and NaN when no value qualifies.
+        const int kh = p.pool_h, kw = p.pool_w, ow = p.pool_ow;
+        const int pw = ow / kw;
+        const int windows = BM / (kh * kw);
+        const int64_t pooled_row0 = i0 / ow / kh;
+#pragma unroll
+        for (int h = 0; h < WN; ++h) {
+            __syncthreads();
+            if (wn == h) {
+#pragma unroll
+                for (int a = 0; a < FM; ++a)
+#pragma unroll
+                    for (int b = 0; b < FN; ++b) {
+                        const int cl = b * 32 + l32;
+                        const int64_t col = j0 + h * TN + cl;
+                        const bool with_bias = p.bias != nullptr && col < p.n;
+                        const float add = with_bias ? p.bias[col] : 0.0f;
+#pragma unroll
+                        for (int v = 0; v < 16; ++v) {
+                            const int rl = wm * TM + a * 32 + (v >> 2) * 8 + half * 4 + (v & 3);
+                            const float z = with_bias ? acc[a][b][v] + add : acc[a][b][v];
+                            lds[rl * kPoolPitch + cl] = z > 0.0f ? z : 0.0f;
+                        }
+                    }
+            }
+            __syncthreads();
+            for (int idx = tid; idx < windows * TN; idx += NT) {
+                const int cl = idx % TN, w = idx / TN;
+                const int wr = w / pw, px = w - wr * pw;
+                const int64_t col = j0 + h * TN + cl;
+                if (col >= p.n || i0 + (int64_t)wr * kh * ow >= p.m) continue;
+                float best = -INFINITY;
+                int winner = 255;
+                for (int ky = 0; ky < kh; ++ky)
+                    for (int kx = 0; kx < kw; ++kx) {
+                        const float v = lds[((wr * kh + ky) * ow + px * kw + kx) * kPoolPitch + cl];
+                        if (v >= -FLT_MAX && v <= FLT_MAX && v > best) {
+                            best = v;
+                            winner = ky * kw + kx;
+                        }
+                    }
+                const int64_t out = ((pooled_row0 + wr) * pw + px) * p.n + col;
+                p.pooled[out] = winner == 255 ? __builtin_nanf("") : best;
+                p.argmax[out] = (uint8_t)winner;
             }
         }
+    }
 }
 
 // Sum of reduction slices: lane group g (of 4) adds slices g, g+4, g+8, ... in order, then the
@@ -342,23 +414,38 @@ __global__ void __launch_bounds__(256) split_sum_kernel(const float *__restrict_
     }
 }
 
+// First level for many slices: mid[g][i] = sum of slices [g*span, (g+1)*span) in order.
+__global__ void __launch_bounds__(256) split_range_kernel(const float *__restrict__ partial,
+                                                          float *__restrict__ mid, int64_t len,
+                                                          int32_t splits, int32_t span) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= len) return;
+    const int32_t g = blockIdx.y;
+    const int32_t k1 = (g + 1) * span < splits ? (g + 1) * span : splits;
+    float s = 0.f;
+#pragma unroll 8
+    for (int32_t k = g * span; k < k1; ++k) s += partial[(int64_t)k * len + i];
+    mid[(int64_t)g * len + i] = s;
+}
+
 // Weight permutations between the reference's [(c, ky, kx), n] layout and the implicit-GEMM
-// orders.  mode 0: W'[(ky, kx, c), n] = W[(c, ky, kx), n]            (forward)
-//           mode 1: W''[(ky', kx', n), c] = W[(c, kh-1-ky', kw-1-kx'), n] (dgrad, flipped)
-//           mode 2: W[(c, ky, kx), n] = W'[(ky, kx, c), n]           (wgrad result back)
+// orders, with the channel axis padded to c_pad >= c_in (padding rows are zero).
+//   mode 0: W'[(ky, kx, c), n] = W[(c, ky, kx), n]                 (forward; rows c >= c_in are 0)
+//   mode 1: W''[(ky', kx', n), c] = W[(c, kh-1-ky', kw-1-kx'), n]   (dgrad, flipped; c_pad == c_in)
+//   mode 2: W[(c, ky, kx), n] = W'[(ky, kx, c), n]                 (wgrad result back; c < c_in)
 __global__ void __launch_bounds__(256) conv_weight_permute_kernel(const float *__restrict__ src,
                                                                   float *__restrict__ dst, int32_t c_in,
-                                                                  int32_t n_out, int32_t kh, int32_t kw,
-                                                                  int32_t mode) {
-    const int64_t total = (int64_t)c_in * kh * kw * n_out;
+                                                                  int32_t c_pad, int32_t n_out, int32_t kh,
+                                                                  int32_t kw, int32_t mode) {
+    const int64_t total = (int64_t)(mode == 0 ? c_pad : c_in) * kh * kw * n_out;
     for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total;
          idx += (int64_t)gridDim.x * 256) {
         if (mode == 0) {
             const int32_t n = (int32_t)(idx % n_out);
             const int64_t r = idx / n_out;
-            const int32_t c = (int32_t)(r % c_in);
-            const int32_t pos = (int32_t)(r / c_in);
-            dst[idx] = src[((int64_t)c * kh * kw + pos) * n_out + n];
+            const int32_t c = (int32_t)(r % c_pad);
+            const int32_t pos = (int32_t)(r / c_pad);
+            dst[idx] = c < c_in ? src[((int64_t)c * kh * kw + pos) * n_out + n] : 0.0f;
         } else if (mode == 1) {
             const int32_t c = (int32_t)(idx % c_in);
             const int64_t r = idx / c_in;
@@ -372,26 +459,55 @@ __global__ void __launch_bounds__(256) conv_weight_permute_kernel(const float *_
             const int64_t r = idx / n_out;
             const int32_t pos = (int32_t)(r % (kh * kw));
             const int32_t c = (int32_t)(r / (kh * kw));
-            dst[idx] = src[((int64_t)pos * c_in + c) * n_out + n];
+            dst[idx] = src[((int64_t)pos * c_pad + c) * n_out + n];
         }
     }
 }
 
-template <int BM, int BN, int BK, int WM, int WN, bool XR, bool YR, int VX, int VY, int XMODE>
-void launch_config(const GemmParams &p, dim3 grid, hipStream_t stream) {
-    gemm_kernel<BM, BN, BK, WM, WN, XR, YR, VX, VY, XMODE><<<grid, WM * WN * 64, 0, stream>>>(p);
+// Copies an input of any layout into channel-innermost [batch, height, width, c_pad] with the
+// channels past c_in zero, so every gathered vector is 16 contiguous bytes.  Consecutive lanes
+// take consecutive pixels, which keeps the reads of a channel-major source coalesced.
+__global__ void __launch_bounds__(256) repack_channels_last_kernel(const float *__restrict__ src,
+                                                                   int64_t ld_b, int64_t ld_c,
+                                                                   int64_t ld_h, int64_t ld_w,
+                                                                   float *__restrict__ dst, int64_t pixels,
+                                                                   int32_t height, int32_t width,
+                                                                   int32_t c_in, int32_t c_pad) {
+    const int32_t groups = c_pad / 4;
+    const int64_t total = pixels * groups;
+    for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < total; t += (int64_t)gridDim.x * 256) {
+        const int32_t g = (int32_t)(t / pixels);
+        const int64_t pix = t - (int64_t)g * pixels;
+        const int32_t x = (int32_t)(pix % width);
+        const int64_t rest = pix / width;
+        const int32_t y = (int32_t)(rest % height);
+        const int64_t b = rest / height;
+        const float *s0 = src + b * ld_b + (int64_t)y * ld_h + (int64_t)x * ld_w;
+        floatx4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int32_t c = g * 4 + e;
+            v[e] = c < c_in ? s0[(int64_t)c * ld_c] : 0.0f;
+        }
+        *reinterpret_cast<floatx4 *>(dst + pix * c_pad + g * 4) = v;
+    }
 }
 
-template <int BM, int BN, int BK, int WM, int WN, bool XR, bool YR, int XMODE>
+template <int BM, int BN, int BK, int WM, int WN, bool XR, bool YR, int VX, int VY, int XMODE, int EPI>
+void launch_config(const GemmParams &p, dim3 grid, hipStream_t stream) {
+    gemm_kernel<BM, BN, BK, WM, WN, XR, YR, VX, VY, XMODE, EPI><<<grid, WM * WN * 64, 0, stream>>>(p);
+}
+
+template <int BM, int BN, int BK, int WM, int WN, bool XR, bool YR, int XMODE, int EPI>
 void launch_vec(const GemmParams &p, dim3 grid, hipStream_t stream, bool vx, bool vy) {
     if (vx && vy)
-        launch_config<BM, BN, BK, WM, WN, XR, YR, 4, 4, XMODE>(p, grid, stream);
+        launch_config<BM, BN, BK, WM, WN, XR, YR, 4, 4, XMODE, EPI>(p, grid, stream);
     else if (vx)
-        launch_config<BM, BN, BK, WM, WN, XR, YR, 4, 1, XMODE>(p, grid, stream);
+        launch_config<BM, BN, BK, WM, WN, XR, YR, 4, 1, XMODE, EPI>(p, grid, stream);
     else if (vy)
-        launch_config<BM, BN, BK, WM, WN, XR, YR, 1, 4, XMODE>(p, grid, stream);
+        launch_config<BM, BN, BK, WM, WN, XR, YR, 1, 4, XMODE, EPI>(p, grid, stream);
     else
-        launch_config<BM, BN, BK, WM, WN, XR, YR, 1, 1, XMODE>(p, grid, stream);
+        launch_config<BM, BN, BK, WM, WN, XR, YR, 1, 1, XMODE, EPI>(p, grid, stream);
 }
 
 // Vector loads need the contiguous extent, the other stride and the base to be 4-aligned.
@@ -399,22 +515,60 @@ bool vec_ok(const float *base, int64_t contiguous_extent, int64_t other_stride) 
     return axis::aligned16(base) && contiguous_extent % 4 == 0 && other_stride % 4 == 0;
 }
 
-template <bool XR, bool YR, int XMODE>
+// Tile shapes, all 32 deep per LDS stage: large 128x128 when both output extents fill it; 128x64
+// when the columns are few (<= 64); 64x64 otherwise.  Resident blocks per CU follow from the
+// register budget of each shape.
+enum class Shape { Large, Tall, Small };
+
+struct Choice {
+    Shape shape;
+    int bm, bn, bk, per_cu;
+};
+
+Choice choose(int64_t m, int64_t n, bool pool_epilogue) {
+    if ((m >= 128 || pool_epilogue) && n >= 128) return {Shape::Large, 128, 128, 32, 2};
+    if (m >= 128 || pool_epilogue) {
+        if (n <= 64 || pool_epilogue) return {Shape::Tall, 128, 64, 32, 4};
+    }
+    return {Shape::Small, 64, 64, 32, 8};
+}
+
+// Deterministic sum of reduction slices (+ bias): up to 32 slices in one pass; beyond that, ranges
+// of 32 consecutive slices first, then the range sums -- a fixed association for a given count.
+int sum_splits(axis_device device, const float *partial, float *out, int64_t len, int64_t splits,
+               const float *bias, int64_t n) {
+    const unsigned blocks = axis::blocks_for(len, 64, INT32_MAX);
+    if (splits <= 32) {
+        split_sum_kernel<<<blocks, 256, 0, device->stream>>>(partial, out, len, (int32_t)splits, len, bias, n);
+        return axis::launch_status("split_sum_kernel");
+    }
+    const int32_t span = 32;
+    const int64_t ranges = (splits + span - 1) / span;
+    axis::Scratch mid;
+    if (int st = mid.get(device, sizeof(float) * (size_t)(ranges * len))) return st;
+    dim3 grid(axis::blocks_for(len, 256, INT32_MAX), (unsigned)ranges);
+    split_range_kernel<<<grid, 256, 0, device->stream>>>(partial, mid.as<float>(), len, (int32_t)splits, span);
+    if (int st = axis::launch_status("split_range_kernel")) return st;
+    split_sum_kernel<<<blocks, 256, 0, device->stream>>>(mid.as<float>(), out, len, (int32_t)ranges, len, bias, n);
+    return axis::launch_status("split_sum_kernel");
+}
+
+template <bool XR, bool YR, int XMODE, int EPI>
 int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out) {
     const int64_t cus = device->multiprocessors;
-    // Large tiles whenever both output extents fill them; a reduction split restores the block
-    // count when the output alone has too few tiles.  Large tiles run 32 deep per LDS stage.
-    const bool big = p.m >= 128 && p.n >= 128;
-    const int BK = big ? 32 : 16;
-    const int bm = big ? 128 : 64, bn = big ? 128 : 64;
-    p.tiles_m = static_cast<int32_t>((p.m + bm - 1) / bm);
-    p.tiles_n = static_cast<int32_t>((p.n + bn - 1) / bn);
+    const Choice ch = choose(p.m, p.n, EPI == 1);
+    const int BK = ch.bk;
+    p.tiles_m = static_cast<int32_t>((p.m + ch.bm - 1) / ch.bm);
+    p.tiles_n = static_cast<int32_t>((p.n + ch.bn - 1) / ch.bn);
     const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n * batch;
-    // Split the reduction when the tiles alone cannot fill the chip.
+    // Split the reduction when the tiles alone cannot fill the chip: aim at one full round of
+    // resident blocks so no round runs nearly empty.  The pooling epilogue needs whole sums.
+    // The partial slices stay within 64 MiB.
+    const int64_t slots = cus * ch.per_cu;
+    const int64_t out_len = batch * p.m * p.n;
     int64_t splits = 1;
-    if (tiles < 2 * cus && p.k >= 8 * BK) {
-        splits = std::min<int64_t>((4 * cus + tiles - 1) / tiles, 2 * cus);
-        splits = std::min<int64_t>(splits, p.k / (BK * 4));
+    if (EPI == 0 && tiles < slots && p.k >= 8 * BK) {
+        splits = std::min<int64_t>({slots / tiles, p.k / (BK * 4), (int64_t(16) << 20) / out_len});
         splits = std::max<int64_t>(splits, 1);
     }
     int64_t chunk = (p.k + splits - 1) / splits;
@@ -430,12 +584,12 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out) {
         vx = XR ? vec_ok(p.x, p.k, p.x_si) && p.x_batch % 4 == 0
                 : vec_ok(p.x, p.m, p.x_sr) && p.x_batch % 4 == 0;
     else
-        vx = axis::aligned16(p.conv.src) && p.conv.channels % 4 == 0;
+        vx = axis::aligned16(p.conv.src) && p.conv.channels % 4 == 0 && p.conv.ld_c == 1 &&
+             p.conv.ld_w % 4 == 0 && p.conv.ld_h % 4 == 0 && p.conv.ld_b % 4 == 0;
     const bool vy = YR ? vec_ok(p.y, p.k, p.y_sj) && p.y_batch % 4 == 0
                        : vec_ok(p.y, p.n, p.y_sr) && p.y_batch % 4 == 0;
 
     axis::Scratch partial;
-    const int64_t out_len = batch * p.m * p.n;
     if (splits > 1) {
         int status = partial.get(device, sizeof(float) * (size_t)(out_len * splits));
         if (status) return status;
@@ -449,19 +603,25 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out) {
     }
     if (batch * splits > 65535)
         return axis::fail(AXIS_ERROR_INVALID, "matmul batch too large for one launch");
-    axis::TimedLaunch timed(device, "gemm", 2.0 * (double)batch * (double)p.m * (double)p.n * (double)p.k);
+    const double k_work = (double)(p.k_work > 0 ? p.k_work : p.k);
+    axis::TimedLaunch timed(device, "gemm", 2.0 * (double)batch * (double)p.m * (double)p.n * k_work);
     dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n), static_cast<unsigned>(batch * splits));
-    if (big)
-        launch_vec<128, 128, 32, 2, 2, XR, YR, XMODE>(p, grid, device->stream, vx, vy);
-    else
-        launch_vec<64, 64, 16, 2, 2, XR, YR, XMODE>(p, grid, device->stream, vx, vy);
+    if constexpr (EPI == 1) {
+        if (ch.shape == Shape::Large)
+            launch_vec<128, 128, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, device->stream, vx, vy);
+        else
+            launch_vec<128, 64, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, device->stream, vx, vy);
+    } else {
+        if (ch.shape == Shape::Large)
+            launch_vec<128, 128, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, device->stream, vx, vy);
+        else if (ch.shape == Shape::Tall)
+            launch_vec<128, 64, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, device->stream, vx, vy);
+        else
+            launch_vec<64, 64, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, device->stream, vx, vy);
+    }
     int status = axis::launch_status("gemm_kernel");
     if (status) return status;
-    if (splits > 1) {
-        split_sum_kernel<<<axis::blocks_for(out_len, 64, INT32_MAX), 256, 0, device->stream>>>(
-            partial.as<float>(), out, out_len, static_cast<int32_t>(splits), out_len, p.bias, p.n);
-        status = axis::launch_status("split_sum_kernel");
-    }
+    if (splits > 1) status = sum_splits(device, partial.as<float>(), out, out_len, splits, p.bias, p.n);
     return status;
 }
 
@@ -514,10 +674,38 @@ int conv_shape(int64_t batch, int32_t height, int32_t width, int32_t channels, i
     return AXIS_OK;
 }
 
-ConvGeom geom(const float *src, int32_t height, int32_t width, int32_t channels, int32_t out_h,
-              int32_t out_w, int32_t kw, int32_t sy, int32_t sx, int32_t py, int32_t px) {
+// Strides of a channel-innermost contiguous [batch, height, width, channels] tensor.
+void channels_last(int32_t height, int32_t width, int32_t channels, int64_t ld[4]) {
+    ld[0] = (int64_t)height * width * channels;
+    ld[1] = 1;
+    ld[2] = (int64_t)width * channels;
+    ld[3] = channels;
+}
+
+// Validates caller strides {batch, channel, row, column} (null = channel-innermost contiguous).
+int input_strides(const int64_t *given, int64_t batch, int32_t height, int32_t width,
+                  int32_t channels, int64_t ld[4]) {
+    if (!given) {
+        channels_last(height, width, channels, ld);
+        return AXIS_OK;
+    }
+    for (int i = 0; i < 4; ++i) ld[i] = given[i];
+    AXIS_REQUIRE(ld[0] >= 0 && ld[1] >= 0 && ld[2] >= 0 && ld[3] >= 0, "input strides must be nonnegative");
+    AXIS_REQUIRE(ld[1] < INT32_MAX && ld[2] < INT32_MAX && ld[3] < INT32_MAX, "input stride too large");
+    const int64_t last = (batch - 1) * ld[0] + (int64_t)(channels - 1) * ld[1] +
+                         (int64_t)(height - 1) * ld[2] + (int64_t)(width - 1) * ld[3];
+    AXIS_REQUIRE(last < (int64_t(1) << 40), "input strides address too far");
+    return AXIS_OK;
+}
+
+ConvGeom geom(const float *src, const int64_t ld[4], int32_t height, int32_t width, int32_t channels,
+              int32_t out_h, int32_t out_w, int32_t kw, int32_t sy, int32_t sx, int32_t py, int32_t px) {
     ConvGeom g{};
     g.src = src;
+    g.ld_b = ld[0];
+    g.ld_c = (int32_t)ld[1];
+    g.ld_h = (int32_t)ld[2];
+    g.ld_w = (int32_t)ld[3];
     g.height = height;
     g.width = width;
     g.channels = channels;
@@ -535,12 +723,44 @@ ConvGeom geom(const float *src, int32_t height, int32_t width, int32_t channels,
     return g;
 }
 
-int permute_weight(axis_device device, const float *src, float *dst, const ConvShape &s, int mode) {
-    const int64_t total = (int64_t)s.channels * s.kh * s.kw * s.out_channels;
+int permute_weight(axis_device device, const float *src, float *dst, const ConvShape &s, int mode,
+                   int32_t c_pad) {
+    const int64_t total = (int64_t)(mode == 0 ? c_pad : s.channels) * s.kh * s.kw * s.out_channels;
     conv_weight_permute_kernel<<<axis::blocks_for(total, 256, 4096), 256, 0, device->stream>>>(
-        src, dst, s.channels, s.out_channels, s.kh, s.kw, mode);
+        src, dst, s.channels, c_pad, s.out_channels, s.kh, s.kw, mode);
     return axis::launch_status("conv_weight_permute_kernel");
 }
+
+// The gathered input of a forward or weight-gradient launch: the caller's tensor when it is
+// channel-innermost with a multiple of 4 channels on a 16-byte boundary, otherwise a repacked
+// channel-innermost copy with the channels padded to a multiple of 4.
+struct GatherInput {
+    axis::Scratch copy;
+    const float *src = nullptr;
+    int64_t ld[4];
+    int32_t channels = 0;  // channel extent the GEMM reduces over (padded)
+
+    int prepare(axis_device device, const float *input, const int64_t given[4], int64_t batch,
+                int32_t height, int32_t width, int32_t c_in) {
+        if (int st = input_strides(given, batch, height, width, c_in, ld)) return st;
+        if (ld[1] == 1 && c_in % 4 == 0 && ld[2] % 4 == 0 && ld[3] % 4 == 0 && ld[0] % 4 == 0 &&
+            axis::aligned16(input)) {
+            src = input;
+            channels = c_in;
+            return AXIS_OK;
+        }
+        channels = (c_in + 3) / 4 * 4;
+        const int64_t pixels = batch * height * width;
+        if (int st = copy.get(device, sizeof(float) * (size_t)(pixels * channels))) return st;
+        repack_channels_last_kernel<<<axis::blocks_for(pixels * (channels / 4), 256, 1 << 16), 256, 0,
+                                      device->stream>>>(input, ld[0], ld[1], ld[2], ld[3], copy.as<float>(),
+                                                        pixels, height, width, c_in, channels);
+        if (int st = axis::launch_status("repack_channels_last_kernel")) return st;
+        src = copy.as<float>();
+        channels_last(height, width, channels, ld);
+        return AXIS_OK;
+    }
+};
 
 }  // namespace
 
@@ -562,7 +782,7 @@ int axis_matmul(axis_device device, const float *a, const float *b, float *out, 
     p.y_sj = 1;
     p.x_batch = m * k;
     p.y_batch = k * n;
-    return run_gemm<true, false, 0>(device, p, batch, out);
+    return run_gemm<true, false, 0, 0>(device, p, batch, out);
 }
 
 int axis_matmul_left_backward(axis_device device, const float *gradient, const float *rhs,
@@ -582,7 +802,7 @@ int axis_matmul_left_backward(axis_device device, const float *gradient, const f
     p.y_sj = n;
     p.x_batch = m * n;
     p.y_batch = k * n;
-    return run_gemm<true, true, 0>(device, p, batch, out);
+    return run_gemm<true, true, 0, 0>(device, p, batch, out);
 }
 
 int axis_matmul_right_backward(axis_device device, const float *lhs, const float *gradient,
@@ -602,33 +822,79 @@ int axis_matmul_right_backward(axis_device device, const float *lhs, const float
     p.y_sj = 1;
     p.x_batch = m * k;
     p.y_batch = m * n;
-    return run_gemm<false, false, 0>(device, p, batch, out);
+    return run_gemm<false, false, 0, 0>(device, p, batch, out);
 }
 
-int axis_conv2d_forward(axis_device device, const float *input, const float *weight,
-                        const float *bias, float *out, int64_t batch, int32_t height, int32_t width,
-                        int32_t channels, int32_t out_channels, const int32_t kernel[2],
-                        const int32_t stride[2], const int32_t padding[2]) {
+int axis_conv2d_forward(axis_device device, const float *input, const int64_t input_strides_[4],
+                        const float *weight, const float *bias, float *out, int64_t batch,
+                        int32_t height, int32_t width, int32_t channels, int32_t out_channels,
+                        const int32_t kernel[2], const int32_t stride[2], const int32_t padding[2]) {
     AXIS_ENTER(device);
     AXIS_REQUIRE(input && weight && out, "null convolution buffer");
     ConvShape s{};
     if (int st = conv_shape(batch, height, width, channels, out_channels, kernel, stride, padding, &s))
         return st;
-    const int64_t patch = (int64_t)channels * s.kh * s.kw;
+    GatherInput in;
+    if (int st = in.prepare(device, input, input_strides_, batch, height, width, channels)) return st;
+    const int64_t patch = (int64_t)in.channels * s.kh * s.kw;
     axis::Scratch permuted;
     if (int st = permuted.get(device, sizeof(float) * (size_t)(patch * out_channels))) return st;
-    if (int st = permute_weight(device, weight, permuted.as<float>(), s, 0)) return st;
+    if (int st = permute_weight(device, weight, permuted.as<float>(), s, 0, in.channels)) return st;
     GemmParams p{};
-    p.x = input;
     p.y = permuted.as<float>();
     p.bias = bias;
     p.m = batch * s.out_h * s.out_w;
     p.n = out_channels;
     p.k = patch;
+    p.k_work = (int64_t)channels * s.kh * s.kw;
     p.y_sr = out_channels;
     p.y_sj = 1;
-    p.conv = geom(input, height, width, channels, s.out_h, s.out_w, s.kw, s.sy, s.sx, s.py, s.px);
-    return run_gemm<true, false, 1>(device, p, 1, out);
+    p.conv = geom(in.src, in.ld, height, width, in.channels, s.out_h, s.out_w, s.kw, s.sy, s.sx, s.py, s.px);
+    return run_gemm<true, false, 1, 0>(device, p, 1, out);
+}
+
+int axis_conv2d_relu_pool_forward(axis_device device, const float *input,
+                                  const int64_t input_strides_[4], const float *weight,
+                                  const float *bias, float *pooled, uint8_t *argmax, int64_t batch,
+                                  int32_t height, int32_t width, int32_t channels,
+                                  int32_t out_channels, const int32_t kernel[2],
+                                  const int32_t stride[2], const int32_t padding[2],
+                                  const int32_t pool[2]) {
+    AXIS_ENTER(device);
+    AXIS_REQUIRE(input && weight && pooled && argmax && pool, "null convolution buffer");
+    ConvShape s{};
+    if (int st = conv_shape(batch, height, width, channels, out_channels, kernel, stride, padding, &s))
+        return st;
+    int64_t ld_check[4];
+    if (int st = input_strides(input_strides_, batch, height, width, channels, ld_check)) return st;
+    AXIS_REQUIRE(pool[0] >= 1 && pool[1] >= 1 && pool[0] * pool[1] < 255,
+                 "pool window must be positive with fewer than 255 positions");
+    AXIS_REQUIRE(s.out_h % pool[0] == 0 && s.out_w % pool[1] == 0,
+                 "fused pooling needs windows that tile the convolution output exactly");
+    AXIS_REQUIRE(128 % (pool[0] * s.out_w) == 0,
+                 "fused pooling needs pool height x output width to divide 128");
+    GatherInput in;
+    if (int st = in.prepare(device, input, input_strides_, batch, height, width, channels)) return st;
+    const int64_t patch = (int64_t)in.channels * s.kh * s.kw;
+    axis::Scratch permuted;
+    if (int st = permuted.get(device, sizeof(float) * (size_t)(patch * out_channels))) return st;
+    if (int st = permute_weight(device, weight, permuted.as<float>(), s, 0, in.channels)) return st;
+    GemmParams p{};
+    p.y = permuted.as<float>();
+    p.bias = bias;
+    p.m = batch * s.out_h * s.out_w;
+    p.n = out_channels;
+    p.k = patch;
+    p.k_work = (int64_t)channels * s.kh * s.kw;
+    p.y_sr = out_channels;
+    p.y_sj = 1;
+    p.conv = geom(in.src, in.ld, height, width, in.channels, s.out_h, s.out_w, s.kw, s.sy, s.sx, s.py, s.px);
+    p.pooled = pooled;
+    p.argmax = argmax;
+    p.pool_h = pool[0];
+    p.pool_w = pool[1];
+    p.pool_ow = s.out_w;
+    return run_gemm<true, false, 1, 1>(device, p, 1, nullptr);
 }
 
 int axis_conv2d_backward_data(axis_device device, const float *gradient, const float *weight,
@@ -645,7 +911,7 @@ int axis_conv2d_backward_data(axis_device device, const float *gradient, const f
     const int64_t patch = (int64_t)channels * s.kh * s.kw;
     axis::Scratch flipped;
     if (int st = flipped.get(device, sizeof(float) * (size_t)(patch * out_channels))) return st;
-    if (int st = permute_weight(device, weight, flipped.as<float>(), s, 1)) return st;
+    if (int st = permute_weight(device, weight, flipped.as<float>(), s, 1, channels)) return st;
     // d_input[b, y, x, c] = sum over (ky', kx', n) of gradient[b, y + ky' - (kh-1-py),
     // x + kx' - (kw-1-px), n] * W[(c, kh-1-ky', kw-1-kx'), n]: a stride-1 convolution of the
     // output gradient with the flipped, transposed kernel -- the reference's col2im of
@@ -658,12 +924,15 @@ int axis_conv2d_backward_data(axis_device device, const float *gradient, const f
     p.k = (int64_t)s.kh * s.kw * out_channels;
     p.y_sr = channels;
     p.y_sj = 1;
-    p.conv = geom(gradient, s.out_h, s.out_w, out_channels, height, width, s.kw, 1, 1, s.kh - 1 - s.py,
-                  s.kw - 1 - s.px);
-    return run_gemm<true, false, 1>(device, p, 1, d_input);
+    int64_t ld[4];
+    channels_last(s.out_h, s.out_w, out_channels, ld);
+    p.conv = geom(gradient, ld, s.out_h, s.out_w, out_channels, height, width, s.kw, 1, 1,
+                  s.kh - 1 - s.py, s.kw - 1 - s.px);
+    return run_gemm<true, false, 1, 0>(device, p, 1, d_input);
 }
 
-int axis_conv2d_backward_weight(axis_device device, const float *input, const float *gradient,
+int axis_conv2d_backward_weight(axis_device device, const float *input,
+                                const int64_t input_strides_[4], const float *gradient,
                                 float *d_weight, int64_t batch, int32_t height, int32_t width,
                                 int32_t channels, int32_t out_channels, const int32_t kernel[2],
                                 const int32_t stride[2], const int32_t padding[2]) {
@@ -672,20 +941,23 @@ int axis_conv2d_backward_weight(axis_device device, const float *input, const fl
     ConvShape s{};
     if (int st = conv_shape(batch, height, width, channels, out_channels, kernel, stride, padding, &s))
         return st;
-    const int64_t patch = (int64_t)channels * s.kh * s.kw;
+    GatherInput in;
+    if (int st = in.prepare(device, input, input_strides_, batch, height, width, channels)) return st;
+    const int64_t patch = (int64_t)in.channels * s.kh * s.kw;
     axis::Scratch ordered;
     if (int st = ordered.get(device, sizeof(float) * (size_t)(patch * out_channels))) return st;
     GemmParams p{};
-    p.x = input;
     p.y = gradient;
     p.m = patch;
     p.n = out_channels;
     p.k = batch * (int64_t)s.out_h * s.out_w;
+    // rows past the real channels are padding: time the algorithmic 2 * patch * n * pixels
+    p.k_work = (int64_t)((double)p.k * (double)channels / (double)in.channels);
     p.y_sr = out_channels;
     p.y_sj = 1;
-    p.conv = geom(input, height, width, channels, s.out_h, s.out_w, s.kw, s.sy, s.sx, s.py, s.px);
-    if (int st = run_gemm<false, false, 2>(device, p, 1, ordered.as<float>())) return st;
-    return permute_weight(device, ordered.as<float>(), d_weight, s, 2);
+    p.conv = geom(in.src, in.ld, height, width, in.channels, s.out_h, s.out_w, s.kw, s.sy, s.sx, s.py, s.px);
+    if (int st = run_gemm<false, false, 2, 0>(device, p, 1, ordered.as<float>())) return st;
+    return permute_weight(device, ordered.as<float>(), d_weight, s, 2, in.channels);
 }
 
 }  // extern "C"

@@ -108,6 +108,11 @@ struct ConvGeometry {
     int64_t batch = 0;
     int32_t height = 0, width = 0, channels = 0, out_channels = 0;
     int32_t kernel[2] = {1, 1}, stride[2] = {1, 1}, padding[2] = {0, 0};
+    // Element strides {batch, channel, row, column} of the input when it is not channel-innermost
+    // contiguous.
+    bool strided = false;
+    int64_t input_strides[4] = {0, 0, 0, 0};
+    const int64_t *strides() const { return strided ? input_strides : nullptr; }
 };
 
 // Device (runtime/backend.rs:116-392): one GPU, one stream, out-of-place ops returning fresh
@@ -181,6 +186,7 @@ struct Rule {
         MaxPool,
         ConvData,    // input gradient of an implicit-GEMM convolution (a = weight)
         ConvWeight,  // weight gradient of an implicit-GEMM convolution (a = input)
+        ReluPool,    // ReLU then non-overlapping max pool (a = argmax bytes, b = pooled values)
     } kind = Identity;
     float factor = 1.0f;
     Buffer a, b;  // saved operands (rhs / lhs / probability / input / winners / argmax)
@@ -352,7 +358,13 @@ class Conv2d : public Module {
     Shape output_shape(const Shape &in) override;
     Shape build(const Shape &in, const Device &device, uint64_t seed) override;
     Tensor forward(const Tensor &x) override;
+    // Conv2d -> ReLU -> pool as one launch when the geometry allows it (Sequential uses this).
+    std::optional<Tensor> forward_relu_pool(const Tensor &x, const class MaxPool2d &pool);
     std::vector<std::pair<std::string, Parameter>> named_parameters() override;
+
+  private:
+    bool implicit_geometry(const Tensor &x, ConvGeometry &q) const;
+    std::vector<Edge> implicit_edges(const Tensor &x, const ConvGeometry &q, int64_t out_len) const;
 };
 
 class MaxPool2d : public Module {

@@ -192,58 +192,98 @@ Shape Conv2d::build(const Shape &in, const Device &device, uint64_t seed) {
     return shape;
 }
 
-Tensor Conv2d::forward(const Tensor &x) {
-    Shape out_shape = output_shape(x.shape());
-    if (!bound) raise("Conv2d must be built before forward");
-    // A one-group, stride-1 convolution of a contiguous [.., height, width, channels] input runs
-    // as implicit GEMM (no patch matrix) with the bias added in the epilogue; its rules are the
-    // derivatives of exactly that composition.  Every other geometry takes the reference's
-    // unfold -> contract -> merge -> add lowering below.
+// Geometry of an implicit-GEMM launch for x (one group), or false when x needs the reference's
+// explicit lowering.  A channel-innermost contiguous [.., height, width, channels] input takes
+// every rule (stride 1 and padding < kernel when x needs its gradient, which the data-gradient
+// kernel writes channel-innermost); any other rank-4 layout, e.g. channel-major, is gathered
+// through its strides and is accepted only when x needs no gradient.
+bool Conv2d::implicit_geometry(const Tensor &x, ConvGeometry &q) const {
+    if (groups != 1) return false;
     const Shape &in = x.shape();
     const size_t r = in.rank();
-    const bool channels_last = r >= 3 && x.is_contiguous() && in.dims[r - 1].axis == input &&
+    if (r < 3 || in.len >= (int64_t(1) << 31)) return false;
+    const bool channels_last = x.is_contiguous() && in.dims[r - 1].axis == input &&
                                in.dims[r - 3].axis == spatial[0] && in.dims[r - 2].axis == spatial[1];
-    if (groups == 1 && channels_last && stride[0] == 1 && stride[1] == 1 &&
-        padding[0] <= kernel[0] - 1 && padding[1] <= kernel[1] - 1 && in.len < (int64_t(1) << 31) &&
-        out_shape.len < (int64_t(1) << 31)) {
-        ConvGeometry q;
+    q = ConvGeometry{};
+    for (int i = 0; i < 2; ++i) {
+        q.kernel[i] = (int32_t)kernel[i];
+        q.stride[i] = (int32_t)stride[i];
+        q.padding[i] = (int32_t)padding[i];
+    }
+    q.out_channels = (int32_t)output.extent;
+    if (channels_last) {
         q.channels = (int32_t)in.dims[r - 1].extent;
         q.height = (int32_t)in.dims[r - 3].extent;
         q.width = (int32_t)in.dims[r - 2].extent;
         q.batch = in.len / ((int64_t)q.channels * q.height * q.width);
-        q.out_channels = (int32_t)output.extent;
-        for (int i = 0; i < 2; ++i) {
-            q.kernel[i] = (int32_t)kernel[i];
-            q.stride[i] = (int32_t)stride[i];
-            q.padding[i] = (int32_t)padding[i];
-        }
+        if (!x.requires_grad()) return true;
+        return stride[0] == 1 && stride[1] == 1 && padding[0] <= kernel[0] - 1 && padding[1] <= kernel[1] - 1;
+    }
+    if (r != 4 || x.requires_grad()) return false;
+    int ci = -1, hi = -1, wi = -1, bi = -1;
+    for (int i = 0; i < 4; ++i) {
+        const Axis &a = in.dims[i].axis;
+        if (a == input) ci = i;
+        else if (a == spatial[0]) hi = i;
+        else if (a == spatial[1]) wi = i;
+        else bi = i;
+    }
+    if (ci < 0 || hi < 0 || wi < 0 || bi < 0) return false;
+    const std::vector<int64_t> &st = x.layout().strides;
+    q.batch = in.dims[bi].extent;
+    q.channels = (int32_t)in.dims[ci].extent;
+    q.height = (int32_t)in.dims[hi].extent;
+    q.width = (int32_t)in.dims[wi].extent;
+    q.strided = true;
+    q.input_strides[0] = st[bi];
+    q.input_strides[1] = st[ci];
+    q.input_strides[2] = st[hi];
+    q.input_strides[3] = st[wi];
+    return true;
+}
+
+// Rules of the implicit convolution: data and weight gradients through the implicit-GEMM
+// kernels, bias gradient as the column sum of the output gradient.
+std::vector<Edge> Conv2d::implicit_edges(const Tensor &x, const ConvGeometry &q, int64_t out_len) const {
+    std::vector<Edge> edges;
+    Rule data;
+    data.kind = Rule::ConvData;
+    data.a = bound->weight.tensor().value();
+    data.conv = q;
+    edges.push_back(Edge{x, data});
+    Rule weight_rule;
+    weight_rule.kind = Rule::ConvWeight;
+    weight_rule.a = x.value();
+    weight_rule.conv = q;
+    edges.push_back(Edge{bound->weight.tensor(), weight_rule});
+    if (bound->bias) {
+        Rule rb;
+        rb.kind = Rule::BiasBroadcast;
+        rb.outer = out_len / output.extent;
+        rb.inner = output.extent;
+        edges.push_back(Edge{bound->bias->tensor(), rb});
+    }
+    return edges;
+}
+
+Tensor Conv2d::forward(const Tensor &x) {
+    Shape out_shape = output_shape(x.shape());
+    if (!bound) raise("Conv2d must be built before forward");
+    // The implicit-GEMM path adds the bias in the epilogue; its rules are the derivatives of
+    // exactly that composition.  Every other geometry takes the reference's unfold -> contract ->
+    // merge -> add lowering below.
+    ConvGeometry q;
+    if (out_shape.len < (int64_t(1) << 31) && implicit_geometry(x, q)) {
         const Device &dev = x.device();
         Tensor w = bound->weight.tensor();
         Buffer out = dev.alloc(out_shape.len);
         const float *bias_ptr = bound->bias ? bound->bias->tensor().value()->f32() : nullptr;
-        check(axis_conv2d_forward(dev.h(), x.value()->f32(), w.value()->f32(), bias_ptr, out->f32(),
-                                  q.batch, q.height, q.width, q.channels, q.out_channels, q.kernel,
-                                  q.stride, q.padding),
+        check(axis_conv2d_forward(dev.h(), x.value()->f32(), q.strides(), w.value()->f32(), bias_ptr,
+                                  out->f32(), q.batch, q.height, q.width, q.channels, q.out_channels,
+                                  q.kernel, q.stride, q.padding),
               "conv2d_forward");
-        std::vector<Edge> edges;
-        Rule data;
-        data.kind = Rule::ConvData;
-        data.a = w.value();
-        data.conv = q;
-        edges.push_back(Edge{x, data});
-        Rule weight_rule;
-        weight_rule.kind = Rule::ConvWeight;
-        weight_rule.a = x.value();
-        weight_rule.conv = q;
-        edges.push_back(Edge{w, weight_rule});
-        if (bound->bias) {
-            Rule rb;
-            rb.kind = Rule::BiasBroadcast;
-            rb.outer = out_shape.len / output.extent;
-            rb.inner = output.extent;
-            edges.push_back(Edge{bound->bias->tensor(), rb});
-        }
-        return Tensor::node(out_shape, Layout::contiguous(out_shape), out, dev, std::move(edges), false);
+        return Tensor::node(out_shape, Layout::contiguous(out_shape), out, dev,
+                            implicit_edges(x, q, out_shape.len), false);
     }
     Tensor projected = x.unfold_grouped(input, spatial, Dim{group, groups}, Dim{patch, bound->patch},
                                         kernel, stride, padding, 0.0f)
@@ -251,6 +291,54 @@ Tensor Conv2d::forward(const Tensor &x) {
                            .merge({group, output_in_group}, output_role);
     if (bound->bias) projected = projected.add(bound->bias->tensor());
     return projected.rename(output_role, output.axis);
+}
+
+// Conv2d -> ReLU -> MaxPool2d in one launch: the GEMM epilogue adds the bias, applies ReLU and
+// pools whole windows, so the pre-activation is never stored.  The graph gets an internal
+// pre-activation node (no value) carrying the convolution's rules and the pooled node with a
+// ReluPool rule; backward scatters the pooled gradient through the winners and the ReLU mask in
+// one pass.  Returns nothing when the shapes need the separate modules.
+std::optional<Tensor> Conv2d::forward_relu_pool(const Tensor &x, const MaxPool2d &pool) {
+    if (!bound) raise("Conv2d must be built before forward");
+    Shape conv_shape = output_shape(x.shape());
+    const size_t r = conv_shape.rank();
+    if (pool.channels != output.axis || pool.spatial.size() != 2 || pool.spatial[0] != spatial[0] ||
+        pool.spatial[1] != spatial[1] || r < 3 || conv_shape.dims[r - 1].axis != output.axis ||
+        conv_shape.dims[r - 3].axis != spatial[0] || conv_shape.dims[r - 2].axis != spatial[1])
+        return std::nullopt;
+    for (int i = 0; i < 2; ++i)
+        if (pool.stride[i] != pool.kernel[i] || pool.padding[i] != 0 || pool.kernel[i] < 1)
+            return std::nullopt;
+    const int64_t oh = conv_shape.dims[r - 3].extent, ow = conv_shape.dims[r - 2].extent;
+    const int64_t kh = pool.kernel[0], kw = pool.kernel[1];
+    if (kh * kw >= 255 || oh % kh || ow % kw || 128 % (kh * ow) || conv_shape.len >= (int64_t(1) << 31))
+        return std::nullopt;
+    ConvGeometry q;
+    if (!implicit_geometry(x, q)) return std::nullopt;
+    Shape pooled_shape = const_cast<MaxPool2d &>(pool).output_shape(conv_shape);
+    const Device &dev = x.device();
+    Buffer pooled = dev.alloc(pooled_shape.len);
+    Buffer argmax = dev.alloc_bytes(pooled_shape.len);
+    const float *bias_ptr = bound->bias ? bound->bias->tensor().value()->f32() : nullptr;
+    const int32_t window[2] = {(int32_t)kh, (int32_t)kw};
+    check(axis_conv2d_relu_pool_forward(dev.h(), x.value()->f32(), q.strides(),
+                                        bound->weight.tensor().value()->f32(), bias_ptr, pooled->f32(),
+                                        static_cast<uint8_t *>(argmax->ptr), q.batch, q.height, q.width,
+                                        q.channels, q.out_channels, q.kernel, q.stride, q.padding, window),
+          "conv2d_relu_pool_forward");
+    Tensor pre = Tensor::node(conv_shape, Layout::contiguous(conv_shape), nullptr, dev,
+                              implicit_edges(x, q, conv_shape.len), false);
+    Rule rp;
+    rp.kind = Rule::ReluPool;
+    rp.a = argmax;
+    rp.b = pooled;
+    rp.pool.outer = conv_shape.len / (oh * ow * output.extent);
+    rp.pool.height = (int32_t)oh;
+    rp.pool.width = (int32_t)ow;
+    rp.pool.channels = output.extent;
+    rp.pool.kernel[0] = rp.pool.stride[0] = (int32_t)kh;
+    rp.pool.kernel[1] = rp.pool.stride[1] = (int32_t)kw;
+    return Tensor::node(pooled_shape, Layout::contiguous(pooled_shape), pooled, dev, {Edge{pre, rp}}, false);
 }
 
 std::vector<std::pair<std::string, Parameter>> Conv2d::named_parameters() {
@@ -326,7 +414,22 @@ Shape Sequential::build(const Shape &in, const Device &device, uint64_t seed) {
 Tensor Sequential::forward(const Tensor &x) {
     output_shape(x.shape());
     Tensor v = x;
-    for (auto &l : layers) v = l->forward(v);
+    for (size_t i = 0; i < layers.size(); ++i) {
+        // Conv2d -> ReLU -> MaxPool2d runs as one fused launch when its geometry allows.
+        if (i + 2 < layers.size()) {
+            auto conv = std::dynamic_pointer_cast<Conv2d>(layers[i]);
+            auto relu = std::dynamic_pointer_cast<ReLU>(layers[i + 1]);
+            auto pool = std::dynamic_pointer_cast<MaxPool2d>(layers[i + 2]);
+            if (conv && relu && pool) {
+                if (auto fused = conv->forward_relu_pool(v, *pool)) {
+                    v = *fused;
+                    i += 2;
+                    continue;
+                }
+            }
+        }
+        v = layers[i]->forward(v);
+    }
     return v;
 }
 

@@ -959,10 +959,35 @@ void Tensor::backward() const {
                 case Rule::ConvWeight: {
                     const ConvGeometry &q = r.conv;
                     c = dev.alloc((int64_t)q.channels * q.kernel[0] * q.kernel[1] * q.out_channels);
-                    check(axis_conv2d_backward_weight(dev.h(), r.a->f32(), g->f32(), c->f32(), q.batch,
+                    check(axis_conv2d_backward_weight(dev.h(), r.a->f32(), q.strides(), g->f32(), c->f32(), q.batch,
                                                       q.height, q.width, q.channels, q.out_channels,
                                                       q.kernel, q.stride, q.padding),
                           "conv2d_backward_weight");
+                    break;
+                }
+                case Rule::ReluPool: {
+                    // The pre-activation node's bias gradient comes out of the same pass when that
+                    // node has exactly one BiasBroadcast edge and no other reader.
+                    const PoolGeometry &p = r.pool;
+                    c = dev.alloc(p.outer * p.height * p.width * p.channels);
+                    const std::shared_ptr<Node> &x = e.input.n;
+                    const Rule *bias_rule = nullptr;
+                    if (uses[x->id] == 1 && x->edges) {
+                        int biases = 0;
+                        for (auto &xe : *x->edges)
+                            if (xe.rule.kind == Rule::BiasBroadcast) bias_rule = &xe.rule, ++biases;
+                        if (biases != 1) bias_rule = nullptr;
+                    }
+                    Buffer db;
+                    if (bias_rule && bias_rule->inner == p.channels &&
+                        bias_rule->outer == p.outer * p.height * p.width)
+                        db = dev.alloc(p.channels);
+                    check(axis_relu_pool_backward(dev.h(), g->f32(), r.b->f32(),
+                                                  static_cast<const uint8_t *>(r.a->ptr), c->f32(),
+                                                  db ? db->f32() : nullptr, p.outer, p.height, p.width,
+                                                  (int32_t)p.channels, p.kernel),
+                          "relu_pool_backward");
+                    if (db) fused_bias[x->id] = db;
                     break;
                 }
                 case Rule::MaxPool: {

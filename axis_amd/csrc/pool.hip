@@ -11,6 +11,7 @@
 // input receives exactly one term, written as 0.0f + g like the sum the reference starts at +0.0.
 #include <cfloat>
 
+#include "column_sum.hpp"
 #include "common.hpp"
 #include "fastdiv.hpp"
 
@@ -128,6 +129,85 @@ __global__ void __launch_bounds__(256) max_pool2d_backward_tiled_kernel(
             store_vec<VEC>(base + ((int64_t)iy * a.width + ix) * a.channels, r);
         }
     }
+}
+
+// ReLU -> non-overlapping max pool, backward in one scatter: the winner of each window receives
+// 0.0f + g when the pooled value (the ReLU output at the winner) is positive; every other input
+// position receives 0 -- the pool's scatter followed by the ReLU mask, element for element.
+template <int VEC>
+__global__ void __launch_bounds__(256) relu_pool_backward_kernel(
+    const float *__restrict__ gradient, const float *__restrict__ pooled,
+    const uint8_t *__restrict__ argmax, float *__restrict__ out, PoolArgs a) {
+    const uint32_t t = blockIdx.x * 256u + threadIdx.x;
+    if (t >= a.total) return;
+    const uint32_t cv = a.cvec.mod(t);
+    uint32_t rest = a.cvec.div(t);
+    const int32_t ox = (int32_t)a.ow.mod(rest);
+    rest = a.ow.div(rest);
+    const int32_t oy = (int32_t)a.oh.mod(rest);
+    const uint32_t o = a.oh.div(rest);
+    const int32_t c = (int32_t)cv * VEC;
+    float g[VEC], y[VEC];
+    int w[VEC];
+    load_vec<VEC>(gradient + (int64_t)t * VEC, g);
+    load_vec<VEC>(pooled + (int64_t)t * VEC, y);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) w[e] = y[e] > 0.0f ? (int)argmax[(int64_t)t * VEC + e] : -1;
+    float *base = out + (int64_t)o * a.height * a.width * a.channels + c;
+    for (int32_t ky = 0; ky < a.ky; ++ky) {
+        const int32_t iy = oy * a.ky + ky;
+        for (int32_t kx = 0; kx < a.kx; ++kx) {
+            const int32_t ix = ox * a.kx + kx;
+            const int k = ky * a.kx + kx;
+            float r[VEC];
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) r[e] = w[e] == k ? 0.0f + g[e] : 0.0f;
+            store_vec<VEC>(base + ((int64_t)iy * a.width + ix) * a.channels, r);
+        }
+    }
+}
+
+// Bias-gradient chunks of the same d_pre without reading it: partial[q][c] sums rows
+// [512q, 512q + 512) of the [outer*height*width, channels] view in row order, where a row holds
+// 0.0f + g exactly at its window's positive winner and +0.0 elsewhere -- the values the scatter
+// writes, added in the plain column sum's order.  Each row's window is read unconditionally (the
+// window tensors are a quarter of d_pre and stay in cache) so the loads of consecutive rows are
+// independent and overlap.
+__global__ void __launch_bounds__(256) relu_pool_bias_chunk_kernel(
+    const float *__restrict__ gradient, const float *__restrict__ pooled,
+    const uint8_t *__restrict__ argmax, float *__restrict__ partial, int64_t rows, int64_t pairs,
+    PoolArgs a) {
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= pairs) return;
+    const int64_t q = t / a.channels;
+    const int32_t c = (int32_t)(t - q * a.channels);
+    const int64_t r0 = q * axis::kGroupedChunk;
+    const int32_t count = (int32_t)(r0 + axis::kGroupedChunk < rows ? axis::kGroupedChunk : rows - r0);
+    int32_t x = (int32_t)(r0 % a.width);
+    int64_t rest = r0 / a.width;
+    int32_t y = (int32_t)(rest % a.height);
+    int64_t o = rest / a.height;
+    int32_t py = y / a.ky, ky = y - py * a.ky;
+    int32_t px = x / a.kx, kx = x - px * a.kx;
+    // window offset of the current row (in elements of the pooled tensors) and its position code
+    int64_t wbase = ((o * a.out_h + py) * a.out_w) * a.channels + c;
+    float sum = 0.0f;
+#pragma unroll 8
+    for (int32_t i = 0; i < count; ++i) {
+        const int64_t w = wbase + (int64_t)px * a.channels;
+        const int k = ky * a.kx + kx;
+        const uint8_t win = argmax[w];
+        const float v = pooled[w];
+        const float g = gradient[w];
+        sum = sum + ((win == k && v > 0.0f) ? 0.0f + g : 0.0f);
+        if (++kx == a.kx) kx = 0, ++px;
+        if (++x == a.width) {
+            x = 0, px = 0, kx = 0;
+            if (++ky == a.ky) ky = 0, wbase += (int64_t)a.out_w * a.channels;
+            if (++y == a.height) y = 0;
+        }
+    }
+    partial[q * a.channels + c] = sum;
 }
 
 // General windows: one lane per input vector gathers the windows it won, ky major, kx minor.
@@ -262,6 +342,42 @@ int axis_max_pool2d_backward(axis_device device, const float *gradient, const ui
         max_pool2d_backward_kernel<1><<<axis::blocks_for(a.total, 256, INT32_MAX), 256, 0,
                                         device->stream>>>(gradient, argmax, out, a);
     return axis::launch_status("max_pool2d_backward_kernel");
+}
+
+int axis_relu_pool_backward(axis_device device, const float *gradient, const float *pooled,
+                            const uint8_t *argmax, float *d_pre, float *d_bias, int64_t outer,
+                            int32_t height, int32_t width, int32_t channels, const int32_t pool[2]) {
+    AXIS_ENTER(device);
+    AXIS_REQUIRE(gradient && pooled && argmax && d_pre && pool, "null relu_pool_backward buffer");
+    const int32_t zero[2] = {0, 0};
+    PoolArgs a{};
+    if (int s = pool_args(outer, height, width, channels, pool, pool, zero, &a)) return s;
+    AXIS_REQUIRE(height % pool[0] == 0 && width % pool[1] == 0,
+                 "relu_pool_backward needs windows that tile the input exactly");
+    const bool vec = channels % 4 == 0 && axis::aligned16(gradient) && axis::aligned16(pooled) &&
+                     axis::aligned16(d_pre) && (reinterpret_cast<uintptr_t>(argmax) & 3u) == 0;
+    const int v = vec ? 4 : 1;
+    a.cvec = FastDiv((uint32_t)(channels / v));
+    a.total = (uint32_t)(outer * a.out_h * a.out_w * (channels / v));
+    if (vec)
+        relu_pool_backward_kernel<4><<<axis::blocks_for(a.total, 256, INT32_MAX), 256, 0, device->stream>>>(
+            gradient, pooled, argmax, d_pre, a);
+    else
+        relu_pool_backward_kernel<1><<<axis::blocks_for(a.total, 256, INT32_MAX), 256, 0, device->stream>>>(
+            gradient, pooled, argmax, d_pre, a);
+    if (int s = axis::launch_status("relu_pool_backward_kernel")) return s;
+    if (!d_bias) return AXIS_OK;
+    const int64_t rows = outer * height * width;
+    const int64_t chunks = (rows + axis::kGroupedChunk - 1) / axis::kGroupedChunk;
+    const int64_t pairs = chunks * channels;
+    axis::Scratch partial;
+    if (int s = partial.get(device, sizeof(float) * (size_t)pairs)) return s;
+    relu_pool_bias_chunk_kernel<<<axis::blocks_for(pairs, 256, INT32_MAX), 256, 0, device->stream>>>(
+        gradient, pooled, argmax, partial.as<float>(), rows, pairs, a);
+    if (int s = axis::launch_status("relu_pool_bias_chunk_kernel")) return s;
+    axis::column_combine_kernel<<<(unsigned)channels, 256, 0, device->stream>>>(partial.as<float>(), chunks,
+                                                                              channels, 1.0f, d_bias);
+    return axis::launch_status("column_combine_kernel");
 }
 
 }  // extern "C"

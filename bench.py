@@ -326,7 +326,12 @@ def main():
 
     ms_per_step = elapsed * 1000.0 / args.steps
     value = BATCH * args.steps / elapsed
-    gemm_tflops = work.value / (ms.value * 1e-3) / 1e12 if ms.value > 0 else 0.0
+    # Algorithmic FLOPs (2*m*n*k of the reference's GEMMs, no padding) over the family's event time;
+    # the library's own per-launch accounting must agree.
+    flops_step = cnn_gemm_flops()
+    if abs(work.value / args.steps - flops_step) > 1e-6 * flops_step:
+        raise RuntimeError(f"GEMM work accounting {work.value / args.steps} != {flops_step} per step")
+    gemm_tflops = flops_step * args.steps / (ms.value * 1e-3) / 1e12 if ms.value > 0 else 0.0
     per_launch_flops = work.value / max(launches.value, 1)
     result = {
         "metric": BASELINE_METRIC,
@@ -356,7 +361,7 @@ def main():
             "launches_per_step": launches.value / args.steps,
             "gemm_ms_per_step": round(ms.value / args.steps, 4),
             "flops_per_launch": per_launch_flops,
-            "flops_per_step": cnn_gemm_flops(),
+            "flops_per_step": flops_step,
         },
         "loss": float(loss.item()),
     }

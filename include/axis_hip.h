@@ -258,29 +258,57 @@ int axis_reduce_middle(axis_device device, const float *a, float *out, int64_t o
 /* Its Group-rule backward: out[o][r][i] = factor * gradient[o][i]. */
 int axis_broadcast_middle(axis_device device, const float *gradient, float *out, int64_t outer,
                           int64_t reduce, int64_t inner, float factor);
-/* Implicit-GEMM convolution of a channel-innermost input, one group: the reference's Conv2d
- * lowering (convolution.rs:211-235: unfold -> contract -> merge -> + bias) without materialising
- * the patch matrix.  input [batch, height, width, channels] contiguous; weight in the reference's
- * layout [(channel, ky, kx), out_channels]; bias [out_channels] or NULL;
- * out [batch, out_h, out_w, out_channels].  The patch reduction runs in (ky, kx, channel) order on
- * fp32 MFMA, so results agree with the explicit path to fp32 tolerance. */
-int axis_conv2d_forward(axis_device device, const float *input, const float *weight,
-                        const float *bias, float *out, int64_t batch, int32_t height, int32_t width,
-                        int32_t channels, int32_t out_channels, const int32_t kernel[2],
-                        const int32_t stride[2], const int32_t padding[2]);
+/* Implicit-GEMM convolution, one group: the reference's Conv2d lowering (convolution.rs:211-235:
+ * unfold -> contract -> merge -> + bias) without materialising the patch matrix.  input is read
+ * through input_strides {batch, channel, row, column} (elements; NULL = channel-innermost
+ * contiguous [batch, height, width, channels]); weight in the reference's layout
+ * [(channel, ky, kx), out_channels]; bias [out_channels] or NULL;
+ * out [batch, out_h, out_w, out_channels] (the reference's unfold output order).  The patch
+ * reduction runs in (ky, kx, channel) order on fp32 MFMA, so results agree with the explicit path
+ * to fp32 tolerance. */
+int axis_conv2d_forward(axis_device device, const float *input, const int64_t input_strides[4],
+                        const float *weight, const float *bias, float *out, int64_t batch,
+                        int32_t height, int32_t width, int32_t channels, int32_t out_channels,
+                        const int32_t kernel[2], const int32_t stride[2], const int32_t padding[2]);
+/* The same convolution followed by ReLU and a non-overlapping max pool (window = stride = pool,
+ * no padding) in the GEMM epilogue: Conv2d -> ReLU -> MaxPool2d (convolution.rs:211-235,
+ * tensor.rs:2136-2147, convolution.rs:1357-1370) with the pre-activation never written.
+ * pooled and argmax are [batch, out_h/pool[0], out_w/pool[1], out_channels]; argmax holds the
+ * window-local winner ky*pool[1]+kx (255 with a NaN output when no finite value exists), as
+ * axis_max_pool2d.  Requires out_h % pool[0] == 0, out_w % pool[1] == 0 and
+ * 128 % (pool[0] * out_w) == 0. */
+int axis_conv2d_relu_pool_forward(axis_device device, const float *input,
+                                  const int64_t input_strides[4], const float *weight,
+                                  const float *bias, float *pooled, uint8_t *argmax, int64_t batch,
+                                  int32_t height, int32_t width, int32_t channels,
+                                  int32_t out_channels, const int32_t kernel[2],
+                                  const int32_t stride[2], const int32_t padding[2],
+                                  const int32_t pool[2]);
 /* Its input gradient (Rule::MatmulLeft then Rule::Unfold, tensor.rs:5650-5680): d_input
- * [batch, height, width, channels] from gradient [batch, out_h, out_w, out_channels], computed as
- * a stride-1 convolution with the flipped kernel (no col2im pass).  Stride 1 only. */
+ * [batch, height, width, channels] (channel-innermost) from gradient
+ * [batch, out_h, out_w, out_channels], computed as a stride-1 convolution with the flipped kernel
+ * (no col2im pass).  Stride 1 and padding < kernel only. */
 int axis_conv2d_backward_data(axis_device device, const float *gradient, const float *weight,
                               float *d_input, int64_t batch, int32_t height, int32_t width,
                               int32_t channels, int32_t out_channels, const int32_t kernel[2],
                               const int32_t stride[2], const int32_t padding[2]);
 /* Its weight gradient (Rule::MatmulRight over the patches): d_weight in the reference's layout
- * [(channel, ky, kx), out_channels], deterministic split over output pixels. */
-int axis_conv2d_backward_weight(axis_device device, const float *input, const float *gradient,
+ * [(channel, ky, kx), out_channels], deterministic split over output pixels; input strides as in
+ * axis_conv2d_forward. */
+int axis_conv2d_backward_weight(axis_device device, const float *input,
+                                const int64_t input_strides[4], const float *gradient,
                                 float *d_weight, int64_t batch, int32_t height, int32_t width,
                                 int32_t channels, int32_t out_channels, const int32_t kernel[2],
                                 const int32_t stride[2], const int32_t padding[2]);
+/* Backward of ReLU -> non-overlapping max pool given the pool's outputs (Rule::Minimum gather +
+ * mask, col2im, tensor.rs:5679-5683; Rule::Relu, tensor.rs:2136-2147): d_pre
+ * [outer, height, width, channels] holds 0.0f + gradient at each window's winner when the pooled
+ * value is > 0, and 0 elsewhere -- exactly axis_max_pool2d_backward then axis_relu_backward.
+ * d_bias (or NULL) receives the column sums of d_pre in the order of axis_bias_gradient.
+ * height % pool[0] == 0 and width % pool[1] == 0. */
+int axis_relu_pool_backward(axis_device device, const float *gradient, const float *pooled,
+                            const uint8_t *argmax, float *d_pre, float *d_bias, int64_t outer,
+                            int32_t height, int32_t width, int32_t channels, const int32_t pool[2]);
 /* Softmax + categorical cross-entropy of [rows, width] logits in one pass (tensor.rs:1540-1543):
  * writes probability [rows, width] and per-row loss [rows]; each equals the separate entries. */
 int axis_softmax_cross_entropy(axis_device device, const float *logits, const float *targets,

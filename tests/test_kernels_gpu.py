@@ -393,12 +393,12 @@ def test_conv2d_entries_match_explicit_lowering(dev, oracle, b, h, w, c, n, k, s
     ref = oracle.binary(oracle.matmul(patches, weight, 1, m, c * k * k, n), np.tile(bias, m), 0)
     geo = [(I32 * 2)(k, k), (I32 * 2)(s, s), (I32 * 2)(p, p)]
     dx, dw, db, out = up(dev, x), up(dev, weight), up(dev, bias), dev.empty(m * n)
-    dev.call("axis_conv2d_forward", dx.vp, dw.vp, db.vp, out.vp, I64(b), I32(h), I32(w), I32(c), I32(n), *geo)
+    dev.call("axis_conv2d_forward", dx.vp, None, dw.vp, db.vp, out.vp, I64(b), I32(h), I32(w), I32(c), I32(n), *geo)
     assert rel_err(dev.read(out, m * n), ref) < 1e-5
     g = rng.standard_normal(m * n).astype(np.float32)
     dg = up(dev, g)
     gw = dev.empty(c * k * k * n)
-    dev.call("axis_conv2d_backward_weight", dx.vp, dg.vp, gw.vp, I64(b), I32(h), I32(w), I32(c), I32(n), *geo)
+    dev.call("axis_conv2d_backward_weight", dx.vp, None, dg.vp, gw.vp, I64(b), I32(h), I32(w), I32(c), I32(n), *geo)
     assert rel_err(dev.read(gw, c * k * k * n), oracle.matmul_right_backward(patches, g, 1, m, c * k * k, n)) < 1e-5
     gx = dev.empty(b * h * w * c)
     if s == 1:
@@ -408,3 +408,159 @@ def test_conv2d_entries_match_explicit_lowering(dev, oracle, b, h, w, c, n, k, s
     else:
         with pytest.raises(hip.AxisError, match="stride 1"):
             dev.call("axis_conv2d_backward_data", dg.vp, dw.vp, gx.vp, I64(b), I32(h), I32(w), I32(c), I32(n), *geo)
+
+
+def _oracle_conv(oracle, x, weight, bias, dims, b, c, n, k, s, p, oh, ow):
+    """unfold -> matmul -> + bias on the CPU oracle; returns (pre-activation [m, n], patches)."""
+    u = oracle.unfold_spec(dims, oracle.contiguous(dims), "c", ["height", "width"], ("group", 1),
+                           ("patch", c * k * k), [k, k], [s, s], [p, p], 0.0)
+    m = b * oh * ow
+    patches = oracle.unfold2d(x, u)
+    z = oracle.matmul(patches, weight, 1, m, c * k * k, n)
+    if bias is not None:
+        z = oracle.binary(z, np.tile(bias, m), 0)
+    return z, patches
+
+
+def _first_max(windows):
+    """The reference's pool winner: first strictly greater finite value in window order (255 and
+    NaN when none); windows [..., positions]."""
+    w = np.where(np.isfinite(windows), windows, -np.inf)
+    best = w.max(axis=-1)
+    arg = np.argmax(w == best[..., None], axis=-1).astype(np.uint8)
+    none = ~np.isfinite(windows).any(axis=-1)
+    arg[none] = 255
+    return np.where(none, np.nan, best).astype(np.float32), arg
+
+
+def _windows(y, b, oh, ow, n, ph, pw):
+    t = y.reshape(b, oh // ph, ph, ow // pw, pw, n).transpose(0, 1, 3, 5, 2, 4)
+    return t.reshape(b, oh // ph, ow // pw, n, ph * pw)
+
+
+def test_conv2d_channel_major_input(dev, oracle):
+    # conv1 of the CNN: [batch, channel, height, width] input gathered through its strides
+    b, c, h, w, n, k = 2, 3, 17, 12, 64, 3
+    rng = np.random.default_rng(31)
+    x = rng.uniform(0, 1, b * c * h * w).astype(np.float32)
+    weight = rng.standard_normal(c * k * k * n).astype(np.float32) * 0.2
+    bias = rng.standard_normal(n).astype(np.float32) * 0.1
+    dims = [("batch", b), ("c", c), ("height", h), ("width", w)]
+    z, patches = _oracle_conv(oracle, x, weight, bias, dims, b, c, n, k, 1, 1, h, w)
+    m = b * h * w
+    strides = (I64 * 4)(c * h * w, h * w, w, 1)
+    geo = [(I32 * 2)(k, k), (I32 * 2)(1, 1), (I32 * 2)(1, 1)]
+    dx, dw, db, out = up(dev, x), up(dev, weight), up(dev, bias), dev.empty(m * n)
+    dev.call("axis_conv2d_forward", dx.vp, strides, dw.vp, db.vp, out.vp, I64(b), I32(h), I32(w), I32(c),
+             I32(n), *geo)
+    assert rel_err(dev.read(out, m * n), z) < 1e-5
+    g = rng.standard_normal(m * n).astype(np.float32)
+    dg, gw = up(dev, g), dev.empty(c * k * k * n)
+    dev.call("axis_conv2d_backward_weight", dx.vp, strides, dg.vp, gw.vp, I64(b), I32(h), I32(w), I32(c),
+             I32(n), *geo)
+    assert rel_err(dev.read(gw, c * k * k * n), oracle.matmul_right_backward(patches, g, 1, m, c * k * k, n)) < 1e-5
+
+
+FUSED_CASES = [
+    # layout, b, c, h, w, n, pool
+    ("nchw", 2, 3, 16, 16, 64, (2, 2)),   # conv1 of the CNN
+    ("nhwc", 3, 64, 8, 8, 128, (2, 2)),   # conv3-like, large tiles
+    ("nhwc", 2, 5, 8, 8, 20, (2, 2)),     # scalar gathers, partial column tile
+    ("nhwc", 2, 8, 8, 8, 72, (2, 4)),     # wide windows, two column tiles
+]
+
+
+@pytest.mark.parametrize("case", range(len(FUSED_CASES)))
+def test_conv2d_relu_pool_forward(dev, oracle, case):
+    layout, b, c, h, w, n, (ph, pw) = FUSED_CASES[case]
+    k = 3
+    rng = np.random.default_rng(40 + case)
+    x = rng.standard_normal(b * c * h * w).astype(np.float32)
+    weight = rng.standard_normal(c * k * k * n).astype(np.float32) * 0.2
+    bias = rng.standard_normal(n).astype(np.float32) * 0.1
+    bias[0] = np.inf    # every ReLU output infinite: no finite winner -> NaN, 255
+    bias[1] = -np.inf   # every ReLU output 0: the first position wins with 0
+    if layout == "nchw":
+        dims = [("batch", b), ("c", c), ("height", h), ("width", w)]
+        strides = (I64 * 4)(c * h * w, h * w, w, 1)
+    else:
+        dims = [("batch", b), ("height", h), ("width", w), ("c", c)]
+        strides = None
+    z, _ = _oracle_conv(oracle, x, weight, bias, dims, b, c, n, k, 1, 1, h, w)
+    y = np.where(z > 0, z, np.float32(0))
+    ref, ref_arg = _first_max(_windows(y, b, h, w, n, ph, pw))
+    ref, ref_arg = ref.reshape(-1), ref_arg.reshape(-1)
+    pooled_len = len(ref)
+    geo = [(I32 * 2)(k, k), (I32 * 2)(1, 1), (I32 * 2)(1, 1)]
+    dx, dw, db = up(dev, x), up(dev, weight), up(dev, bias)
+    pooled, arg = dev.empty(pooled_len), dev.empty(pooled_len, np.uint8)
+    dev.call("axis_conv2d_relu_pool_forward", dx.vp, strides, dw.vp, db.vp, pooled.vp, arg.vp, I64(b), I32(h),
+             I32(w), I32(c), I32(n), *geo, (I32 * 2)(ph, pw))
+    got, got_arg = dev.read(pooled, pooled_len), dev.read(arg, pooled_len, np.uint8)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan) and nan.sum() == pooled_len // n
+    scale = np.abs(np.where(np.isfinite(z), z, 0)).max()
+    assert np.abs(got[~nan] - ref[~nan]).max() <= 1e-5 * scale
+    assert np.array_equal(got_arg[nan], ref_arg[nan])
+    # winners must agree wherever the window's best beats its runner-up by more than rounding
+    wins = _windows(np.where(np.isfinite(y), y, -np.inf), b, h, w, n, ph, pw).reshape(pooled_len, -1)
+    top2 = np.sort(wins, axis=-1)[:, -2:]
+    all_negative = (_windows(z, b, h, w, n, ph, pw).reshape(pooled_len, -1) < -1e-4 * scale).all(axis=-1)
+    clear = ((top2[:, 1] - top2[:, 0] > 1e-4 * scale) | all_negative) & ~nan
+    assert np.all(got_arg[all_negative] == 0) and np.all(got[all_negative] == 0)
+    assert clear.mean() > 0.5
+    assert np.array_equal(got_arg[clear], ref_arg[clear])
+    # bit-identical to the separate GPU entries when the plain forward runs unsplit (k < 256)
+    if c * k * k < 256:
+        zz = dev.empty(b * h * w * n)
+        dev.call("axis_conv2d_forward", dx.vp, strides, dw.vp, db.vp, zz.vp, I64(b), I32(h), I32(w), I32(c),
+                 I32(n), *geo)
+        yy = dev.empty(b * h * w * n)
+        dev.call("axis_relu", zz.vp, yy.vp, I64(b * h * w * n))
+        p2, a2 = dev.empty(pooled_len), dev.empty(pooled_len, np.uint8)
+        dev.call("axis_max_pool2d", yy.vp, p2.vp, a2.vp, I64(b), I32(h), I32(w), I64(n), (I32 * 2)(ph, pw),
+                 (I32 * 2)(ph, pw), (I32 * 2)(0, 0))
+        p2v = dev.read(p2, pooled_len)
+        assert np.array_equal(np.isnan(p2v), np.isnan(got))
+        assert np.array_equal(p2v[~nan], got[~nan])
+        assert np.array_equal(dev.read(a2, pooled_len, np.uint8), got_arg)
+
+
+def test_conv2d_relu_pool_rejects_partial_windows(dev):
+    buf = dev.empty(4096)
+    arg = dev.empty(4096, np.uint8)
+    geo = [(I32 * 2)(3, 3), (I32 * 2)(1, 1), (I32 * 2)(1, 1)]
+    with pytest.raises(hip.AxisError, match="tile the convolution output"):
+        dev.call("axis_conv2d_relu_pool_forward", buf.vp, None, buf.vp, None, buf.vp, arg.vp, I64(1), I32(7),
+                 I32(8), I32(4), I32(8), *geo, (I32 * 2)(2, 2))
+    with pytest.raises(hip.AxisError, match="divide 128"):
+        dev.call("axis_conv2d_relu_pool_forward", buf.vp, None, buf.vp, None, buf.vp, arg.vp, I64(1), I32(8),
+                 I32(96), I32(4), I32(8), *geo, (I32 * 2)(2, 2))
+
+
+@pytest.mark.parametrize("b,h,w,c,pool", [(5, 16, 18, 64, (2, 2)), (3, 10, 12, 6, (2, 3)), (2, 8, 8, 20, (4, 4))])
+def test_relu_pool_backward_bit_exact(dev, oracle, b, h, w, c, pool):
+    rng = np.random.default_rng(h * w + c)
+    z = rng.integers(-3, 4, b * h * w * c).astype(np.float32) * 0.5  # ties and exact zeros
+    z[::37] = np.nan
+    y = oracle.relu(z)
+    n_in = len(z)
+    ph, pw = pool
+    n_out = n_in // (ph * pw)
+    win = (I32 * 2)(ph, pw)
+    dy, pooled, arg = up(dev, y), dev.empty(n_out), dev.empty(n_out, np.uint8)
+    dev.call("axis_max_pool2d", dy.vp, pooled.vp, arg.vp, I64(b), I32(h), I32(w), I64(c), win, win,
+             (I32 * 2)(0, 0))
+    g = rng.standard_normal(n_out).astype(np.float32)
+    g[::11] = -0.0
+    dg, back = up(dev, g), dev.empty(n_in)
+    dev.call("axis_max_pool2d_backward", dg.vp, arg.vp, back.vp, I64(b), I32(h), I32(w), I64(c), win, win,
+             (I32 * 2)(0, 0))
+    expected = oracle.relu_backward(dev.read(back, n_in), z)
+    expected_db = oracle.bias_gradient(expected, b * h * w, c)
+    d_pre, d_bias = dev.empty(n_in), dev.empty(c)
+    dev.call("axis_relu_pool_backward", dg.vp, pooled.vp, arg.vp, d_pre.vp, d_bias.vp, I64(b), I32(h), I32(w),
+             I32(c), win)
+    got = dev.read(d_pre, n_in)
+    assert np.array_equal(got.view(np.uint32), expected.view(np.uint32))
+    assert np.array_equal(dev.read(d_bias, c).view(np.uint32), expected_db.view(np.uint32))
