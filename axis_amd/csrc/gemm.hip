@@ -528,7 +528,7 @@ struct Choice {
 Choice choose(int64_t m, int64_t n, bool pool_epilogue) {
     if ((m >= 128 || pool_epilogue) && n >= 128) return {Shape::Large, 128, 128, 32, 2};
     if (m >= 128 || pool_epilogue) {
-        if (n <= 64 || pool_epilogue) return {Shape::Tall, 128, 64, 32, 4};
+        if (n <= 64 || pool_epilogue) return {Shape::Tall, 128, 64, 32, 3};
     }
     return {Shape::Small, 64, 64, 32, 8};
 }
