@@ -19,6 +19,10 @@ struct axis_device_s {
     // last use was enqueued can serve any later launch without a host wait.
     std::multimap<size_t, void *> free_blocks;
     std::unordered_map<void *, size_t> live;
+    // Large blocks start at a rotating 4 KiB offset into their driver allocation (raw base kept
+    // here): buffers a power of two apart alias onto the same HBM channels when streamed together.
+    std::unordered_map<void *, void *> raw;
+    unsigned skew_next = 0;
     size_t in_use = 0;
     size_t cached = 0;
     int multiprocessors = 256;

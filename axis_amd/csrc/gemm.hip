@@ -301,10 +301,22 @@ __global__ void __launch_bounds__(WM *WN * 64)
 #pragma unroll
         for (int kk = 0; kk < BK; kk += 2) {
             float av[FM], bv[FN];
+            // With two 32-blocks per wave side, block a takes rows 2i + a, so both operands are
+            // one 8-byte LDS read at an immediate offset from a single base.
+            if constexpr (FM == 2) {
+                const float2 v = *reinterpret_cast<const float2 *>(xs + (kk + half) * LX::LD + wm * TM + 2 * l32);
+                av[0] = v.x, av[1] = v.y;
+            } else {
 #pragma unroll
-            for (int a = 0; a < FM; ++a) av[a] = xs[(kk + half) * LX::LD + wm * TM + a * 32 + l32];
+                for (int a = 0; a < FM; ++a) av[a] = xs[(kk + half) * LX::LD + wm * TM + a * 32 + l32];
+            }
+            if constexpr (FN == 2) {
+                const float2 v = *reinterpret_cast<const float2 *>(ys + (kk + half) * LY::LD + wn * TN + 2 * l32);
+                bv[0] = v.x, bv[1] = v.y;
+            } else {
 #pragma unroll
-            for (int b = 0; b < FN; ++b) bv[b] = ys[(kk + half) * LY::LD + wn * TN + b * 32 + l32];
+                for (int b = 0; b < FN; ++b) bv[b] = ys[(kk + half) * LY::LD + wn * TN + b * 32 + l32];
+            }
 #pragma unroll
             for (int a = 0; a < FM; ++a)
 #pragma unroll
@@ -320,24 +332,48 @@ __global__ void __launch_bounds__(WM *WN * 64)
     }
 
     // Accumulator layout of the 32x32 block: lane -> column l32; register v -> row
-    // 8*(v/4) + 4*(lane/32) + (v%4).  The bias (one value per column) is added only when the
-    // reduction is not split; split sums add it once at the end.
+    // 8*(v/4) + 4*(lane/32) + (v%4), both mapped into the wave's tile by the block placement
+    // above (rows 2i + a when FM == 2, else a*32 + i; columns likewise).  The bias (one value per
+    // column) is added only when the reduction is not split; split sums add it once at the end.
+    auto row_in = [](int a, int i) { return FM == 2 ? 2 * i + a : a * 32 + i; };
+    auto col_in = [](int b, int l) { return FN == 2 ? 2 * l + b : b * 32 + l; };
     if constexpr (EPI == 0) {
         float *c = p.c + batch * p.c_batch + (int64_t)split * p.c_split;
         const bool with_bias = p.bias != nullptr && p.splits == 1;
+        if (FN == 2 && (p.n & 1) == 0) {
+            // the two column blocks of a lane are adjacent columns: one 8-byte store per row
+            const int64_t col = j0 + wn * TN + 2 * l32;
+            if (col < p.n) {
+                const float add0 = with_bias ? p.bias[col] : 0.0f;
+                const float add1 = with_bias ? p.bias[col + 1] : 0.0f;
 #pragma unroll
-        for (int a = 0; a < FM; ++a)
+                for (int a = 0; a < FM; ++a)
 #pragma unroll
-            for (int b = 0; b < FN; ++b) {
-                const int64_t col = j0 + wn * TN + b * 32 + l32;
-                if (col >= p.n) continue;
-                const float add = with_bias ? p.bias[col] : 0.0f;
-#pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const int64_t row = i0 + wm * TM + a * 32 + (v >> 2) * 8 + half * 4 + (v & 3);
-                    if (row < p.m) c[row * p.n + col] = with_bias ? acc[a][b][v] + add : acc[a][b][v];
-                }
+                    for (int v = 0; v < 16; ++v) {
+                        const int64_t row = i0 + wm * TM + row_in(a, (v >> 2) * 8 + half * 4 + (v & 3));
+                        if (row < p.m) {
+                            float2 o;
+                            o.x = with_bias ? acc[a][0][v] + add0 : acc[a][0][v];
+                            o.y = with_bias ? acc[a][FN - 1][v] + add1 : acc[a][FN - 1][v];
+                            *reinterpret_cast<float2 *>(c + row * p.n + col) = o;
+                        }
+                    }
             }
+        } else {
+#pragma unroll
+            for (int a = 0; a < FM; ++a)
+#pragma unroll
+                for (int b = 0; b < FN; ++b) {
+                    const int64_t col = j0 + wn * TN + col_in(b, l32);
+                    if (col >= p.n) continue;
+                    const float add = with_bias ? p.bias[col] : 0.0f;
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        const int64_t row = i0 + wm * TM + row_in(a, (v >> 2) * 8 + half * 4 + (v & 3));
+                        if (row < p.m) c[row * p.n + col] = with_bias ? acc[a][b][v] + add : acc[a][b][v];
+                    }
+                }
+        }
     } else {
         // The block's BM rows are whole rows of pooling windows (the host guarantees
         // BM % (pool_h * pool_ow) == 0 and an exact tiling), so every window is complete here.
@@ -356,13 +392,13 @@ __global__ void __launch_bounds__(WM *WN * 64)
                 for (int a = 0; a < FM; ++a)
 #pragma unroll
                     for (int b = 0; b < FN; ++b) {
-                        const int cl = b * 32 + l32;
+                        const int cl = col_in(b, l32);
                         const int64_t col = j0 + h * TN + cl;
                         const bool with_bias = p.bias != nullptr && col < p.n;
                         const float add = with_bias ? p.bias[col] : 0.0f;
 #pragma unroll
                         for (int v = 0; v < 16; ++v) {
-                            const int rl = wm * TM + a * 32 + (v >> 2) * 8 + half * 4 + (v & 3);
+                            const int rl = wm * TM + row_in(a, (v >> 2) * 8 + half * 4 + (v & 3));
                             const float z = with_bias ? acc[a][b][v] + add : acc[a][b][v];
                             lds[rl * kPoolPitch + cl] = z > 0.0f ? z : 0.0f;
                         }
