@@ -118,40 +118,52 @@ struct Staging {
     }
 };
 
-// Dense operand: element (t, r) at base[t * s_t + r * s_r].
+// Dense operand: element (t, r) at base[t * s_t + r * s_r].  Each of the thread's vectors keeps
+// its own pointer at r = 0; a K step adds the wave-uniform r0 * s_r, so the per-step address
+// work is one 64-bit add per vector.
 template <int BT, int BK, int NT, bool RCONTIG, int VEC>
 struct DenseLoader : Staging<BT, BK, NT, RCONTIG, VEC> {
     using S = Staging<BT, BK, NT, RCONTIG, VEC>;
-    const float *base;
-    int64_t s_t, s_r, t0, t_end;
+    const float *ptr[S::kVecs];
+    int32_t rr[S::kVecs];   // r offset of each vector inside the tile
+    bool t_ok[S::kVecs];
+    int64_t s_r;
 
-    __device__ __forceinline__ void init(const float *b, int64_t st, int64_t sr, int64_t t_begin,
-                                         int64_t t_limit) {
-        base = b, s_t = st, s_r = sr, t0 = t_begin, t_end = t_limit;
-    }
-    __device__ __forceinline__ void load(const ConvGeom &, int64_t r0, int64_t r_end, int tid) {
+    __device__ __forceinline__ void init(const float *b, int64_t st, int64_t sr, int64_t t0,
+                                         int64_t t_end, int tid) {
+        s_r = sr;
 #pragma unroll
         for (int e = 0; e < S::kVecs; ++e) {
             const int idx = tid + e * NT;
-            int tt, rr;
+            int tt, r;
             if (RCONTIG) {
-                rr = (idx % S::kPer) * VEC;
+                r = (idx % S::kPer) * VEC;
                 tt = idx / S::kPer;
             } else {
                 tt = (idx % S::kPer) * VEC;
-                rr = idx / S::kPer;
+                r = idx / S::kPer;
             }
-            const int64_t gt = t0 + tt, gr = r0 + rr;
-            load_into<VEC>(this->reg + e * VEC, base + gt * s_t + gr * s_r, gt < t_end && gr < r_end);
+            const int64_t gt = t0 + tt;
+            t_ok[e] = gt < t_end;
+            rr[e] = r;
+            ptr[e] = b + (t_ok[e] ? gt : 0) * st + (int64_t)r * sr;
         }
+    }
+    __device__ __forceinline__ void load(const ConvGeom &, int64_t r0, int64_t r_end, int) {
+        const int64_t step = r0 * s_r;
+#pragma unroll
+        for (int e = 0; e < S::kVecs; ++e)
+            load_into<VEC>(this->reg + e * VEC, ptr[e] + step, t_ok[e] && r0 + rr[e] < r_end);
     }
 };
 
 // Convolution operand, rows mode: t = output pixel, r = (ky*kw + kx)*channels + channel.
+// Per row: the offset of its window origin and the origin's coordinates (for the padding test);
+// per K step: one decode of the thread's r into a 32-bit offset shared by every row.
 template <int BT, int BK, int NT, int VEC>
 struct ConvRowsLoader : Staging<BT, BK, NT, true, VEC> {
     using S = Staging<BT, BK, NT, true, VEC>;
-    int64_t pixel_base[S::kVecs];  // offset of (b, 0, 0, 0); -1 past the last row
+    uint32_t origin[S::kVecs];   // b*ld_b + iy0*ld_h + ix0*ld_w (mod 2^32; exact when valid)
     int32_t iy0[S::kVecs], ix0[S::kVecs];
     int rr;
 
@@ -160,78 +172,106 @@ struct ConvRowsLoader : Staging<BT, BK, NT, true, VEC> {
 #pragma unroll
         for (int e = 0; e < S::kVecs; ++e) {
             const int64_t gt = t0 + (tid + e * NT) / S::kPer;
-            // Rows past the end get base -1 and a far-out origin; computed branch-free so the
-            // per-row arrays stay in registers.
+            // Rows past the end get an origin far outside the image, so every tap is padding;
+            // computed branch-free so the per-row arrays stay in registers.
             const bool live = gt < t_end;
             const uint32_t pix = live ? (uint32_t)gt : 0u;
             const uint32_t q = geom.ow_div.div(pix);
             const int32_t ox = (int32_t)(pix - q * (uint32_t)geom.out_w);
             const uint32_t b = geom.oh_div.div(q);
             const int32_t oy = (int32_t)(q - b * (uint32_t)geom.out_h);
-            pixel_base[e] = live ? (int64_t)b * geom.ld_b : -1;
-            iy0[e] = oy * geom.sy - geom.py;
+            const int32_t y0 = oy * geom.sy - geom.py;
             ix0[e] = ox * geom.sx - geom.px;
+            origin[e] = b * (uint32_t)geom.ld_b + (uint32_t)y0 * (uint32_t)geom.ld_h +
+                        (uint32_t)ix0[e] * (uint32_t)geom.ld_w;
+            iy0[e] = live ? y0 : -(1 << 30);
         }
     }
     __device__ __forceinline__ void load(const ConvGeom &geom, int64_t r0, int64_t r_end, int) {
         const int64_t gr = r0 + rr;
         const bool r_ok = gr < r_end;
-        int32_t c = 0, ky = 0, kx = 0;
-        if (r_ok) {
-            const uint32_t pos = geom.c_div.div((uint32_t)gr);
-            c = (int32_t)((uint32_t)gr - pos * (uint32_t)geom.channels);
-            ky = (int32_t)geom.kw_div.div(pos);
-            kx = (int32_t)pos - ky * geom.kw;
-        }
+        const uint32_t g = r_ok ? (uint32_t)gr : 0u;
+        const uint32_t pos = geom.c_div.div(g);
+        const int32_t c = (int32_t)(g - pos * (uint32_t)geom.channels);
+        const int32_t ky = (int32_t)geom.kw_div.div(pos);
+        const int32_t kx = (int32_t)pos - ky * geom.kw;
+        const uint32_t delta = (uint32_t)(ky * geom.ld_h + kx * geom.ld_w + c * geom.ld_c);
 #pragma unroll
         for (int e = 0; e < S::kVecs; ++e) {
-            const int32_t iy = iy0[e] + ky, ix = ix0[e] + kx;
-            const bool valid = r_ok && pixel_base[e] >= 0 && iy >= 0 && iy < geom.height && ix >= 0 &&
-                               ix < geom.width;
-            const int64_t off =
-                valid ? pixel_base[e] + (int64_t)iy * geom.ld_h + (int64_t)ix * geom.ld_w + (int64_t)c * geom.ld_c
-                      : 0;
-            load_into<VEC>(this->reg + e * VEC, geom.src + off, valid);
+            const bool valid = r_ok && (uint32_t)(iy0[e] + ky) < (uint32_t)geom.height &&
+                               (uint32_t)(ix0[e] + kx) < (uint32_t)geom.width;
+            load_into<VEC>(this->reg + e * VEC, geom.src + (valid ? origin[e] + delta : 0u), valid);
         }
     }
 };
 
-// Convolution operand, cols mode: t = (ky*kw + kx)*channels + channel, r = output pixel.
+// Convolution operand, cols mode: t = (ky*kw + kx)*channels + channel, r = output pixel.  The
+// thread's t is fixed; each row keeps its pixel's coordinates and offset and walks forward BK
+// pixels per K step.
 template <int BT, int BK, int NT, int VEC>
 struct ConvColsLoader : Staging<BT, BK, NT, false, VEC> {
     using S = Staging<BT, BK, NT, false, VEC>;
-    int32_t c, ky, kx;
+    static constexpr int kRowStep = NT / S::kPer;  // pixels between the thread's rows
+    uint32_t tap;                // (ky-py)*ld_h + (kx-px)*ld_w + c*ld_c of the thread's t (mod 2^32)
+    int32_t ky, kx;
     bool t_ok;
-    int row0;
+    int32_t ox[S::kVecs], oy[S::kVecs];
+    uint32_t off[S::kVecs];      // b*ld_b + oy*sy*ld_h + ox*sx*ld_w (mod 2^32)
+    int64_t next_r;              // r0 the state describes
 
     __device__ __forceinline__ void init(const ConvGeom &geom, int64_t t0, int64_t t_end, int tid) {
         const int64_t gt = t0 + (tid % S::kPer) * VEC;
         t_ok = gt < t_end;
-        const uint32_t pos = geom.c_div.div((uint32_t)(t_ok ? gt : 0));
-        c = (int32_t)((uint32_t)(t_ok ? gt : 0) - pos * (uint32_t)geom.channels);
+        const uint32_t g = t_ok ? (uint32_t)gt : 0u;
+        const uint32_t pos = geom.c_div.div(g);
+        const int32_t c = (int32_t)(g - pos * (uint32_t)geom.channels);
         ky = (int32_t)geom.kw_div.div(pos);
         kx = (int32_t)pos - ky * geom.kw;
-        row0 = tid / S::kPer;
+        tap = (uint32_t)(ky - geom.py) * (uint32_t)geom.ld_h + (uint32_t)(kx - geom.px) * (uint32_t)geom.ld_w +
+              (uint32_t)c * (uint32_t)geom.ld_c;
+        next_r = -1;
     }
-    __device__ __forceinline__ void load(const ConvGeom &geom, int64_t r0, int64_t r_end, int) {
+    __device__ __forceinline__ void locate(const ConvGeom &geom, int64_t r0, int tid) {
 #pragma unroll
         for (int e = 0; e < S::kVecs; ++e) {
-            const int64_t gr = r0 + row0 + e * (NT / S::kPer);
-            bool valid = t_ok && gr < r_end;
-            int64_t off = 0;
-            if (valid) {
-                const uint32_t pix = (uint32_t)gr;
-                const uint32_t q = geom.ow_div.div(pix);
-                const int32_t ox = (int32_t)(pix - q * (uint32_t)geom.out_w);
-                const uint32_t b = geom.oh_div.div(q);
-                const int32_t oy = (int32_t)(q - b * (uint32_t)geom.out_h);
-                const int32_t iy = oy * geom.sy + ky - geom.py, ix = ox * geom.sx + kx - geom.px;
-                valid = iy >= 0 && iy < geom.height && ix >= 0 && ix < geom.width;
-                off = (int64_t)b * geom.ld_b + (int64_t)iy * geom.ld_h + (int64_t)ix * geom.ld_w +
-                      (int64_t)c * geom.ld_c;
-            }
-            load_into<VEC>(this->reg + e * VEC, geom.src + (valid ? off : 0), valid);
+            const uint32_t pix = (uint32_t)(r0 + tid / S::kPer + e * kRowStep);
+            const uint32_t q = geom.ow_div.div(pix);
+            ox[e] = (int32_t)(pix - q * (uint32_t)geom.out_w);
+            const uint32_t b = geom.oh_div.div(q);
+            oy[e] = (int32_t)(q - b * (uint32_t)geom.out_h);
+            off[e] = b * (uint32_t)geom.ld_b + (uint32_t)(oy[e] * geom.sy) * (uint32_t)geom.ld_h +
+                     (uint32_t)(ox[e] * geom.sx) * (uint32_t)geom.ld_w;
         }
+        next_r = r0;
+    }
+    __device__ __forceinline__ void advance(const ConvGeom &geom) {
+        const uint32_t col_step = (uint32_t)(geom.sx * geom.ld_w), row_step = (uint32_t)(geom.sy * geom.ld_h);
+#pragma unroll
+        for (int e = 0; e < S::kVecs; ++e) {
+            ox[e] += BK;
+            off[e] += BK * col_step;
+            while (ox[e] >= geom.out_w) {
+                ox[e] -= geom.out_w;
+                off[e] += row_step - (uint32_t)geom.out_w * col_step;
+                if (++oy[e] == geom.out_h) {
+                    oy[e] = 0;
+                    off[e] += (uint32_t)geom.ld_b - (uint32_t)geom.out_h * row_step;
+                }
+            }
+        }
+        next_r += BK;
+    }
+    __device__ __forceinline__ void load(const ConvGeom &geom, int64_t r0, int64_t r_end, int tid) {
+        if (r0 != next_r) locate(geom, r0, tid);
+#pragma unroll
+        for (int e = 0; e < S::kVecs; ++e) {
+            const int64_t gr = r0 + tid / S::kPer + e * kRowStep;
+            const int32_t iy = oy[e] * geom.sy + ky - geom.py, ix = ox[e] * geom.sx + kx - geom.px;
+            const bool valid = t_ok && gr < r_end && (uint32_t)iy < (uint32_t)geom.height &&
+                               (uint32_t)ix < (uint32_t)geom.width;
+            load_into<VEC>(this->reg + e * VEC, geom.src + (valid ? off[e] + tap : 0u), valid);
+        }
+        advance(geom);
     }
 };
 
@@ -278,10 +318,10 @@ __global__ void __launch_bounds__(WM *WN * 64)
     LX lx;
     LY ly;
     if constexpr (XMODE == 0)
-        lx.init(p.x + batch * p.x_batch, p.x_si, p.x_sr, i0, p.m);
+        lx.init(p.x + batch * p.x_batch, p.x_si, p.x_sr, i0, p.m, tid);
     else
         lx.init(p.conv, i0, p.m, tid);
-    ly.init(p.y + batch * p.y_batch, p.y_sj, p.y_sr, j0, p.n);
+    ly.init(p.y + batch * p.y_batch, p.y_sj, p.y_sr, j0, p.n, tid);
     if (r_begin < r_end) {
         lx.load(p.conv, r_begin, r_end, tid);
         ly.load(p.conv, r_begin, r_end, tid);
@@ -529,21 +569,22 @@ __global__ void __launch_bounds__(256) repack_channels_last_kernel(const float *
     }
 }
 
+// lds_pad: unused dynamic LDS per block, which caps how many blocks share a CU.
 template <int BM, int BN, int BK, int WM, int WN, bool XR, bool YR, int VX, int VY, int XMODE, int EPI>
-void launch_config(const GemmParams &p, dim3 grid, hipStream_t stream) {
-    gemm_kernel<BM, BN, BK, WM, WN, XR, YR, VX, VY, XMODE, EPI><<<grid, WM * WN * 64, 0, stream>>>(p);
+void launch_config(const GemmParams &p, dim3 grid, size_t lds_pad, hipStream_t stream) {
+    gemm_kernel<BM, BN, BK, WM, WN, XR, YR, VX, VY, XMODE, EPI><<<grid, WM * WN * 64, lds_pad, stream>>>(p);
 }
 
 template <int BM, int BN, int BK, int WM, int WN, bool XR, bool YR, int XMODE, int EPI>
-void launch_vec(const GemmParams &p, dim3 grid, hipStream_t stream, bool vx, bool vy) {
+void launch_vec(const GemmParams &p, dim3 grid, size_t lds_pad, hipStream_t stream, bool vx, bool vy) {
     if (vx && vy)
-        launch_config<BM, BN, BK, WM, WN, XR, YR, 4, 4, XMODE, EPI>(p, grid, stream);
+        launch_config<BM, BN, BK, WM, WN, XR, YR, 4, 4, XMODE, EPI>(p, grid, lds_pad, stream);
     else if (vx)
-        launch_config<BM, BN, BK, WM, WN, XR, YR, 4, 1, XMODE, EPI>(p, grid, stream);
+        launch_config<BM, BN, BK, WM, WN, XR, YR, 4, 1, XMODE, EPI>(p, grid, lds_pad, stream);
     else if (vy)
-        launch_config<BM, BN, BK, WM, WN, XR, YR, 1, 4, XMODE, EPI>(p, grid, stream);
+        launch_config<BM, BN, BK, WM, WN, XR, YR, 1, 4, XMODE, EPI>(p, grid, lds_pad, stream);
     else
-        launch_config<BM, BN, BK, WM, WN, XR, YR, 1, 1, XMODE, EPI>(p, grid, stream);
+        launch_config<BM, BN, BK, WM, WN, XR, YR, 1, 1, XMODE, EPI>(p, grid, lds_pad, stream);
 }
 
 // Vector loads need the contiguous extent, the other stride and the base to be 4-aligned.
@@ -559,14 +600,26 @@ enum class Shape { Large, Tall, Small };
 struct Choice {
     Shape shape;
     int bm, bn, bk, per_cu;
+    size_t lds_pad = 0;
 };
 
-Choice choose(int64_t m, int64_t n, bool pool_epilogue) {
-    if ((m >= 128 || pool_epilogue) && n >= 128) return {Shape::Large, 128, 128, 32, 2};
-    if (m >= 128 || pool_epilogue) {
-        if (n <= 64 || pool_epilogue) return {Shape::Tall, 128, 64, 32, 3};
+Choice choose(int64_t m, int64_t n, int64_t batch, int64_t cus, bool pool_epilogue) {
+    const Choice large{Shape::Large, 128, 128, 32, 3}, tall{Shape::Tall, 128, 64, 32, 4},
+        small{Shape::Small, 64, 64, 32, 5};
+    if (m < 128 && !pool_epilogue) return small;
+    if (n < 128) return n <= 64 || pool_epilogue ? tall : small;
+    // Large tiles run three to a CU.  When that leaves each CU one lone block in its last round
+    // (of a few), that block runs at one wave per SIMD; holding them to two per CU (padding the
+    // dynamic LDS past a third of the CU's 160 KiB) fills every round instead.
+    const int64_t tiles = ((m + 127) / 128) * ((n + 127) / 128) * batch;
+    const int64_t per_cu = (tiles + cus - 1) / cus;
+    if (tiles % cus == 0 && per_cu % large.per_cu == 1 && per_cu < 4 * large.per_cu) {
+        Choice two = large;
+        two.per_cu = 2;
+        two.lds_pad = 30 * 1024;
+        return two;
     }
-    return {Shape::Small, 64, 64, 32, 8};
+    return large;
 }
 
 // Deterministic sum of reduction slices (+ bias): up to 32 slices in one pass; beyond that, ranges
@@ -592,7 +645,7 @@ int sum_splits(axis_device device, const float *partial, float *out, int64_t len
 template <bool XR, bool YR, int XMODE, int EPI>
 int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out) {
     const int64_t cus = device->multiprocessors;
-    const Choice ch = choose(p.m, p.n, EPI == 1);
+    const Choice ch = choose(p.m, p.n, batch, cus, EPI == 1);
     const int BK = ch.bk;
     p.tiles_m = static_cast<int32_t>((p.m + ch.bm - 1) / ch.bm);
     p.tiles_n = static_cast<int32_t>((p.n + ch.bn - 1) / ch.bn);
@@ -644,16 +697,16 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out) {
     dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n), static_cast<unsigned>(batch * splits));
     if constexpr (EPI == 1) {
         if (ch.shape == Shape::Large)
-            launch_vec<128, 128, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, device->stream, vx, vy);
+            launch_vec<128, 128, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, ch.lds_pad, device->stream, vx, vy);
         else
-            launch_vec<128, 64, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, device->stream, vx, vy);
+            launch_vec<128, 64, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, ch.lds_pad, device->stream, vx, vy);
     } else {
         if (ch.shape == Shape::Large)
-            launch_vec<128, 128, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, device->stream, vx, vy);
+            launch_vec<128, 128, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, ch.lds_pad, device->stream, vx, vy);
         else if (ch.shape == Shape::Tall)
-            launch_vec<128, 64, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, device->stream, vx, vy);
+            launch_vec<128, 64, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, ch.lds_pad, device->stream, vx, vy);
         else
-            launch_vec<64, 64, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, device->stream, vx, vy);
+            launch_vec<64, 64, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, ch.lds_pad, device->stream, vx, vy);
     }
     int status = axis::launch_status("gemm_kernel");
     if (status) return status;
@@ -779,14 +832,18 @@ struct GatherInput {
     int prepare(axis_device device, const float *input, const int64_t given[4], int64_t batch,
                 int32_t height, int32_t width, int32_t c_in) {
         if (int st = input_strides(given, batch, height, width, c_in, ld)) return st;
+        // Gathers address the tensor with 32-bit offsets.
+        const int64_t last = (batch - 1) * ld[0] + (int64_t)(c_in - 1) * ld[1] +
+                             (int64_t)(height - 1) * ld[2] + (int64_t)(width - 1) * ld[3];
         if (ld[1] == 1 && c_in % 4 == 0 && ld[2] % 4 == 0 && ld[3] % 4 == 0 && ld[0] % 4 == 0 &&
-            axis::aligned16(input)) {
+            axis::aligned16(input) && last < INT32_MAX && ld[0] < INT32_MAX) {
             src = input;
             channels = c_in;
             return AXIS_OK;
         }
         channels = (c_in + 3) / 4 * 4;
         const int64_t pixels = batch * height * width;
+        AXIS_REQUIRE(pixels * channels < INT32_MAX, "convolution input too large for 32-bit gathers");
         if (int st = copy.get(device, sizeof(float) * (size_t)(pixels * channels))) return st;
         repack_channels_last_kernel<<<axis::blocks_for(pixels * (channels / 4), 256, 1 << 16), 256, 0,
                                       device->stream>>>(input, ld[0], ld[1], ld[2], ld[3], copy.as<float>(),
