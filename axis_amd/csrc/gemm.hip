@@ -64,6 +64,7 @@ struct GemmParams {
     int64_t k_work;            // algorithmic reduction length for timing (k without padding), or 0
     int32_t splits;
     int32_t tiles_m, tiles_n;
+    uint32_t xcd_span;         // blocks per XCD when the launch is remapped (blocks % 8 == 0), else 0
     ConvGeom conv;
     // Pooling epilogue: output rows are pixels of a [.., out_h, out_w] grid (out_w = pool_ow).
     float *pooled;
@@ -299,11 +300,18 @@ __global__ void __launch_bounds__(WM *WN * 64)
     const int wave = tid >> 6;
     const int wm = wave % WM, wn = wave / WM;
 
-    const int tile = blockIdx.x;
-    const int64_t i0 = (int64_t)(tile % p.tiles_m) * BM;
-    const int64_t j0 = (int64_t)(tile / p.tiles_m) * BN;
-    const int split = blockIdx.y % p.splits;
-    const int64_t batch = blockIdx.y / p.splits;
+    // Workgroups go to the 8 XCDs round-robin in launch order; block L takes logical tile
+    // (L % 8) * (blocks / 8) + L / 8 so each XCD (its own L2) works through a contiguous range
+    // of tiles: the tiles of one reduction slice, or neighbouring row panels, share its cache.
+    const uint32_t tiles = (uint32_t)p.tiles_m * (uint32_t)p.tiles_n;
+    const uint32_t L = blockIdx.x;
+    const uint32_t logical = p.xcd_span ? (L % 8u) * p.xcd_span + L / 8u : L;
+    const uint32_t tile = logical % tiles;
+    const uint32_t slice = logical / tiles;
+    const int64_t i0 = (int64_t)(tile % (uint32_t)p.tiles_m) * BM;
+    const int64_t j0 = (int64_t)(tile / (uint32_t)p.tiles_m) * BN;
+    const int split = (int)(slice % (uint32_t)p.splits);
+    const int64_t batch = slice / (uint32_t)p.splits;
     const int64_t r_begin = (int64_t)split * p.k_chunk;
     const int64_t r_end = r_begin + p.k_chunk < p.k ? r_begin + p.k_chunk : p.k;
 
@@ -690,11 +698,12 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out) {
         p.c_split = 0;
         p.c_batch = p.m * p.n;
     }
-    if (batch * splits > 65535)
-        return axis::fail(AXIS_ERROR_INVALID, "matmul batch too large for one launch");
+    const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n * batch * splits;
+    if (blocks >= INT32_MAX) return axis::fail(AXIS_ERROR_INVALID, "matmul too large for one launch");
+    p.xcd_span = blocks % 8 == 0 ? (uint32_t)(blocks / 8) : 0u;
     const double k_work = (double)(p.k_work > 0 ? p.k_work : p.k);
     axis::TimedLaunch timed(device, "gemm", 2.0 * (double)batch * (double)p.m * (double)p.n * k_work);
-    dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n), static_cast<unsigned>(batch * splits));
+    dim3 grid(static_cast<unsigned>(blocks));
     if constexpr (EPI == 1) {
         if (ch.shape == Shape::Large)
             launch_vec<128, 128, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, ch.lds_pad, device->stream, vx, vy);

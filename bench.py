@@ -279,6 +279,21 @@ def bench_muon(args):
                       "loss": float(loss.item())}))
 
 
+def calibration_copy(lib, handle, nbytes):
+    """One device-to-device copy of nbytes: the known-size reference for HBM traffic counters."""
+    from axis_amd import hip
+    src, dst = ctypes.c_void_p(), ctypes.c_void_p()
+    hip.check(lib.axis_alloc(handle, ctypes.c_size_t(nbytes), ctypes.byref(src)), "axis_alloc")
+    hip.check(lib.axis_alloc(handle, ctypes.c_size_t(nbytes), ctypes.byref(dst)), "axis_alloc")
+    hip.check(lib.axis_fill(handle, ctypes.cast(src, ctypes.POINTER(ctypes.c_float)), ctypes.c_float(1.0),
+                            ctypes.c_int64(nbytes // 4)), "axis_fill")
+    hip.check(lib.axis_device_synchronize(handle), "axis_device_synchronize")
+    hip.check(lib.axis_copy(handle, dst, src, ctypes.c_size_t(nbytes)), "axis_copy")
+    hip.check(lib.axis_device_synchronize(handle), "axis_device_synchronize")
+    lib.axis_free(handle, src)
+    lib.axis_free(handle, dst)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -286,6 +301,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-batch", type=int, default=256)
+    ap.add_argument("--calibration-copy-mib", type=int, default=0,
+                    help="one device-to-device copy of this size before the timed steps (a known-size "
+                         "dispatch that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     ap.add_argument("--workload", choices=["cnn", "matmul", "adam", "muon"], default="cnn",
                     help="cnn: the headline metric (BASELINE config 4); the others are configs 2, 3, 5")
     args = ap.parse_args()
@@ -311,6 +329,8 @@ def main():
 
     # The host layer's device handle: timing is toggled through the same C ABI.
     dev_handle = _device_handle(device)
+    if args.calibration_copy_mib > 0:
+        calibration_copy(lib, dev_handle, args.calibration_copy_mib << 20)
     lib.axis_timing_reset(dev_handle)
     lib.axis_timing_enable(dev_handle, 1)
     device.synchronize()
