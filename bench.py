@@ -199,6 +199,8 @@ def bench_adam(args):
         t += 1
         step(t)
     dev.synchronize()
+    if args.calibration_copy_mib > 0:
+        calibration_copy(lib, dev.handle, args.calibration_copy_mib << 20)
     lib.axis_timing_reset(dev.handle)
     lib.axis_timing_enable(dev.handle, 1)
     start = time.perf_counter()
@@ -210,13 +212,15 @@ def bench_adam(args):
     lib.axis_timing_enable(dev.handle, 0)
     launches, ms, work = _timing(lib, dev.handle, "adam")
     gbs = work / (ms * 1e-3) / 1e9
+    traffic, traffic_source = profile_traffic("adam_16x4M_pmc.md")
     print(json.dumps({"metric": "fused Adam GB/s (16 x 4M fp32 params, 28 B/param)", "value": round(gbs, 1),
                       "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
                       "ms_per_step": round(ms / args.steps, 4), "wall_ms_per_step": round(elapsed * 1e3 / args.steps, 4),
                       "higher_is_better": True, "dtype": "fp32", "data": "synthetic, seeds 100-115 / 200-215",
                       "config": {"workload": "BASELINE config 3: Adam over 64Mi params in 16 tensors"},
                       "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                                   "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}}))
+                                   "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                                   "traffic_source": traffic_source}}))
 
 
 def bench_muon(args):
@@ -277,6 +281,19 @@ def bench_muon(args):
                                    "gemm_ms_per_step": round(ms / args.steps, 3),
                                    "gemm_tflop_per_step": round(work / args.steps / 1e12, 3)},
                       "loss": float(loss.item())}))
+
+
+def profile_traffic(name):
+    """HBM bytes per launch measured by rocprofv3 FETCH_SIZE + WRITE_SIZE passes (copy-calibrated),
+    as recorded in profiles/<name> (the counters cannot be read from inside this process)."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", name)
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1])), "profiles/" + name
+    except OSError:
+        pass
+    return None, None
 
 
 def calibration_copy(lib, handle, nbytes):
@@ -352,6 +369,7 @@ def main():
     if abs(work.value / args.steps - flops_step) > 1e-6 * flops_step:
         raise RuntimeError(f"GEMM work accounting {work.value / args.steps} != {flops_step} per step")
     gemm_tflops = flops_step * args.steps / (ms.value * 1e-3) / 1e12 if ms.value > 0 else 0.0
+    traffic, traffic_source = profile_traffic("cnn_train_step_bs256_pmc.md")
     per_launch_flops = work.value / max(launches.value, 1)
     result = {
         "metric": BASELINE_METRIC,
@@ -377,7 +395,8 @@ def main():
             "peak": FP32_MFMA_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(gemm_tflops / FP32_MFMA_PEAK_TFLOPS, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": traffic_source,
             "launches_per_step": launches.value / args.steps,
             "gemm_ms_per_step": round(ms.value / args.steps, 4),
             "flops_per_launch": per_launch_flops,
