@@ -9,6 +9,7 @@
 // Non-overlapping windows (stride == kernel, no padding, exact tiling) take a scatter-form
 // backward -- one lane per output writes its window -- which equals the gather sum exactly: each
 // input receives exactly one term, written as 0.0f + g like the sum the reference starts at +0.0.
+#include <algorithm>
 #include <cfloat>
 
 #include "column_sum.hpp"
@@ -165,6 +166,83 @@ __global__ void __launch_bounds__(256) relu_pool_backward_kernel(
             store_vec<VEC>(base + ((int64_t)iy * a.width + ix) * a.channels, r);
         }
     }
+}
+
+// The same scatter with the bias gradient folded in.  A block walks a contiguous range of pooled
+// vectors with stride 256, so a lane keeps one channel vector (256 is a multiple of the vector
+// count per pixel) and sums the terms it writes; a fixed-order block reduction leaves one partial
+// per block and channel, summed afterwards by relu_pool_bias_combine_kernel in a fixed tree.  The
+// association differs from the reference's 512-row chunks (fp32 tolerance, not bit equality) but
+// is the same on every run.
+template <int VEC>
+__global__ void __launch_bounds__(256) relu_pool_backward_bias_kernel(
+    const float *__restrict__ gradient, const float *__restrict__ pooled,
+    const uint8_t *__restrict__ argmax, float *__restrict__ out, float *__restrict__ partial,
+    uint32_t span, PoolArgs a) {
+    __shared__ float lane_sum[256][VEC];
+    const uint32_t begin = blockIdx.x * span;
+    const uint32_t end = begin + span < a.total ? begin + span : a.total;
+    float acc[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] = 0.0f;
+    for (uint32_t t = begin + threadIdx.x; t < end; t += 256u) {
+        const uint32_t cv = a.cvec.mod(t);
+        uint32_t rest = a.cvec.div(t);
+        const int32_t ox = (int32_t)a.ow.mod(rest);
+        rest = a.ow.div(rest);
+        const int32_t oy = (int32_t)a.oh.mod(rest);
+        const uint32_t o = a.oh.div(rest);
+        const int32_t c = (int32_t)cv * VEC;
+        float g[VEC], y[VEC];
+        int w[VEC];
+        load_vec<VEC>(gradient + (int64_t)t * VEC, g);
+        load_vec<VEC>(pooled + (int64_t)t * VEC, y);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+            w[e] = y[e] > 0.0f ? (int)argmax[(int64_t)t * VEC + e] : -1;
+            acc[e] += (w[e] >= 0 && w[e] < a.ky * a.kx) ? 0.0f + g[e] : 0.0f;
+        }
+        float *base = out + (int64_t)o * a.height * a.width * a.channels + c;
+        for (int32_t ky = 0; ky < a.ky; ++ky) {
+            const int32_t iy = oy * a.ky + ky;
+            for (int32_t kx = 0; kx < a.kx; ++kx) {
+                const int32_t ix = ox * a.kx + kx;
+                const int k = ky * a.kx + kx;
+                float r[VEC];
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) r[e] = w[e] == k ? 0.0f + g[e] : 0.0f;
+                store_vec<VEC>(base + ((int64_t)iy * a.width + ix) * a.channels, r);
+            }
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) lane_sum[threadIdx.x][e] = acc[e];
+    __syncthreads();
+    const int per_pixel = a.channels / VEC;  // lanes l, l + per_pixel, ... share a channel vector
+    for (int c = threadIdx.x; c < a.channels; c += 256) {
+        const int cv = c / VEC, e = c % VEC;
+        float sum = 0.0f;
+        for (int l = cv; l < 256; l += per_pixel) sum += lane_sum[l][e];
+        partial[(int64_t)blockIdx.x * a.channels + c] = sum;
+    }
+}
+
+// d_bias[c] = sum over blocks of partial[b][c]: lanes add strided blocks in order, then a fixed
+// pairwise tree over the 256 lane sums.
+__global__ void __launch_bounds__(256) relu_pool_bias_combine_kernel(const float *__restrict__ partial,
+                                                                     int32_t blocks, int32_t channels,
+                                                                     float *__restrict__ out) {
+    __shared__ float s[256];
+    const int c = blockIdx.x;
+    float v = 0.0f;
+    for (int b = threadIdx.x; b < blocks; b += 256) v += partial[(int64_t)b * channels + c];
+    s[threadIdx.x] = v;
+    __syncthreads();
+    for (int half = 128; half > 0; half >>= 1) {
+        if ((int)threadIdx.x < half) s[threadIdx.x] = s[threadIdx.x] + s[threadIdx.x + half];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[c] = s[0];
 }
 
 // Bias-gradient chunks of the same d_pre without reading it: partial[q][c] sums rows
@@ -359,6 +437,24 @@ int axis_relu_pool_backward(axis_device device, const float *gradient, const flo
     const int v = vec ? 4 : 1;
     a.cvec = FastDiv((uint32_t)(channels / v));
     a.total = (uint32_t)(outer * a.out_h * a.out_w * (channels / v));
+    if (d_bias && 256 % (channels / v) == 0) {
+        // bias folded into the scatter: blocks of whole 256-vector strides, one partial each
+        const int64_t blocks = std::min<int64_t>((a.total + 255) / 256, (int64_t)device->multiprocessors * 8);
+        const uint32_t span = (uint32_t)(((a.total + blocks - 1) / blocks + 255) / 256 * 256);
+        const int32_t nb = (int32_t)((a.total + span - 1) / span);
+        axis::Scratch partial;
+        if (int s = partial.get(device, sizeof(float) * (size_t)nb * (size_t)channels)) return s;
+        if (vec)
+            relu_pool_backward_bias_kernel<4><<<nb, 256, 0, device->stream>>>(gradient, pooled, argmax, d_pre,
+                                                                            partial.as<float>(), span, a);
+        else
+            relu_pool_backward_bias_kernel<1><<<nb, 256, 0, device->stream>>>(gradient, pooled, argmax, d_pre,
+                                                                            partial.as<float>(), span, a);
+        if (int s = axis::launch_status("relu_pool_backward_bias_kernel")) return s;
+        relu_pool_bias_combine_kernel<<<(unsigned)channels, 256, 0, device->stream>>>(partial.as<float>(), nb,
+                                                                                     channels, d_bias);
+        return axis::launch_status("relu_pool_bias_combine_kernel");
+    }
     if (vec)
         relu_pool_backward_kernel<4><<<axis::blocks_for(a.total, 256, INT32_MAX), 256, 0, device->stream>>>(
             gradient, pooled, argmax, d_pre, a);

@@ -304,8 +304,9 @@ int axis_conv2d_backward_weight(axis_device device, const float *input,
  * mask, col2im, tensor.rs:5679-5683; Rule::Relu, tensor.rs:2136-2147): d_pre
  * [outer, height, width, channels] holds 0.0f + gradient at each window's winner when the pooled
  * value is > 0, and 0 elsewhere -- exactly axis_max_pool2d_backward then axis_relu_backward.
- * d_bias (or NULL) receives the column sums of d_pre in the order of axis_bias_gradient.
- * height % pool[0] == 0 and width % pool[1] == 0. */
+ * d_bias (or NULL) receives the column sums of d_pre in a fixed association (identical on every
+ * run; equal to axis_bias_gradient's chunked order to fp32 tolerance, bit for bit when 256 is not
+ * a multiple of the channel-vector count).  height % pool[0] == 0 and width % pool[1] == 0. */
 int axis_relu_pool_backward(axis_device device, const float *gradient, const float *pooled,
                             const uint8_t *argmax, float *d_pre, float *d_bias, int64_t outer,
                             int32_t height, int32_t width, int32_t channels, const int32_t pool[2]);
