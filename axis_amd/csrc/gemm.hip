@@ -54,6 +54,8 @@ struct GemmParams {
     const float *y;
     float *c;
     const float *bias;         // added to every row of C (length n), or null
+    const float *d;            // out = beta * d + alpha * (A.B) when non-null (d shaped like out)
+    float alpha, beta;
     int64_t m, n, k;           // C is [m, n]; reduction length k
     int64_t x_si, x_sr;        // dense X(i, r) = x[i * x_si + r * x_sr]
     int64_t y_sr, y_sj;        // Y(r, j) = y[r * y_sr + j * y_sj]
@@ -276,6 +278,21 @@ struct ConvColsLoader : Staging<BT, BK, NT, false, VEC> {
     }
 };
 
+// Finishes one output value v (the whole reduction) at flat output index idx: + bias[col], then
+// beta * d + alpha * v.  Each product and the sum round separately, as the separate scale / scale
+// / add operations they replace.
+__device__ __forceinline__ float finish_value(const float *bias, const float *d, float alpha, float beta,
+                                              float v, int64_t idx, int64_t col) {
+#pragma clang fp contract(off)
+    if (bias) v = v + bias[col];
+    if (d) {
+        const float t1 = beta * d[idx];
+        const float t2 = alpha * v;
+        v = t1 + t2;
+    }
+    return v;
+}
+
 // XMODE: 0 dense X, 1 convolution rows mode, 2 convolution cols mode.
 // EPI: 0 store C (+ bias), 1 bias + ReLU + max pool of whole windows (rows are output pixels).
 template <int BM, int BN, int BK, int WM, int WN, bool XR, bool YR, int VX, int VY, int XMODE, int EPI>
@@ -387,23 +404,27 @@ __global__ void __launch_bounds__(WM *WN * 64)
     auto col_in = [](int b, int l) { return FN == 2 ? 2 * l + b : b * 32 + l; };
     if constexpr (EPI == 0) {
         float *c = p.c + batch * p.c_batch + (int64_t)split * p.c_split;
-        const bool with_bias = p.bias != nullptr && p.splits == 1;
+        // bias / axpby apply to whole sums only; split sums finish them at the end
+        const bool whole = p.splits == 1;
+        const float *bias = whole ? p.bias : nullptr;
+        const float *d = whole ? p.d : nullptr;
+        const int64_t out_base = batch * p.m * p.n;
         if (FN == 2 && (p.n & 1) == 0) {
             // the two column blocks of a lane are adjacent columns: one 8-byte store per row
             const int64_t col = j0 + wn * TN + 2 * l32;
             if (col < p.n) {
-                const float add0 = with_bias ? p.bias[col] : 0.0f;
-                const float add1 = with_bias ? p.bias[col + 1] : 0.0f;
 #pragma unroll
                 for (int a = 0; a < FM; ++a)
 #pragma unroll
                     for (int v = 0; v < 16; ++v) {
                         const int64_t row = i0 + wm * TM + row_in(a, (v >> 2) * 8 + half * 4 + (v & 3));
                         if (row < p.m) {
+                            const int64_t idx = row * p.n + col;
                             float2 o;
-                            o.x = with_bias ? acc[a][0][v] + add0 : acc[a][0][v];
-                            o.y = with_bias ? acc[a][FN - 1][v] + add1 : acc[a][FN - 1][v];
-                            *reinterpret_cast<float2 *>(c + row * p.n + col) = o;
+                            o.x = finish_value(bias, d, p.alpha, p.beta, acc[a][0][v], out_base + idx, col);
+                            o.y = finish_value(bias, d, p.alpha, p.beta, acc[a][FN - 1][v], out_base + idx + 1,
+                                               col + 1);
+                            *reinterpret_cast<float2 *>(c + idx) = o;
                         }
                     }
             }
@@ -414,11 +435,12 @@ __global__ void __launch_bounds__(WM *WN * 64)
                 for (int b = 0; b < FN; ++b) {
                     const int64_t col = j0 + wn * TN + col_in(b, l32);
                     if (col >= p.n) continue;
-                    const float add = with_bias ? p.bias[col] : 0.0f;
 #pragma unroll
                     for (int v = 0; v < 16; ++v) {
                         const int64_t row = i0 + wm * TM + row_in(a, (v >> 2) * 8 + half * 4 + (v & 3));
-                        if (row < p.m) c[row * p.n + col] = with_bias ? acc[a][b][v] + add : acc[a][b][v];
+                        if (row < p.m)
+                            c[row * p.n + col] =
+                                finish_value(bias, d, p.alpha, p.beta, acc[a][b][v], out_base + row * p.n + col, col);
                     }
                 }
         }
@@ -483,7 +505,9 @@ __global__ void __launch_bounds__(WM *WN * 64)
 __global__ void __launch_bounds__(256) split_sum_kernel(const float *__restrict__ partial,
                                                         float *__restrict__ out, int64_t len,
                                                         int32_t splits, int64_t split_stride,
-                                                        const float *__restrict__ bias, int64_t n) {
+                                                        const float *__restrict__ bias, int64_t n,
+                                                        const float *__restrict__ d, float alpha,
+                                                        float beta) {
     __shared__ float acc[4][64];
     const int lane = threadIdx.x & 63, group = threadIdx.x >> 6;
     const int64_t i = (int64_t)blockIdx.x * 64 + lane;
@@ -494,7 +518,7 @@ __global__ void __launch_bounds__(256) split_sum_kernel(const float *__restrict_
     __syncthreads();
     if (group == 0 && i < len) {
         const float total = ((acc[0][lane] + acc[1][lane]) + acc[2][lane]) + acc[3][lane];
-        out[i] = bias ? total + bias[i % n] : total;
+        out[i] = finish_value(bias, d, alpha, beta, total, i, i % n);
     }
 }
 
@@ -633,10 +657,11 @@ Choice choose(int64_t m, int64_t n, int64_t batch, int64_t cus, bool pool_epilog
 // Deterministic sum of reduction slices (+ bias): up to 32 slices in one pass; beyond that, ranges
 // of 32 consecutive slices first, then the range sums -- a fixed association for a given count.
 int sum_splits(axis_device device, const float *partial, float *out, int64_t len, int64_t splits,
-               const float *bias, int64_t n) {
+               const float *bias, int64_t n, const float *d, float alpha, float beta) {
     const unsigned blocks = axis::blocks_for(len, 64, INT32_MAX);
     if (splits <= 32) {
-        split_sum_kernel<<<blocks, 256, 0, device->stream>>>(partial, out, len, (int32_t)splits, len, bias, n);
+        split_sum_kernel<<<blocks, 256, 0, device->stream>>>(partial, out, len, (int32_t)splits, len, bias, n, d,
+                                                             alpha, beta);
         return axis::launch_status("split_sum_kernel");
     }
     const int32_t span = 32;
@@ -646,7 +671,8 @@ int sum_splits(axis_device device, const float *partial, float *out, int64_t len
     dim3 grid(axis::blocks_for(len, 256, INT32_MAX), (unsigned)ranges);
     split_range_kernel<<<grid, 256, 0, device->stream>>>(partial, mid.as<float>(), len, (int32_t)splits, span);
     if (int st = axis::launch_status("split_range_kernel")) return st;
-    split_sum_kernel<<<blocks, 256, 0, device->stream>>>(mid.as<float>(), out, len, (int32_t)ranges, len, bias, n);
+    split_sum_kernel<<<blocks, 256, 0, device->stream>>>(mid.as<float>(), out, len, (int32_t)ranges, len, bias, n,
+                                                         d, alpha, beta);
     return axis::launch_status("split_sum_kernel");
 }
 
@@ -719,7 +745,8 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out) {
     }
     int status = axis::launch_status("gemm_kernel");
     if (status) return status;
-    if (splits > 1) status = sum_splits(device, partial.as<float>(), out, out_len, splits, p.bias, p.n);
+    if (splits > 1)
+        status = sum_splits(device, partial.as<float>(), out, out_len, splits, p.bias, p.n, p.d, p.alpha, p.beta);
     return status;
 }
 
@@ -875,6 +902,30 @@ int axis_matmul(axis_device device, const float *a, const float *b, float *out, 
     GemmParams p{};
     p.x = a;
     p.y = b;
+    p.m = m;
+    p.n = n;
+    p.k = k;
+    p.x_si = k;
+    p.x_sr = 1;
+    p.y_sr = n;
+    p.y_sj = 1;
+    p.x_batch = m * k;
+    p.y_batch = k * n;
+    return run_gemm<true, false, 0, 0>(device, p, batch, out);
+}
+
+int axis_matmul_axpby(axis_device device, const float *a, const float *b, const float *d, float *out,
+                      int64_t batch, int64_t m, int64_t k, int64_t n, float alpha, float beta) {
+    AXIS_ENTER(device);
+    if (int s = check_dims(a, b, out, batch, m, k, n)) return s;
+    AXIS_REQUIRE(d, "null axpby addend");
+    AXIS_REQUIRE(d != out, "axpby addend must not alias the output");
+    GemmParams p{};
+    p.x = a;
+    p.y = b;
+    p.d = d;
+    p.alpha = alpha;
+    p.beta = beta;
     p.m = m;
     p.n = n;
     p.k = k;

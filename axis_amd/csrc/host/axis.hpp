@@ -144,6 +144,9 @@ class Device {
     Buffer matmul(const Buffer &a, const Buffer &b, int64_t batch, int64_t m, int64_t k, int64_t n) const;
     Buffer matmul_left_backward(const Buffer &g, const Buffer &rhs, int64_t batch, int64_t m,
                                 int64_t k, int64_t n) const;
+    // beta * d + alpha * (a . b), each product and the sum rounded once (Newton-Schulz steps)
+    Buffer matmul_axpby(const Buffer &a, const Buffer &b, const Buffer &d, int64_t batch, int64_t m,
+                        int64_t k, int64_t n, float alpha, float beta) const;
     Buffer matmul_right_backward(const Buffer &lhs, const Buffer &g, int64_t batch, int64_t m,
                                  int64_t k, int64_t n) const;
     Buffer unfold(const Buffer &input, const axis_unfold_spec &spec) const;

@@ -247,6 +247,14 @@ Buffer Device::matmul_left_backward(const Buffer &g, const Buffer &rhs, int64_t 
     return out;
 }
 
+Buffer Device::matmul_axpby(const Buffer &a, const Buffer &b, const Buffer &d, int64_t batch, int64_t m,
+                            int64_t k, int64_t n, float alpha, float beta) const {
+    Buffer out = alloc(batch * m * n);
+    check(axis_matmul_axpby(h(), a->f32(), b->f32(), d->f32(), out->f32(), batch, m, k, n, alpha, beta),
+          "matmul_axpby");
+    return out;
+}
+
 Buffer Device::matmul_right_backward(const Buffer &lhs, const Buffer &g, int64_t batch, int64_t m,
                                      int64_t k, int64_t n) const {
     Buffer out = alloc(batch * k * n);

@@ -58,7 +58,7 @@ Adam::Prepared Adam::prepare(const std::vector<Parameter> &parameters) const {
         unique.push_back(p);
     }
     if (unique.empty()) return prepared;
-    const Device &dev = unique.front().tensor().device();
+    const Device dev = unique.front().tensor().device();
     std::vector<axis_adam_tensor> in_place;
     for (auto &p : unique) {
         const Tensor t = p.tensor();
@@ -218,6 +218,23 @@ Tensor zeroth_power(const Tensor &matrix) {
     Axis inner = small.role("muon_ns_inner");
     Axis output = small.role("muon_ns_output");
     Tensor x = matrix.normalized_l2(kNormalizationEpsilon);
+    if (!x.requires_grad()) {
+        // No gradient flows through the orthogonalisation, so the iteration runs on x held
+        // [small, large] row-major: gram = x.x^T through the NT kernel (no transpose copy), and each
+        // scale-and-add folds into its product's epilogue with the same roundings:
+        //   b  = kNsB * gram + kNsC * (gram . gram)      (gram_squared of the lowering below)
+        //   x' = kNsA * x + b . x
+        if (!(x.layout() == Layout::make(x.shape(), {small, large}))) x = x.with_layout({small, large});
+        const Device dev = x.device();  // a copy: x is reassigned below
+        const int64_t s = x.extent(small), l = x.extent(large);
+        for (int i = 0; i < kNsSteps; ++i) {
+            Tensor gram = x.contract(x.rename(small, inner), {large});
+            Buffer b = dev.matmul_axpby(gram.value(), gram.value(), gram.value(), 1, s, s, s, kNsC, kNsB);
+            Buffer next = dev.matmul_axpby(b, x.value(), x.value(), 1, s, s, l, 1.0f, kNsA);
+            x = Tensor::node(x.shape(), x.layout(), next, dev, {}, false);
+        }
+        return x;
+    }
     for (int i = 0; i < kNsSteps; ++i) {
         Tensor gram = x.contract(x.rename(small, inner), {large});
         Tensor gram_rhs = gram.rename(inner, output).rename(small, inner);

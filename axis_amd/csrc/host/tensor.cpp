@@ -448,11 +448,40 @@ Tensor Tensor::contract(const Tensor &rhs, const std::vector<Axis> &axes_in) con
         Layout l = Layout::make(t.shape(), order);
         return t.layout() == l ? t : t.with_layout(order);
     };
-    Tensor left = ordered(*this, left_order), right = ordered(rhs, right_order);
+    auto laid_out = [](const Tensor &t, const std::vector<Axis> &order) {
+        return t.layout() == Layout::make(t.shape(), order);
+    };
     int64_t batch = 1, m = 1, n = 1;
     for (auto &a : batch_axes) batch *= extent(a);
     for (auto &a : left_axes) m *= extent(a);
     for (auto &a : right_axes) n *= rhs.extent(a);
+    std::vector<Axis> output_order = batch_axes;
+    output_order.insert(output_order.end(), left_axes.begin(), left_axes.end());
+    output_order.insert(output_order.end(), right_axes.begin(), right_axes.end());
+    // An untracked product (no gradient rules to save) reads a transposed operand in place: a
+    // contraction-major lhs through the TN kernel, a contraction-minor rhs through the NT kernel
+    // (matmul_right_backward / matmul_left_backward compute exactly those products, in the same
+    // reduction order).  Tracked products keep the reference's [batch, m, k] x [batch, k, n] operands
+    // because their saved rules assume that layout.
+    if (!requires_grad() && !rhs.requires_grad()) {
+        std::vector<Axis> left_t = batch_axes, right_t = batch_axes;
+        left_t.insert(left_t.end(), axes.begin(), axes.end());
+        left_t.insert(left_t.end(), left_axes.begin(), left_axes.end());
+        right_t.insert(right_t.end(), right_axes.begin(), right_axes.end());
+        right_t.insert(right_t.end(), axes.begin(), axes.end());
+        const bool lhs_plain = laid_out(*this, left_order), rhs_plain = laid_out(rhs, right_order);
+        Buffer value;
+        if (!lhs_plain && laid_out(*this, left_t)) {
+            Tensor right = ordered(rhs, right_order);
+            value = device().matmul_right_backward(this->value(), right.value(), batch, k, m, n);
+        } else if (!rhs_plain && laid_out(rhs, right_t)) {
+            Tensor left = ordered(*this, left_order);
+            value = device().matmul_left_backward(left.value(), rhs.value(), batch, m, n, k);
+        }
+        if (value)
+            return node(out_shape, Layout::make(out_shape, output_order), value, device(), {}, false);
+    }
+    Tensor left = ordered(*this, left_order), right = ordered(rhs, right_order);
     Buffer value = device().matmul(left.value(), right.value(), batch, m, k, n);
     std::vector<Edge> edges;
     if (left.requires_grad()) {
@@ -467,9 +496,6 @@ Tensor Tensor::contract(const Tensor &rhs, const std::vector<Axis> &axes_in) con
         r.batch = batch, r.m = m, r.k = k, r.n = n;
         edges.push_back(Edge{right, r});
     }
-    std::vector<Axis> output_order = batch_axes;
-    output_order.insert(output_order.end(), left_axes.begin(), left_axes.end());
-    output_order.insert(output_order.end(), right_axes.begin(), right_axes.end());
     return node(out_shape, Layout::make(out_shape, output_order), value, device(), std::move(edges),
                 false);
 }

@@ -84,6 +84,12 @@ int axis_timing_read(axis_device device, const char *family, int64_t *launches, 
  * out [batch,m,n], all row-major.  fp32 on MFMA. */
 int axis_matmul(axis_device device, const float *a, const float *b, float *out, int64_t batch,
                 int64_t m, int64_t k, int64_t n);
+/* out[b] = beta * d[b] + alpha * (a[b] . b[b]) for row-major [m,k] x [k,n] (d and out [m,n], d not
+ * aliasing out): the Newton-Schulz steps of Muon::zeroth_power (optim.rs:728-752),
+ * `gram.scale(b).add(gram2.scale(c))` and `x.scale(a).add(b.x)`, with the product's scale, the
+ * addend's scale and the sum each rounded once, as the separate operations round them. */
+int axis_matmul_axpby(axis_device device, const float *a, const float *b, const float *d, float *out,
+                      int64_t batch, int64_t m, int64_t k, int64_t n, float alpha, float beta);
 /* Device::matmul_left_backward (backend.rs:958-989), dgrad: out[b] = gradient[b] . rhs[b]^T;
  * gradient [batch,m,n], rhs [batch,k,n], out [batch,m,k]. */
 int axis_matmul_left_backward(axis_device device, const float *gradient, const float *rhs,

@@ -578,3 +578,34 @@ def test_relu_pool_backward_bit_exact(dev, oracle, b, h, w, c, pool):
     dev.call("axis_relu_pool_backward", dg.vp, pooled.vp, arg.vp, d_pre.vp, d_bias2.vp, I64(b), I32(h), I32(w),
              I32(c), win)
     assert np.array_equal(dev.read(d_bias2, c).view(np.uint32), got_db.view(np.uint32))
+
+
+@pytest.mark.parametrize("batch,m,k,n", [(1, 256, 256, 256), (1, 64, 4096, 96), (2, 130, 70, 33), (1, 512, 512, 1024)])
+def test_matmul_axpby_equals_separate_operations(dev, oracle, batch, m, k, n):
+    rng = np.random.default_rng(m + k + n)
+    a = rng.standard_normal(batch * m * k).astype(np.float32)
+    b = rng.standard_normal(batch * k * n).astype(np.float32)
+    d = rng.standard_normal(batch * m * n).astype(np.float32)
+    alpha, beta = 2.0315, -4.7750
+    da, db, dd = up(dev, a), up(dev, b), up(dev, d)
+    fused = dev.empty(batch * m * n)
+    dev.call("axis_matmul_axpby", da.vp, db.vp, dd.vp, fused.vp, I64(batch), I64(m), I64(k), I64(n), F32(alpha),
+             F32(beta))
+    got = dev.read(fused, batch * m * n)
+    # the same arithmetic through the separate entries: bit-identical
+    prod, t1, t2, summed = (dev.empty(batch * m * n) for _ in range(4))
+    dev.call("axis_matmul", da.vp, db.vp, prod.vp, I64(batch), I64(m), I64(k), I64(n))
+    dev.call("axis_scale", dd.vp, F32(beta), t1.vp, I64(batch * m * n))
+    dev.call("axis_scale", prod.vp, F32(alpha), t2.vp, I64(batch * m * n))
+    dev.call("axis_binary", t1.vp, t2.vp, I32(0), summed.vp, I64(batch * m * n))
+    assert np.array_equal(got.view(np.uint32), dev.read(summed, batch * m * n).view(np.uint32))
+    # and the oracle to GEMM tolerance
+    ref = oracle.binary(oracle.scale(d, beta), oracle.scale(oracle.matmul(a, b, batch, m, k, n), alpha), 0)
+    assert rel_err(got, ref) < 1e-5
+
+
+def test_matmul_axpby_rejects_aliasing(dev):
+    buf = dev.empty(16)
+    with pytest.raises(hip.AxisError, match="alias"):
+        dev.call("axis_matmul_axpby", buf.vp, buf.vp, buf.vp, buf.vp, I64(1), I64(4), I64(4), I64(4), F32(1.0),
+                 F32(1.0))
