@@ -376,3 +376,104 @@ def test_cnn_full_config_invariants(ax, device, oracle):
         delta = np.abs(model.parameter(ours).tensor().to_vec() - params[mapping[ours]])
         assert delta.max() <= 1e-3 * 1.0001, ours
     assert abs(float(grads["1.bias"].astype(np.float64).sum())) < 1e-5
+
+
+# ---------------------------------------------------------------- convolution block lowerings
+
+def _torch_block(x_nchw, weight, bias, kh, kw, stride, pad, pool):
+    """Reference forward in float64 on the CPU: conv2d -> relu -> optional max pool."""
+    import torch
+    xt = torch.tensor(x_nchw, dtype=torch.float64, requires_grad=True)
+    wt = torch.tensor(weight, dtype=torch.float64, requires_grad=True)
+    bt = torch.tensor(bias, dtype=torch.float64, requires_grad=True)
+    y = torch.nn.functional.conv2d(xt, wt, bt, stride=stride, padding=pad).relu()
+    if pool is not None:
+        k, s, p = pool
+        y = torch.nn.functional.max_pool2d(y, k, s, p)
+    return xt, wt, bt, y
+
+
+BLOCK_CASES = [
+    # input layout, x requires grad, conv stride, pool (kernel, stride, padding) -- and which lowering runs
+    ("nhwc", True, 1, (2, 2, 0)),   # fused Conv2d+ReLU+MaxPool2d
+    ("nhwc", True, 1, (3, 2, 1)),   # implicit conv, then separate ReLU and overlapping pool
+    ("nhwc", True, 2, (2, 2, 0)),   # strided conv with an input gradient: the explicit unfold lowering
+    ("nhwc", False, 2, (2, 2, 0)),  # strided conv without one: implicit forward + wgrad, fused block
+    ("nchw", True, 1, (2, 2, 0)),   # channel-major input needing its gradient: explicit lowering
+    ("nchw", False, 1, (2, 2, 0)),  # channel-major input without one: repacked implicit conv, fused
+]
+
+
+@pytest.mark.parametrize("case", range(len(BLOCK_CASES)))
+def test_conv_relu_pool_block_lowerings(ax, device, case):
+    layout, needs_grad, stride, pool = BLOCK_CASES[case]
+    b, c, hh, ww, out, k = 2, 5, 16, 16, 16, 3
+    rng = np.random.default_rng(100 + case)
+    x_nchw = rng.standard_normal((b, c, hh, ww))
+    weight = rng.standard_normal((out, c, k, k)) * 0.3
+    bias = rng.standard_normal(out) * 0.1
+    bt_, ch, h, w, o = ax.Axis("batch"), ax.Axis("channel"), ax.Axis("height"), ax.Axis("width"), ax.Axis("out")
+    if layout == "nhwc":
+        dims = [bt_.of(b), h.of(hh), w.of(ww), ch.of(c)]
+        x_host = x_nchw.transpose(0, 2, 3, 1)
+    else:
+        dims = [bt_.of(b), ch.of(c), h.of(hh), w.of(ww)]
+        x_host = x_nchw
+    x = ax.Tensor.from_slice(np.ascontiguousarray(x_host, np.float32).reshape(-1), dims, device)
+    if needs_grad:
+        x = x.with_grad()
+    conv = ax.Conv2d(ch, o.of(out), [h, w], [k, k]).padding([1, 1]).stride([stride, stride])
+    mp = ax.MaxPool2d(o, [h, w], [pool[0], pool[0]]).stride([pool[1], pool[1]]).padding([pool[2], pool[2]])
+    model = ax.Sequential([conv, ax.ReLU(), mp])
+    model.build(x.shape, device, 3)
+    # the reference's weight layout [(c, ky, kx), out]
+    conv.parameter("weight").set_values(np.ascontiguousarray(weight.transpose(1, 2, 3, 0), np.float32).reshape(-1))
+    conv.parameter("bias").set_values(bias.astype(np.float32))
+    y = model.forward(x)
+    xt, wt, btt, yt = _torch_block(x_nchw, weight, bias, k, k, stride, 1, pool)
+    y_ref = yt.detach().numpy().transpose(0, 2, 3, 1)  # outputs are channel-innermost
+    assert y.shape == ax.Shape([bt_.of(b), h.of(y_ref.shape[1]), w.of(y_ref.shape[2]), o.of(out)])
+    assert rel_max(y.to_vec(), y_ref.reshape(-1)) < 1e-5
+    r = rng.standard_normal(y_ref.shape)
+    rt = ax.Tensor.from_slice(r.astype(np.float32).reshape(-1), [bt_.of(b), h.of(r.shape[1]), w.of(r.shape[2]), o.of(out)],
+                              device)
+    y.mul(rt).sum([bt_, h, w, o]).backward()
+    import torch
+    (yt * torch.tensor(r.transpose(0, 3, 1, 2), dtype=torch.float64)).sum().backward()
+    gw = np.asarray(conv.parameter("weight").grad().to_vec())
+    assert rel_max(gw, wt.grad.numpy().transpose(1, 2, 3, 0).reshape(-1)) < 1e-4
+    assert rel_max(conv.parameter("bias").grad().to_vec(), btt.grad.numpy()) < 1e-4
+    if needs_grad:
+        gx = xt.grad.numpy()
+        gx = gx.transpose(0, 2, 3, 1) if layout == "nhwc" else gx
+        assert rel_max(x.grad().to_vec(), gx.reshape(-1)) < 1e-4
+    else:
+        assert x.grad() is None
+
+
+@pytest.mark.parametrize("lhs_t,rhs_t,tracked", [(False, True, False), (True, False, False), (True, True, False),
+                                                 (False, True, True), (True, False, True)])
+def test_contract_reads_transposed_operands(ax, device, lhs_t, rhs_t, tracked):
+    # untracked products read a transposed operand in place (NT / TN kernels); tracked ones keep the
+    # reference's operand layouts for their saved rules -- same values either way
+    i, kk, j = ax.Axis("i"), ax.Axis("k"), ax.Axis("j")
+    m, k, n = 96, 80, 72
+    rng = np.random.default_rng(7)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    la = ax.Tensor.from_slice(a.reshape(-1), [i.of(m), kk.of(k)], device)
+    lb = ax.Tensor.from_slice(b.reshape(-1), [kk.of(k), j.of(n)], device)
+    if tracked:
+        la, lb = la.with_grad(), lb.with_grad()
+    ta = la.with_layout([kk, i]) if lhs_t else la
+    tb = lb.with_layout([j, kk]) if rhs_t else lb
+    y = ta.contract(tb, [kk])
+    ref = a.astype(np.float64) @ b.astype(np.float64)
+    assert y.shape == ax.Shape([i.of(m), j.of(n)])
+    assert rel_max(y.to_vec(), ref.reshape(-1)) < 1e-5
+    if tracked:
+        g = rng.standard_normal((m, n)).astype(np.float32)
+        tg = ax.Tensor.from_slice(g.reshape(-1), [i.of(m), j.of(n)], device)
+        y.mul(tg).sum([i, j]).backward()
+        assert rel_max(la.grad().to_vec(), (g.astype(np.float64) @ b.T.astype(np.float64)).reshape(-1)) < 1e-4
+        assert rel_max(lb.grad().to_vec(), (a.T.astype(np.float64) @ g.astype(np.float64)).reshape(-1)) < 1e-4
