@@ -357,36 +357,46 @@ __global__ void __launch_bounds__(WM *WN * 64)
 
     const int half = lane >> 5;  // which k of the pair this lane feeds
     const int l32 = lane & 31;
+    // MFMA operands of one k pair.  With two 32-blocks per wave side, block a takes rows 2i + a,
+    // so both operands are one 8-byte LDS read at an immediate offset from a single base.
+    auto read_operands = [&](int kk, float *av, float *bv) {
+        if constexpr (FM == 2) {
+            const float2 v = *reinterpret_cast<const float2 *>(xs + (kk + half) * LX::LD + wm * TM + 2 * l32);
+            av[0] = v.x, av[1] = v.y;
+        } else {
+#pragma unroll
+            for (int a = 0; a < FM; ++a) av[a] = xs[(kk + half) * LX::LD + wm * TM + a * 32 + l32];
+        }
+        if constexpr (FN == 2) {
+            const float2 v = *reinterpret_cast<const float2 *>(ys + (kk + half) * LY::LD + wn * TN + 2 * l32);
+            bv[0] = v.x, bv[1] = v.y;
+        } else {
+#pragma unroll
+            for (int b = 0; b < FN; ++b) bv[b] = ys[(kk + half) * LY::LD + wn * TN + b * 32 + l32];
+        }
+    };
     for (int64_t r0 = r_begin; r0 < r_end; r0 += BK) {
         const bool more = r0 + BK < r_end;
         if (more) {
             lx.load(p.conv, r0 + BK, r_end, tid);
             ly.load(p.conv, r0 + BK, r_end, tid);
         }
+        // The operands of the next k pair are read before this pair's MFMAs issue, and the
+        // scheduling barriers keep that order: each LDS read has a whole MFMA group to land
+        // (left to itself the compiler sinks every read to just before its use).
+        float av[2][FM], bv[2][FN];
+        read_operands(0, av[0], bv[0]);
 #pragma unroll
         for (int kk = 0; kk < BK; kk += 2) {
-            float av[FM], bv[FN];
-            // With two 32-blocks per wave side, block a takes rows 2i + a, so both operands are
-            // one 8-byte LDS read at an immediate offset from a single base.
-            if constexpr (FM == 2) {
-                const float2 v = *reinterpret_cast<const float2 *>(xs + (kk + half) * LX::LD + wm * TM + 2 * l32);
-                av[0] = v.x, av[1] = v.y;
-            } else {
-#pragma unroll
-                for (int a = 0; a < FM; ++a) av[a] = xs[(kk + half) * LX::LD + wm * TM + a * 32 + l32];
-            }
-            if constexpr (FN == 2) {
-                const float2 v = *reinterpret_cast<const float2 *>(ys + (kk + half) * LY::LD + wn * TN + 2 * l32);
-                bv[0] = v.x, bv[1] = v.y;
-            } else {
-#pragma unroll
-                for (int b = 0; b < FN; ++b) bv[b] = ys[(kk + half) * LY::LD + wn * TN + b * 32 + l32];
-            }
+            const int cur = (kk / 2) & 1;
+            if (kk + 2 < BK) read_operands(kk + 2, av[cur ^ 1], bv[cur ^ 1]);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int a = 0; a < FM; ++a)
 #pragma unroll
                 for (int b = 0; b < FN; ++b)
-                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[a], bv[b], acc[a][b], 0, 0, 0);
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[cur][a], bv[cur][b], acc[a][b], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
         }
         __syncthreads();
         if (more) {
