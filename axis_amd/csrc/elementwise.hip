@@ -5,6 +5,7 @@
 // tail; reductions keep the reference's association (sequential chunks of 512, then chunk
 // partials in order) so they are bit-identical to a sequential restatement.  Built with
 // -ffp-contract=off: every expression rounds exactly as written.
+#include <algorithm>
 #include <cfloat>
 
 #include "common.hpp"
@@ -166,6 +167,141 @@ __global__ void __launch_bounds__(kBlock) select_axis_backward_kernel(const floa
             index += (int64_t)c * a.far[d];
     }
     out[i] = live ? gradient[index] : 0.0f;
+}
+
+// A permutation copy whose destination-innermost dim is strided in the source while another dim
+// is source-contiguous goes through LDS 64 x 64 tiles: the tile is read along the source's
+// contiguous dim (J) and written along the destination's (T), so both sides move whole cache
+// lines.  Remaining dims are batch dims, one per grid row.
+constexpr int kTile = 64;
+constexpr int kMaxBatchDims = 8;
+
+struct TransposeArgs {
+    int64_t base;                 // source offset of the selected coordinate
+    int64_t t_src;                // source stride of T (its destination stride is 1)
+    int64_t j_dst;                // destination stride of J (its source stride is 1)
+    int32_t t_extent, j_extent, tiles_t;
+    int32_t batch_dims;
+    int32_t b_extent[kMaxBatchDims];
+    int64_t b_src[kMaxBatchDims], b_dst[kMaxBatchDims];
+};
+
+__global__ void __launch_bounds__(256) transpose_copy_kernel(const float *__restrict__ src,
+                                                             float *__restrict__ dst, TransposeArgs a) {
+    __shared__ float tile[kTile][kTile + 1];
+    const int t0 = (int)(blockIdx.x % (uint32_t)a.tiles_t) * kTile;
+    const int j0 = (int)(blockIdx.x / (uint32_t)a.tiles_t) * kTile;
+    uint32_t b = blockIdx.y;
+    int64_t s_off = a.base, d_off = 0;
+    for (int d = a.batch_dims - 1; d >= 0; --d) {
+        const uint32_t c = b % (uint32_t)a.b_extent[d];
+        b /= (uint32_t)a.b_extent[d];
+        s_off += (int64_t)c * a.b_src[d];
+        d_off += (int64_t)c * a.b_dst[d];
+    }
+    const int lane = threadIdx.x & 63, row = threadIdx.x >> 6;
+    const int j = j0 + lane;
+#pragma unroll 4
+    for (int tt = row; tt < kTile; tt += 4) {
+        const int t = t0 + tt;
+        if (j < a.j_extent && t < a.t_extent) tile[tt][lane] = src[s_off + j + (int64_t)t * a.t_src];
+    }
+    __syncthreads();
+    const int t = t0 + lane;
+#pragma unroll 4
+    for (int jj = row; jj < kTile; jj += 4) {
+        const int jo = j0 + jj;
+        if (jo < a.j_extent && t < a.t_extent) dst[d_off + (int64_t)jo * a.j_dst + t] = tile[lane][jj];
+    }
+}
+
+// Canonical form of a select_axis copy: dims of extent > 1 sorted by destination stride (outer
+// first), runs contiguous on both sides merged, the selected coordinate folded into the source
+// base.  Returns false when the copy is not a plain permutation/broadcast onto a dense
+// destination (the backward of a selection, which zero-fills, is not).
+struct CopyDims {
+    int rank = 0;
+    int64_t extent[10], src[10], dst[10];
+    int64_t base = 0;
+};
+
+bool canonical_copy(const int32_t *metadata, int32_t rank, int32_t coordinate, bool forward, CopyDims *c) {
+    c->rank = 0;
+    c->base = 0;
+    for (int d = 0; d < rank; ++d) {
+        const int64_t extent = metadata[3 * d], in_stride = metadata[3 * d + 1], out_stride = metadata[3 * d + 2];
+        if (out_stride < 0) {
+            if (!forward) return false;
+            c->base += (int64_t)coordinate * in_stride;
+            continue;
+        }
+        if (extent == 1) continue;
+        c->extent[c->rank] = extent;
+        c->src[c->rank] = forward ? in_stride : out_stride;
+        c->dst[c->rank] = forward ? out_stride : in_stride;
+        ++c->rank;
+    }
+    for (int i = 1; i < c->rank; ++i)  // insertion sort, destination stride descending
+        for (int k = i; k > 0 && c->dst[k] > c->dst[k - 1]; --k) {
+            std::swap(c->extent[k], c->extent[k - 1]);
+            std::swap(c->src[k], c->src[k - 1]);
+            std::swap(c->dst[k], c->dst[k - 1]);
+        }
+    int merged = 0;
+    for (int i = 0; i < c->rank; ++i) {
+        if (merged > 0 && c->dst[merged - 1] == c->dst[i] * c->extent[i] &&
+            c->src[merged - 1] == c->src[i] * c->extent[i]) {
+            c->extent[merged - 1] *= c->extent[i];
+            c->src[merged - 1] = c->src[i];
+            c->dst[merged - 1] = c->dst[i];
+            continue;
+        }
+        c->extent[merged] = c->extent[i];
+        c->src[merged] = c->src[i];
+        c->dst[merged] = c->dst[i];
+        ++merged;
+    }
+    c->rank = merged;
+    int64_t expect = 1;
+    for (int i = c->rank - 1; i >= 0; --i) {
+        if (c->dst[i] != expect) return false;
+        expect *= c->extent[i];
+    }
+    return true;
+}
+
+// Launches the tiled transpose when the canonical copy has one; returns -1 when it does not.
+int try_transpose(axis_device device, const float *src, float *dst, const int32_t *metadata, int32_t rank,
+                  int32_t coordinate, bool forward) {
+    CopyDims c;
+    if (!canonical_copy(metadata, rank, coordinate, forward, &c) || c.rank < 2) return -1;
+    const int last = c.rank - 1;
+    if (c.src[last] == 1) return -1;  // rows already contiguous on both sides
+    int j = -1;
+    for (int i = 0; i < last; ++i)
+        if (c.src[i] == 1) j = i;
+    if (j < 0 || c.extent[last] < 16 || c.extent[j] < 16 || c.rank - 2 > kMaxBatchDims) return -1;
+    TransposeArgs a{};
+    a.base = c.base;
+    a.t_src = c.src[last];
+    a.j_dst = c.dst[j];
+    a.t_extent = (int32_t)c.extent[last];
+    a.j_extent = (int32_t)c.extent[j];
+    a.tiles_t = (a.t_extent + kTile - 1) / kTile;
+    const int64_t tiles_j = (a.j_extent + kTile - 1) / kTile;
+    int64_t batch = 1;
+    for (int i = 0; i < last; ++i) {
+        if (i == j) continue;
+        a.b_extent[a.batch_dims] = (int32_t)c.extent[i];
+        a.b_src[a.batch_dims] = c.src[i];
+        a.b_dst[a.batch_dims] = c.dst[i];
+        ++a.batch_dims;
+        batch *= c.extent[i];
+    }
+    if (batch > 65535 || a.tiles_t * tiles_j >= INT32_MAX) return -1;
+    dim3 grid((unsigned)(a.tiles_t * tiles_j), (unsigned)batch);
+    transpose_copy_kernel<<<grid, 256, 0, device->stream>>>(src, dst, a);
+    return axis::launch_status("transpose_copy_kernel");
 }
 
 int select_args(const int32_t *metadata, int32_t rank, int32_t coordinate, int64_t len, bool forward,
@@ -377,6 +513,8 @@ int axis_select_axis(axis_device device, const float *input, float *out, const i
     AXIS_REQUIRE(input && out, "null select_axis buffer");
     SelectArgs a{};
     if (int s = select_args(metadata, rank, coordinate, output_len, true, &a)) return s;
+    const int tiled = try_transpose(device, input, out, metadata, rank, coordinate, true);
+    if (tiled >= 0) return tiled;
     select_axis_kernel<<<axis::blocks_for(output_len, kBlock, INT32_MAX), kBlock, 0, device->stream>>>(
         input, out, a);
     return axis::launch_status("select_axis_kernel");
@@ -389,6 +527,8 @@ int axis_select_axis_backward(axis_device device, const float *gradient, float *
     AXIS_REQUIRE(gradient && out, "null select_axis_backward buffer");
     SelectArgs a{};
     if (int s = select_args(metadata, rank, coordinate, input_len, false, &a)) return s;
+    const int tiled = try_transpose(device, gradient, out, metadata, rank, coordinate, false);
+    if (tiled >= 0) return tiled;
     select_axis_backward_kernel<<<axis::blocks_for(input_len, kBlock, INT32_MAX), kBlock, 0,
                                   device->stream>>>(gradient, out, a);
     return axis::launch_status("select_axis_backward_kernel");

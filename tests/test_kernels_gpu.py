@@ -229,6 +229,78 @@ def test_select_axis_permutation_and_broadcast(dev, oracle):
     assert np.array_equal(dev.read(out2, 77), np.tile(bias, 11))
 
 
+def _permutation_metadata(shape, perm):
+    """with_layout's metadata (tensor.rs:5278-5333): per source dim (extent, source stride,
+    stride of that axis in the permuted row-major layout)."""
+    src = [int(np.prod(shape[i + 1:])) for i in range(len(shape))]
+    dst_shape = [shape[p] for p in perm]
+    dst_of_axis = {perm[k]: int(np.prod(dst_shape[k + 1:])) for k in range(len(perm))}
+    md = []
+    for i, e in enumerate(shape):
+        md += [e, src[i], dst_of_axis[i]]
+    return np.array(md, np.int32)
+
+
+# Copies whose destination-innermost dim is strided in the source take the LDS-tiled transpose
+# (tails, batch dims, unit dims merged away); the rest keep the per-element copier.
+TRANSPOSE_CASES = [
+    ((70, 130), (1, 0)),
+    ((64, 64), (1, 0)),
+    ((17, 16), (1, 0)),
+    ((5, 33, 100), (2, 0, 1)),
+    ((5, 33, 100), (1, 2, 0)),
+    ((5, 33, 100), (0, 2, 1)),
+    ((5, 33, 100), (2, 1, 0)),
+    ((3, 1, 40, 2, 65), (4, 1, 2, 3, 0)),
+    ((6, 7, 20, 48), (0, 3, 1, 2)),
+    ((8, 3, 5), (2, 1, 0)),
+]
+
+
+@pytest.mark.parametrize("shape,perm", TRANSPOSE_CASES)
+def test_select_axis_tiled_permutations(dev, oracle, shape, perm):
+    rng = np.random.default_rng(len(shape) * 100 + sum(shape))
+    n = int(np.prod(shape))
+    x = rng.standard_normal(n).astype(np.float32)
+    md = _permutation_metadata(shape, perm)
+    rank = len(shape)
+    dx, out, back = up(dev, x), dev.empty(n), dev.empty(n)
+    dev.call("axis_select_axis", dx.vp, out.vp, md.ctypes.data_as(VP), I32(rank), I32(0), I64(n))
+    got = dev.read(out, n)
+    assert np.array_equal(got, x.reshape(shape).transpose(perm).reshape(-1))
+    if n <= 1 << 16:
+        assert np.array_equal(got, oracle.select_axis(x, md, rank, 0, n))
+    dev.call("axis_select_axis_backward", out.vp, back.vp, md.ctypes.data_as(VP), I32(rank), I32(0), I64(n))
+    assert np.array_equal(dev.read(back, n), x)
+
+
+def test_select_axis_tiled_with_selected_coordinate(dev, oracle):
+    """Selecting one coordinate of a middle axis and transposing the rest in one copy."""
+    rng = np.random.default_rng(11)
+    a, b, c = 48, 5, 70
+    x = rng.standard_normal(a * b * c).astype(np.float32)
+    # output [c, a] = x[:, 3, :].T ; per output dim: (extent, input stride, output stride),
+    # the selected axis marked by output stride -1
+    md = np.array([c, 1, a, a, b * c, 1, b, c, -1], np.int32)
+    dx, out = up(dev, x), dev.empty(a * c)
+    dev.call("axis_select_axis", dx.vp, out.vp, md.ctypes.data_as(VP), I32(3), I32(3), I64(a * c))
+    got = dev.read(out, a * c)
+    assert np.array_equal(got, x.reshape(a, b, c)[:, 3, :].T.reshape(-1))
+    assert np.array_equal(got, oracle.select_axis(x, md, 3, 3, a * c))
+
+
+def test_select_axis_muon_sized_transpose(dev):
+    """The [8192, 4096] -> [4096, 8192] layout copy of Muon's Newton-Schulz input."""
+    rng = np.random.default_rng(12)
+    shape = (8192, 4096)
+    n = shape[0] * shape[1]
+    x = rng.standard_normal(n).astype(np.float32)
+    md = _permutation_metadata(shape, (1, 0))
+    dx, out = up(dev, x), dev.empty(n)
+    dev.call("axis_select_axis", dx.vp, out.vp, md.ctypes.data_as(VP), I32(2), I32(0), I64(n))
+    assert np.array_equal(dev.read(out, n), x.reshape(shape).T.reshape(-1))
+
+
 # ---------------------------------------------------------------- softmax / cross-entropy
 
 @pytest.mark.parametrize("rows,width", [(2, 3), (256, 1000), (5, 2049)])
