@@ -443,6 +443,107 @@ __global__ void __launch_bounds__(kBlock) reduce_middle_kernel(const float *__re
     out[t] = total * factor;
 }
 
+// ---------------------------------------------------------------- reductions over any axis set
+
+// Sum over any set of dims of a densely laid-out tensor, without an index plan.  The reduced
+// dims are walked in decreasing input stride (row-major over them), i.e. every group's
+// contributions in increasing memory position -- the order Plan::reverse lists them
+// (runtime/backend.rs:1577-1583) -- summed in chunks of 512, then the chunk partials in order,
+// then scaled (backend.rs:2964-3016).  The output is row-major over the kept dims in shape order.
+constexpr int kMaxReduceDims = 10;
+
+struct ReduceAxesArgs {
+    int32_t kept_rank, red_rank;
+    FastDiv kept_place[kMaxReduceDims], kept_extent[kMaxReduceDims];
+    int64_t kept_src[kMaxReduceDims];
+    FastDiv red_place[kMaxReduceDims], red_extent[kMaxReduceDims];
+    int64_t red_src[kMaxReduceDims];
+    int64_t outputs, count, chunks;
+    float factor;
+};
+
+// Thread (q, o): the sum of chunk q of output o's contributions.  With one chunk the value is
+// final (0 + partial == partial, then the scale); otherwise it goes to partial[q][o].
+__global__ void __launch_bounds__(kBlock) reduce_axes_chunk_kernel(const float *__restrict__ a,
+                                                                   float *__restrict__ dst, ReduceAxesArgs r) {
+    const int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (t >= r.outputs * r.chunks) return;
+    const uint32_t o = (uint32_t)(t % r.outputs);
+    const int64_t q = t / r.outputs;
+    int64_t base = 0;
+    for (int d = 0; d < r.kept_rank; ++d) base += (int64_t)r.kept_extent[d].mod(r.kept_place[d].div(o)) * r.kept_src[d];
+    const int64_t j0 = q * axis::kGroupedChunk;
+    const int64_t j1 = j0 + axis::kGroupedChunk < r.count ? j0 + axis::kGroupedChunk : r.count;
+    float sum = 0.0f;
+    if (r.red_rank == 1) {
+        const float *p = a + base;
+        for (int64_t j = j0; j < j1; ++j) sum = sum + p[j * r.red_src[0]];
+    } else {
+        for (int64_t j = j0; j < j1; ++j) {
+            int64_t off = base;
+            for (int d = 0; d < r.red_rank; ++d)
+                off += (int64_t)r.red_extent[d].mod(r.red_place[d].div((uint32_t)j)) * r.red_src[d];
+            sum = sum + a[off];
+        }
+    }
+    if (r.chunks == 1)
+        dst[o] = sum * r.factor;
+    else
+        dst[q * r.outputs + o] = sum;
+}
+
+__global__ void __launch_bounds__(kBlock) reduce_axes_combine_kernel(const float *__restrict__ partial,
+                                                                     float *__restrict__ out, int64_t outputs,
+                                                                     int64_t chunks, float factor) {
+    const int64_t o = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (o >= outputs) return;
+    float total = 0.0f;
+    for (int64_t q = 0; q < chunks; ++q) total = total + partial[q * outputs + o];
+    out[o] = total * factor;
+}
+
+// Backward: every input element (in memory order) gets factor * gradient[its kept coordinates].
+struct BroadcastAxesArgs {
+    int32_t rank;
+    FastDiv place[kMaxReduceDims], extent[kMaxReduceDims];  // dims in decreasing input stride
+    int64_t out_stride[kMaxReduceDims];                     // 0 for reduced dims
+    int64_t len;
+    float factor;
+};
+
+__global__ void __launch_bounds__(kBlock) broadcast_axes_kernel(const float *__restrict__ g, float *__restrict__ out,
+                                                                BroadcastAxesArgs b) {
+    const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (i >= b.len) return;
+    int64_t off = 0;
+    for (int d = 0; d < b.rank; ++d)
+        off += (int64_t)b.extent[d].mod(b.place[d].div((uint32_t)i)) * b.out_stride[d];
+    out[i] = g[off] * b.factor;
+}
+
+// Validates a dense layout (strides a permutation of row-major ones over the extents) and
+// returns the dims ordered by decreasing stride.
+int dense_order(int32_t rank, const int64_t *extents, const int64_t *strides, int *order, int64_t *len) {
+    AXIS_REQUIRE(rank >= 1 && rank <= kMaxReduceDims, "reduce_axes rank must be 1..10");
+    AXIS_REQUIRE(extents && strides, "null reduce_axes geometry");
+    *len = 1;
+    for (int d = 0; d < rank; ++d) {
+        AXIS_REQUIRE(extents[d] >= 1 && strides[d] >= 0, "reduce_axes extents must be positive");
+        *len *= extents[d];
+        AXIS_REQUIRE(*len <= INT32_MAX - kBlock, "reduce_axes tensor too large");
+        order[d] = d;
+    }
+    for (int i = 1; i < rank; ++i)  // stable: unit dims keep their order
+        for (int k = i; k > 0 && strides[order[k]] > strides[order[k - 1]]; --k) std::swap(order[k], order[k - 1]);
+    int64_t expect = 1;
+    for (int i = rank - 1; i >= 0; --i) {
+        const int d = order[i];
+        AXIS_REQUIRE(extents[d] == 1 || strides[d] == expect, "reduce_axes needs a dense layout");
+        expect *= extents[d];
+    }
+    return AXIS_OK;
+}
+
 struct BroadcastMiddle {
     const float *g;
     float *out;
@@ -605,6 +706,114 @@ int axis_reduce_middle(axis_device device, const float *a, float *out, int64_t o
     reduce_middle_kernel<<<axis::blocks_for(outer * inner, kBlock, INT32_MAX), kBlock, 0,
                            device->stream>>>(a, out, outer, reduce, inner, factor);
     return axis::launch_status("reduce_middle_kernel");
+}
+
+int axis_reduce_axes(axis_device device, const float *a, float *out, int32_t rank, const int64_t *extents,
+                     const int64_t *strides, const int32_t *reduced, float factor) {
+    AXIS_ENTER(device);
+    AXIS_REQUIRE(a && out && reduced, "null reduce_axes buffer");
+    int order[kMaxReduceDims];
+    int64_t len = 0;
+    if (int st = dense_order(rank, extents, strides, order, &len)) return st;
+    ReduceAxesArgs r{};
+    r.factor = factor;
+    // kept dims in shape order; neighbours contiguous in the input merge (the output is
+    // row-major over them, so it is contiguous there too)
+    int64_t ke[kMaxReduceDims], ks[kMaxReduceDims];
+    int kr = 0;
+    for (int d = 0; d < rank; ++d) {
+        if (reduced[d] || extents[d] == 1) continue;
+        if (kr > 0 && ks[kr - 1] == strides[d] * extents[d]) {
+            ke[kr - 1] *= extents[d];
+            ks[kr - 1] = strides[d];
+            continue;
+        }
+        ke[kr] = extents[d];
+        ks[kr] = strides[d];
+        ++kr;
+    }
+    // reduced dims in decreasing stride, contiguous runs merged
+    int64_t re[kMaxReduceDims], rs[kMaxReduceDims];
+    int rr = 0;
+    for (int i = 0; i < rank; ++i) {
+        const int d = order[i];
+        if (!reduced[d] || extents[d] == 1) continue;
+        if (rr > 0 && rs[rr - 1] == strides[d] * extents[d]) {
+            re[rr - 1] *= extents[d];
+            rs[rr - 1] = strides[d];
+            continue;
+        }
+        re[rr] = extents[d];
+        rs[rr] = strides[d];
+        ++rr;
+    }
+    r.outputs = 1;
+    for (int d = kr - 1; d >= 0; --d) {
+        r.kept_place[d] = FastDiv((uint32_t)r.outputs);
+        r.kept_extent[d] = FastDiv((uint32_t)ke[d]);
+        r.kept_src[d] = ks[d];
+        r.outputs *= ke[d];
+    }
+    r.count = 1;
+    for (int d = rr - 1; d >= 0; --d) {
+        r.red_place[d] = FastDiv((uint32_t)r.count);
+        r.red_extent[d] = FastDiv((uint32_t)re[d]);
+        r.red_src[d] = rs[d];
+        r.count *= re[d];
+    }
+    r.kept_rank = kr;
+    r.red_rank = rr;
+    if (rr == 0) {  // nothing reduced (unit extents only): a scaled copy in output order
+        r.red_rank = 1;
+        r.red_place[0] = FastDiv(1u);
+        r.red_extent[0] = FastDiv(1u);
+        r.red_src[0] = 0;
+    }
+    r.chunks = (r.count + axis::kGroupedChunk - 1) / axis::kGroupedChunk;
+    const int64_t threads = r.outputs * r.chunks;
+    axis::Scratch partial;
+    float *dst = out;
+    if (r.chunks > 1) {
+        if (int st = partial.get(device, sizeof(float) * (size_t)threads)) return st;
+        dst = partial.as<float>();
+    }
+    reduce_axes_chunk_kernel<<<axis::blocks_for(threads, kBlock, INT32_MAX), kBlock, 0, device->stream>>>(a, dst, r);
+    if (int st = axis::launch_status("reduce_axes_chunk_kernel")) return st;
+    if (r.chunks == 1) return AXIS_OK;
+    reduce_axes_combine_kernel<<<axis::blocks_for(r.outputs, kBlock, INT32_MAX), kBlock, 0, device->stream>>>(
+        dst, out, r.outputs, r.chunks, factor);
+    return axis::launch_status("reduce_axes_combine_kernel");
+}
+
+int axis_reduce_axes_backward(axis_device device, const float *gradient, float *out, int32_t rank,
+                              const int64_t *extents, const int64_t *strides, const int32_t *reduced,
+                              float factor) {
+    AXIS_ENTER(device);
+    AXIS_REQUIRE(gradient && out && reduced, "null reduce_axes_backward buffer");
+    int order[kMaxReduceDims];
+    int64_t len = 0;
+    if (int st = dense_order(rank, extents, strides, order, &len)) return st;
+    // output strides of the kept dims (row-major over them in shape order)
+    int64_t out_stride[kMaxReduceDims];
+    int64_t s = 1;
+    for (int d = rank - 1; d >= 0; --d) {
+        out_stride[d] = reduced[d] ? 0 : s;
+        if (!reduced[d]) s *= extents[d];
+    }
+    BroadcastAxesArgs b{};
+    b.len = len;
+    b.factor = factor;
+    int64_t place = 1;
+    for (int i = rank - 1; i >= 0; --i) {
+        const int d = order[i];
+        b.place[i] = FastDiv((uint32_t)place);
+        b.extent[i] = FastDiv((uint32_t)extents[d]);
+        b.out_stride[i] = out_stride[d];
+        place *= extents[d];
+    }
+    b.rank = rank;
+    broadcast_axes_kernel<<<axis::blocks_for(len, kBlock, INT32_MAX), kBlock, 0, device->stream>>>(gradient, out, b);
+    return axis::launch_status("broadcast_axes_kernel");
 }
 
 int axis_broadcast_middle(axis_device device, const float *gradient, float *out, int64_t outer,

@@ -190,13 +190,15 @@ struct Rule {
         ConvData,    // input gradient of an implicit-GEMM convolution (a = weight)
         ConvWeight,  // weight gradient of an implicit-GEMM convolution (a = input)
         ReluPool,    // ReLU then non-overlapping max pool (a = argmax bytes, b = pooled values)
+        ReduceAxes,  // sum over any axis set (extents/strides of the input, metadata = reduced flags)
     } kind = Identity;
     float factor = 1.0f;
     Buffer a, b;  // saved operands (rhs / lhs / probability / input / winners / argmax)
     int64_t batch = 0, m = 0, k = 0, n = 0;  // matmul extents; Zero: n = length
     Plan plan;
     std::shared_ptr<axis_unfold_spec> spec;
-    std::vector<int32_t> metadata;  // select_axis metadata
+    std::vector<int32_t> metadata;  // select_axis metadata; ReduceAxes: reduced flags
+    std::vector<int64_t> extents, strides;  // ReduceAxes input geometry
     int64_t outer = 0, reduce = 0, inner = 0;
     PoolGeometry pool;
     ConvGeometry conv;

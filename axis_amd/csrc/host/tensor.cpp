@@ -537,20 +537,19 @@ Tensor Tensor::reduce(const std::vector<Axis> &axes_in, bool mean, const char *l
         r.kind = Rule::MeanMiddle;
         r.outer = outer, r.reduce = red, r.inner = inner, r.factor = factor;
     } else {
-        Layout out_layout = Layout::contiguous(out_shape);
-        std::vector<int64_t> map((size_t)shape().len);
-        for (int64_t i = 0; i < shape().len; ++i) {
-            auto c = shape().coords(i);
-            std::vector<int64_t> kept;
-            for (size_t d = 0; d < c.size(); ++d)
-                if (!contains(axes, shape().dims[d].axis)) kept.push_back(c[d]);
-            map[(size_t)layout().offset(c)] = out_layout.offset(kept);
+        // Any other axis set: the strided reduction walks each group in increasing memory
+        // position, the reverse plan's order, without building an element-sized plan.
+        r.kind = Rule::ReduceAxes;
+        for (size_t i = 0; i < shape().rank(); ++i) {
+            r.extents.push_back(shape().dims[i].extent);
+            r.strides.push_back(layout().strides[i]);
+            r.metadata.push_back(contains(axes, shape().dims[i].axis) ? 1 : 0);
         }
-        Plan forward = upload(device(), plan_reverse(map, out_shape.len));
-        value = device().grouped(this->value(), nullptr, forward, factor);
-        r.kind = Rule::Group;
-        r.plan = upload(device(), plan_gather(map));
         r.factor = factor;
+        value = device().alloc(out_shape.len);
+        check(axis_reduce_axes(device().h(), this->value()->f32(), value->f32(), (int32_t)shape().rank(),
+                               r.extents.data(), r.strides.data(), r.metadata.data(), factor),
+              label);
     }
     Tensor out = node(out_shape, Layout::contiguous(out_shape), value, device(), one_edge(*this, r), false);
     profile(label, started);
@@ -965,6 +964,16 @@ void Tensor::backward() const {
                     check(axis_bias_gradient(dev.h(), g->f32(), nullptr, nullptr, c->f32(), r.outer,
                                              r.inner),
                           "bias_gradient");
+                    break;
+                }
+                case Rule::ReduceAxes: {
+                    int64_t len = 1;
+                    for (int64_t e : r.extents) len *= e;
+                    c = dev.alloc(len);
+                    check(axis_reduce_axes_backward(dev.h(), g->f32(), c->f32(), (int32_t)r.extents.size(),
+                                                    r.extents.data(), r.strides.data(), r.metadata.data(),
+                                                    r.factor),
+                          "reduce_axes_backward");
                     break;
                 }
                 case Rule::MeanMiddle:

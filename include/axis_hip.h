@@ -261,6 +261,20 @@ int axis_max_pool2d_backward(axis_device device, const float *gradient, const ui
  * reference's order (chunks of 512, then chunks). */
 int axis_reduce_middle(axis_device device, const float *a, float *out, int64_t outer,
                        int64_t reduce, int64_t inner, float factor);
+/* Tensor::reduce_grouped for any set of axes (tensor.rs:2755-2854: reduction_plans, then
+ * Device::grouped, backend.rs:1089-1125) without an index plan, so without its 16,777,216 cap.
+ * The tensor has rank dims with the given extents and element strides (a dense layout: the
+ * strides are a permutation of row-major ones); reduced[d] != 0 marks the summed dims.  out is
+ * row-major over the kept dims in dim order: out = factor * sum, each group's contributions in
+ * increasing memory position, chunks of 512 then the chunk partials in order -- bit-identical to
+ * grouped() over the reference's reverse plan.  rank <= 10, at most INT32_MAX elements. */
+int axis_reduce_axes(axis_device device, const float *a, float *out, int32_t rank, const int64_t *extents,
+                     const int64_t *strides, const int32_t *reduced, float factor);
+/* Its backward (the gather plan's grouped, tensor.rs:2805-2854): out, laid out like the input,
+ * gets factor * gradient[kept coordinates] at every element. */
+int axis_reduce_axes_backward(axis_device device, const float *gradient, float *out, int32_t rank,
+                              const int64_t *extents, const int64_t *strides, const int32_t *reduced,
+                              float factor);
 /* Its Group-rule backward: out[o][r][i] = factor * gradient[o][i]. */
 int axis_broadcast_middle(axis_device device, const float *gradient, float *out, int64_t outer,
                           int64_t reduce, int64_t inner, float factor);

@@ -183,6 +183,51 @@ def test_large_group_bias_gradient_fixture(ax, device):
     assert np.array_equal(f.grad().to_vec(), np.ones(1200, np.float32))
 
 
+@pytest.mark.parametrize("reduced,order,mean", [
+    ((0, 2), (2, 0, 3, 1), True),
+    ((1, 3), (0, 1, 2, 3), False),
+    ((0, 3), (3, 1, 0, 2), True),
+    ((1,), (2, 1, 3, 0), False),
+    ((0, 1, 2, 3), (1, 3, 0, 2), True),
+])
+def test_reduce_any_axis_set_and_layout(ax, device, reduced, order, mean):
+    """sum/mean over axis sets that are not one consecutive block of a contiguous tensor
+    (tensor.rs:2755-2854), through a permuted layout; the gradient is factor * upstream at every
+    element, exactly."""
+    names = [ax.Axis(f"d{i}") for i in range(4)]
+    extents = [6, 5, 7, 4]
+    rng = np.random.default_rng(sum(reduced) * 10 + order[0])
+    values = rng.standard_normal(int(np.prod(extents))).astype(np.float32)
+    x = ax.Tensor.from_slice(values, [a.of(e) for a, e in zip(names, extents)], device).with_grad()
+    y = x.with_layout([names[i] for i in order])
+    axes = [names[i] for i in reduced]
+    r = y.mean(axes) if mean else y.sum(axes)
+    expect = values.reshape(extents).astype(np.float64).sum(axis=reduced)
+    kept = int(np.prod([extents[i] for i in range(4) if i not in reduced]))
+    factor = np.float32(kept) / np.float32(values.size) if mean else np.float32(1.0)
+    close("reduce", r.to_vec(), (expect * float(factor)).reshape(-1))
+    w = rng.standard_normal(kept).astype(np.float32)
+    kept_dims = [names[i].of(extents[i]) for i in range(4) if i not in reduced]
+    wt = ax.Tensor.from_slice(w, kept_dims, device) if kept_dims else None
+    (r.mul(wt).sum([d for d in r.shape.axes()]) if wt is not None else r).backward()
+    wk = w.reshape([extents[i] for i in range(4) if i not in reduced]) if kept_dims else np.float32(1.0)
+    grad = np.broadcast_to(np.expand_dims(np.float32(wk) * factor, axis=reduced), extents)
+    assert np.array_equal(x.grad().to_vec(), grad.reshape(-1))
+
+
+def test_reduce_past_the_plan_cap(ax, device):
+    """17.8M elements summed over two non-adjacent axes: the reference's plan path rejects this
+    (16,777,216 contributions, backend.rs:1588-1596); the strided reduction does not need a plan."""
+    names = [ax.Axis(n) for n in ("b", "h", "w", "c")]
+    extents = [17, 64, 32, 512]
+    rng = np.random.default_rng(3)
+    values = rng.standard_normal(int(np.prod(extents))).astype(np.float32)
+    x = ax.Tensor.from_slice(values, [a.of(e) for a, e in zip(names, extents)], device)
+    r = x.mean([names[0], names[2]])
+    expect = values.reshape(extents).astype(np.float64).mean(axis=(0, 2))
+    close("mean", r.to_vec(), expect.reshape(-1))
+
+
 def test_normalized_l2_fixture(ax, device):
     # model/optim.rs:1492-1503
     v = ax.Axis("value")

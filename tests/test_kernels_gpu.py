@@ -446,6 +446,70 @@ def test_reduce_and_broadcast_middle_bit_exact(dev, oracle):
     assert np.array_equal(dev.read(back, len(a)), oracle.grouped(got, None, rev, factor))
 
 
+# (dims, storage order outermost first, reduced axes, mean): non-consecutive axis sets, permuted
+# layouts, unit dims, several chunks per group, a single output, nothing left to merge.
+REDUCE_AXES_CASES = [
+    ([("a", 3), ("b", 5), ("c", 7)], ["a", "b", "c"], ["a", "c"], False),
+    ([("a", 3), ("b", 5), ("c", 7)], ["c", "a", "b"], ["b"], True),
+    ([("n", 4), ("h", 9), ("w", 9), ("ch", 6)], ["n", "ch", "h", "w"], ["h", "w"], True),
+    ([("n", 4), ("h", 9), ("w", 9), ("ch", 6)], ["n", "h", "w", "ch"], ["n", "w"], False),
+    ([("p", 1), ("q", 600), ("u", 1), ("v", 5)], ["v", "q", "p", "u"], ["q", "u"], True),
+    ([("x", 2), ("y", 1300), ("z", 3)], ["y", "z", "x"], ["x", "y", "z"], True),
+    ([("x", 2), ("y", 13), ("z", 3)], ["x", "y", "z"], ["y"], False),
+]
+
+
+@pytest.mark.parametrize("dims,order,axes,mean", REDUCE_AXES_CASES)
+def test_reduce_axes_bit_exact(dev, oracle, dims, order, axes, mean):
+    rng = np.random.default_rng(len(dims) * 31 + sum(e for _, e in dims))
+    n = int(np.prod([e for _, e in dims]))
+    a = rng.standard_normal(n).astype(np.float32)  # physical storage
+    strides = oracle.layout_for(dims, order)
+    out_dims, fwd, rev, factor = oracle.reduction_plans(dims, strides, axes, mean)
+    olen = int(np.prod([e for _, e in out_dims])) if out_dims else 1
+    ext = np.array([e for _, e in dims], np.int64)
+    st = np.array(strides, np.int64)
+    red = np.array([1 if name in axes else 0 for name, _ in dims], np.int32)
+    geo = (I32(len(dims)), ext.ctypes.data_as(VP), st.ctypes.data_as(VP), red.ctypes.data_as(VP), F32(factor))
+    da, out = up(dev, a), dev.empty(olen)
+    dev.call("axis_reduce_axes", da.vp, out.vp, *geo)
+    got = dev.read(out, olen)
+    assert np.array_equal(got, oracle.grouped(a, None, fwd, factor))
+    back = dev.empty(n)
+    dev.call("axis_reduce_axes_backward", out.vp, back.vp, *geo)
+    assert np.array_equal(dev.read(back, n), oracle.grouped(got, None, rev, factor))
+
+
+def test_reduce_axes_past_the_plan_cap(dev, oracle):
+    """A mean over two non-adjacent axes of 2^24 + 2^20 elements: past the reference's 16,777,216
+    contribution cap, still in the reverse plan's order (plan built uncapped on the host)."""
+    dims = [("b", 17), ("h", 64), ("w", 32), ("c", 512)]
+    n = int(np.prod([e for _, e in dims]))
+    assert n > 16777216
+    rng = np.random.default_rng(5)
+    a = rng.standard_normal(n).astype(np.float32)
+    strides = oracle.contiguous(dims)
+    out_dims, fwd, _, factor = oracle.reduction_plans(dims, strides, ["b", "w"], True, cap=False)
+    olen = int(np.prod([e for _, e in out_dims]))
+    ext = np.array([e for _, e in dims], np.int64)
+    st = np.array(strides, np.int64)
+    red = np.array([1, 0, 1, 0], np.int32)
+    da, out = up(dev, a), dev.empty(olen)
+    dev.call("axis_reduce_axes", da.vp, out.vp, I32(4), ext.ctypes.data_as(VP), st.ctypes.data_as(VP),
+             red.ctypes.data_as(VP), F32(factor))
+    assert np.array_equal(dev.read(out, olen), oracle.grouped(a, None, fwd, factor))
+
+
+def test_reduce_axes_rejects_non_dense_layouts(dev):
+    a, out = dev.empty(64), dev.empty(8)
+    ext = np.array([8, 8], np.int64)
+    st = np.array([16, 1], np.int64)  # row pitch 16 over 8 columns: not dense
+    red = np.array([0, 1], np.int32)
+    with pytest.raises(hip.AxisError, match="dense layout"):
+        dev.call("axis_reduce_axes", a.vp, out.vp, I32(2), ext.ctypes.data_as(VP), st.ctypes.data_as(VP),
+                 red.ctypes.data_as(VP), F32(1.0))
+
+
 # ---------------------------------------------------------------- implicit-GEMM convolution
 
 @pytest.mark.parametrize("b,h,w,c,n,k,s,p", [(2, 9, 7, 8, 16, 3, 1, 1), (3, 16, 16, 64, 128, 3, 1, 1),
