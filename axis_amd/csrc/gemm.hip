@@ -278,6 +278,60 @@ struct ConvColsLoader : Staging<BT, BK, NT, false, VEC> {
     }
 };
 
+// Cols mode when every K step covers whole aligned pixel runs: BK divides the output width or is
+// a multiple of it, and the image's pixel count is a multiple of BK.  Then a step starting at
+// pixel p0 (a multiple of BK) never leaves one image and the in-step pixel s sits at
+// (oy0 + s / out_w, ox0 + s % out_w) for every step, so each vector's window position relative
+// to the step origin is fixed at init and a step decodes only its wave-uniform origin.
+template <int BT, int BK, int NT, int VEC>
+struct ConvColsStepLoader : Staging<BT, BK, NT, false, VEC> {
+    using S = Staging<BT, BK, NT, false, VEC>;
+    static constexpr int kRowStep = NT / S::kPer;  // pixels between the thread's rows
+    int32_t iy_rel[S::kVecs], ix_rel[S::kVecs];    // dy*sy + ky - py, dx*sx + kx - px
+    uint32_t rel[S::kVecs];                        // iy_rel*ld_h + ix_rel*ld_w + c*ld_c (mod 2^32)
+    int32_t s0;                                    // in-step pixel of the thread's first row
+    bool t_ok;
+
+    __device__ __forceinline__ void init(const ConvGeom &geom, int64_t t0, int64_t t_end, int tid) {
+        const int64_t gt = t0 + (tid % S::kPer) * VEC;
+        t_ok = gt < t_end;
+        const uint32_t g = t_ok ? (uint32_t)gt : 0u;
+        const uint32_t pos = geom.c_div.div(g);
+        const int32_t c = (int32_t)(g - pos * (uint32_t)geom.channels);
+        const int32_t ky = (int32_t)geom.kw_div.div(pos);
+        const int32_t kx = (int32_t)pos - ky * geom.kw;
+        s0 = tid / S::kPer;
+#pragma unroll
+        for (int e = 0; e < S::kVecs; ++e) {
+            const uint32_t s = (uint32_t)(s0 + e * kRowStep);
+            const int32_t dy = (int32_t)geom.ow_div.div(s);
+            const int32_t dx = (int32_t)s - dy * geom.out_w;
+            iy_rel[e] = dy * geom.sy + ky - geom.py;
+            ix_rel[e] = dx * geom.sx + kx - geom.px;
+            rel[e] = (uint32_t)iy_rel[e] * (uint32_t)geom.ld_h + (uint32_t)ix_rel[e] * (uint32_t)geom.ld_w +
+                     (uint32_t)c * (uint32_t)geom.ld_c;
+        }
+    }
+    __device__ __forceinline__ void load(const ConvGeom &geom, int64_t r0, int64_t r_end, int) {
+        const uint32_t p0 = (uint32_t)r0;
+        const uint32_t q = geom.ow_div.div(p0);
+        const int32_t ox0 = (int32_t)(p0 - q * (uint32_t)geom.out_w);
+        const uint32_t b = geom.oh_div.div(q);
+        const int32_t oy0 = (int32_t)(q - b * (uint32_t)geom.out_h);
+        const int32_t oys = oy0 * geom.sy, oxs = ox0 * geom.sx;
+        const uint32_t base = b * (uint32_t)geom.ld_b + (uint32_t)oys * (uint32_t)geom.ld_h +
+                              (uint32_t)oxs * (uint32_t)geom.ld_w;
+        const int64_t room = r_end - r0;  // pixels of this step inside the reduction
+#pragma unroll
+        for (int e = 0; e < S::kVecs; ++e) {
+            const bool valid = t_ok && s0 + e * kRowStep < room &&
+                               (uint32_t)(oys + iy_rel[e]) < (uint32_t)geom.height &&
+                               (uint32_t)(oxs + ix_rel[e]) < (uint32_t)geom.width;
+            load_into<VEC>(this->reg + e * VEC, geom.src + (valid ? base + rel[e] : 0u), valid);
+        }
+    }
+};
+
 // Finishes one output value v (the whole reduction) at flat output index idx: + bias[col], then
 // beta * d + alpha * v.  Each product and the sum round separately, as the separate scale / scale
 // / add operations they replace.
@@ -293,7 +347,8 @@ __device__ __forceinline__ float finish_value(const float *bias, const float *d,
     return v;
 }
 
-// XMODE: 0 dense X, 1 convolution rows mode, 2 convolution cols mode.
+// XMODE: 0 dense X, 1 convolution rows mode, 2 convolution cols mode, 3 cols mode over aligned
+// pixel steps.
 // EPI: 0 store C (+ bias), 1 bias + ReLU + max pool of whole windows (rows are output pixels).
 template <int BM, int BN, int BK, int WM, int WN, bool XR, bool YR, int VX, int VY, int XMODE, int EPI>
 __global__ void __launch_bounds__(WM *WN * 64)
@@ -301,9 +356,11 @@ __global__ void __launch_bounds__(WM *WN * 64)
     constexpr int NT = WM * WN * 64;
     constexpr int TM = BM / WM, TN = BN / WN;
     constexpr int FM = TM / 32, FN = TN / 32;
-    using LX = std::conditional_t<XMODE == 0, DenseLoader<BM, BK, NT, XR, VX>,
-                                  std::conditional_t<XMODE == 1, ConvRowsLoader<BM, BK, NT, VX>,
-                                                     ConvColsLoader<BM, BK, NT, VX>>>;
+    using LX = std::conditional_t<
+        XMODE == 0, DenseLoader<BM, BK, NT, XR, VX>,
+        std::conditional_t<XMODE == 1, ConvRowsLoader<BM, BK, NT, VX>,
+                           std::conditional_t<XMODE == 2, ConvColsLoader<BM, BK, NT, VX>,
+                                              ConvColsStepLoader<BM, BK, NT, VX>>>>;
     using LY = DenseLoader<BN, BK, NT, YR, VY>;
     constexpr int kStage = BK * LX::LD + BK * LY::LD;
     constexpr int kPoolPitch = TN + 1;
@@ -1119,7 +1176,13 @@ int axis_conv2d_backward_weight(axis_device device, const float *input,
     p.y_sr = out_channels;
     p.y_sj = 1;
     p.conv = geom(in.src, in.ld, height, width, in.channels, s.out_h, s.out_w, s.kw, s.sy, s.sx, s.py, s.px);
-    if (int st = run_gemm<false, false, 2, 0>(device, p, 1, ordered.as<float>())) return st;
+    // Every tile shape is 32 deep: when 32-pixel steps never straddle an image and cut its rows
+    // the same way each time, the cheaper step loader applies.
+    const int64_t image = (int64_t)s.out_h * s.out_w;
+    const bool aligned = (32 % s.out_w == 0 || s.out_w % 32 == 0) && image % 32 == 0;
+    const int st = aligned ? run_gemm<false, false, 3, 0>(device, p, 1, ordered.as<float>())
+                           : run_gemm<false, false, 2, 0>(device, p, 1, ordered.as<float>());
+    if (st) return st;
     return permute_weight(device, ordered.as<float>(), d_weight, s, 2, in.channels);
 }
 
