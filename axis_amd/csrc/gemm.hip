@@ -72,6 +72,7 @@ struct GemmParams {
     float *pooled;
     uint8_t *argmax;
     int32_t pool_h, pool_w, pool_ow;
+    FastDiv pool_cols;         // pooled columns per output row (pool_ow / pool_w)
 };
 
 template <int VEC>
@@ -542,21 +543,31 @@ __global__ void __launch_bounds__(WM *WN * 64)
                     }
             }
             __syncthreads();
-            for (int idx = tid; idx < windows * TN; idx += NT) {
-                const int cl = idx % TN, w = idx / TN;
-                const int wr = w / pw, px = w - wr * pw;
-                const int64_t col = j0 + h * TN + cl;
-                if (col >= p.n || i0 + (int64_t)wr * kh * ow >= p.m) continue;
+            // Thread items: column cl (fixed per thread) of windows w, w + NT/TN, ...
+            const int cl = tid % TN;
+            const int64_t col = j0 + h * TN + cl;
+            const bool col_ok = col < p.n;
+            for (int w = tid / TN; w < windows; w += NT / TN) {
+                const int wr = (int)p.pool_cols.div((uint32_t)w), px = w - wr * pw;
+                if (!col_ok || i0 + (int64_t)wr * kh * ow >= p.m) continue;
                 float best = -INFINITY;
                 int winner = 255;
-                for (int ky = 0; ky < kh; ++ky)
-                    for (int kx = 0; kx < kw; ++kx) {
-                        const float v = lds[((wr * kh + ky) * ow + px * kw + kx) * kPoolPitch + cl];
-                        if (v >= -FLT_MAX && v <= FLT_MAX && v > best) {
-                            best = v;
-                            winner = ky * kw + kx;
-                        }
+                const float *win = lds + ((wr * kh) * ow + px * kw) * kPoolPitch + cl;
+                auto take = [&](float v, int at) {
+                    if (v >= -FLT_MAX && v <= FLT_MAX && v > best) {
+                        best = v;
+                        winner = at;
                     }
+                };
+                if (kh == 2 && kw == 2) {
+                    take(win[0], 0);
+                    take(win[kPoolPitch], 1);
+                    take(win[ow * kPoolPitch], 2);
+                    take(win[(ow + 1) * kPoolPitch], 3);
+                } else {
+                    for (int ky = 0; ky < kh; ++ky)
+                        for (int kx = 0; kx < kw; ++kx) take(win[(ky * ow + kx) * kPoolPitch], ky * kw + kx);
+                }
                 const int64_t out = ((pooled_row0 + wr) * pw + px) * p.n + col;
                 p.pooled[out] = winner == 255 ? __builtin_nanf("") : best;
                 p.argmax[out] = (uint8_t)winner;
@@ -1114,6 +1125,7 @@ int axis_conv2d_relu_pool_forward(axis_device device, const float *input,
     p.pool_h = pool[0];
     p.pool_w = pool[1];
     p.pool_ow = s.out_w;
+    p.pool_cols = FastDiv((uint32_t)(s.out_w / pool[1]));
     return run_gemm<true, false, 1, 1>(device, p, 1, nullptr);
 }
 
