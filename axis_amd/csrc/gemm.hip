@@ -47,6 +47,7 @@ struct ConvGeom {
     int32_t out_h, out_w;             // output pixel grid the reduction/rows enumerate
     int32_t kw, sy, sx, py, px;
     FastDiv c_div, kw_div, ow_div, oh_div;
+    bool tap_steps;                   // channels % 32 == 0: a 32-deep K step stays in one tap
 };
 
 struct GemmParams {
@@ -209,6 +210,85 @@ struct ConvRowsLoader : Staging<BT, BK, NT, true, VEC> {
     }
 };
 
+// Buffer loads: an offset at or past the resource's record count (2^31 - 1 bytes) reads as zero,
+// so padding taps and reduction tails need neither a branch nor zeroed registers.
+constexpr uint32_t kOutside = 0x80000000u;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const float *base) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, 0x7fffffff, 0x00020000);
+}
+template <int VEC>
+__device__ __forceinline__ void buffer_into(float *reg, __amdgpu_buffer_rsrc_t rsrc, uint32_t byte_offset) {
+    if constexpr (VEC == 4) {
+        const floatx4 v = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, byte_offset, 0, 0));
+        reg[0] = v[0];
+        reg[1] = v[1];
+        reg[2] = v[2];
+        reg[3] = v[3];
+    } else {
+        reg[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, byte_offset, 0, 0));
+    }
+}
+
+// Rows mode through buffer loads, for gathered tensors whose offsets fit 31-bit byte offsets.
+// When the channel count is a multiple of BK (geom.tap_steps), a K step covers BK channels of one
+// tap, so the step's tap decode is wave-uniform and each vector costs two bounds tests.
+template <int BT, int BK, int NT, int VEC>
+struct ConvRowsBufferLoader : Staging<BT, BK, NT, true, VEC> {
+    using S = Staging<BT, BK, NT, true, VEC>;
+    uint32_t origin[S::kVecs];   // b*ld_b + iy0*ld_h + ix0*ld_w (mod 2^32; exact when valid)
+    int32_t iy0[S::kVecs], ix0[S::kVecs];
+    int rr;
+
+    __device__ __forceinline__ void init(const ConvGeom &geom, int64_t t0, int64_t t_end, int tid) {
+        rr = (tid % S::kPer) * VEC;
+#pragma unroll
+        for (int e = 0; e < S::kVecs; ++e) {
+            const int64_t gt = t0 + (tid + e * NT) / S::kPer;
+            const bool live = gt < t_end;
+            const uint32_t pix = live ? (uint32_t)gt : 0u;
+            const uint32_t q = geom.ow_div.div(pix);
+            const int32_t ox = (int32_t)(pix - q * (uint32_t)geom.out_w);
+            const uint32_t b = geom.oh_div.div(q);
+            const int32_t oy = (int32_t)(q - b * (uint32_t)geom.out_h);
+            const int32_t y0 = oy * geom.sy - geom.py;
+            ix0[e] = ox * geom.sx - geom.px;
+            origin[e] = b * (uint32_t)geom.ld_b + (uint32_t)y0 * (uint32_t)geom.ld_h +
+                        (uint32_t)ix0[e] * (uint32_t)geom.ld_w;
+            iy0[e] = live ? y0 : -(1 << 30);
+        }
+    }
+    __device__ __forceinline__ void load(const ConvGeom &geom, int64_t r0, int64_t r_end, int) {
+        const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(geom.src);
+        int32_t ky, kx;
+        uint32_t delta;
+        bool r_ok;
+        if (geom.tap_steps) {
+            // r_end is a multiple of BK here, so every k of the step is inside the reduction
+            const uint32_t pos = geom.c_div.div((uint32_t)r0);
+            const int32_t c0 = (int32_t)((uint32_t)r0 - pos * (uint32_t)geom.channels);
+            ky = (int32_t)geom.kw_div.div(pos);
+            kx = (int32_t)pos - ky * geom.kw;
+            delta = (uint32_t)(ky * geom.ld_h + kx * geom.ld_w + (c0 + rr) * geom.ld_c);
+            r_ok = true;
+        } else {
+            const int64_t gr = r0 + rr;
+            r_ok = gr < r_end;
+            const uint32_t g = r_ok ? (uint32_t)gr : 0u;
+            const uint32_t pos = geom.c_div.div(g);
+            const int32_t c = (int32_t)(g - pos * (uint32_t)geom.channels);
+            ky = (int32_t)geom.kw_div.div(pos);
+            kx = (int32_t)pos - ky * geom.kw;
+            delta = (uint32_t)(ky * geom.ld_h + kx * geom.ld_w + c * geom.ld_c);
+        }
+#pragma unroll
+        for (int e = 0; e < S::kVecs; ++e) {
+            const bool valid = r_ok && (uint32_t)(iy0[e] + ky) < (uint32_t)geom.height &&
+                               (uint32_t)(ix0[e] + kx) < (uint32_t)geom.width;
+            buffer_into<VEC>(this->reg + e * VEC, rsrc, valid ? (origin[e] + delta) * 4u : kOutside);
+        }
+    }
+};
+
 // Convolution operand, cols mode: t = (ky*kw + kx)*channels + channel, r = output pixel.  The
 // thread's t is fixed; each row keeps its pixel's coordinates and offset and walks forward BK
 // pixels per K step.
@@ -349,19 +429,22 @@ __device__ __forceinline__ float finish_value(const float *bias, const float *d,
 }
 
 // XMODE: 0 dense X, 1 convolution rows mode, 2 convolution cols mode, 3 cols mode over aligned
-// pixel steps.
+// pixel steps, 4 rows mode through buffer loads.
 // EPI: 0 store C (+ bias), 1 bias + ReLU + max pool of whole windows (rows are output pixels).
 template <int BM, int BN, int BK, int WM, int WN, bool XR, bool YR, int VX, int VY, int XMODE, int EPI>
 __global__ void __launch_bounds__(WM *WN * 64)
     gemm_kernel(GemmParams p) {
     constexpr int NT = WM * WN * 64;
+    static_assert(XMODE != 4 || BK == 32, "the buffer rows loader's tap steps are 32 deep");
     constexpr int TM = BM / WM, TN = BN / WN;
     constexpr int FM = TM / 32, FN = TN / 32;
     using LX = std::conditional_t<
         XMODE == 0, DenseLoader<BM, BK, NT, XR, VX>,
-        std::conditional_t<XMODE == 1, ConvRowsLoader<BM, BK, NT, VX>,
-                           std::conditional_t<XMODE == 2, ConvColsLoader<BM, BK, NT, VX>,
-                                              ConvColsStepLoader<BM, BK, NT, VX>>>>;
+        std::conditional_t<
+            XMODE == 1, ConvRowsLoader<BM, BK, NT, VX>,
+            std::conditional_t<XMODE == 2, ConvColsLoader<BM, BK, NT, VX>,
+                               std::conditional_t<XMODE == 3, ConvColsStepLoader<BM, BK, NT, VX>,
+                                                  ConvRowsBufferLoader<BM, BK, NT, VX>>>>>;
     using LY = DenseLoader<BN, BK, NT, YR, VY>;
     constexpr int kStage = BK * LX::LD + BK * LY::LD;
     constexpr int kPoolPitch = TN + 1;
@@ -923,7 +1006,16 @@ ConvGeom geom(const float *src, const int64_t ld[4], int32_t height, int32_t wid
     g.kw_div = FastDiv((uint32_t)kw);
     g.ow_div = FastDiv((uint32_t)out_w);
     g.oh_div = FastDiv((uint32_t)out_h);
+    g.tap_steps = channels % 32 == 0;
     return g;
+}
+
+// Rows mode reads through 31-bit byte offsets when every element of the gathered tensor is
+// within reach of them (the buffer loader); larger tensors keep 64-bit addresses.
+bool buffer_reach(const ConvGeom &g, int64_t batch) {
+    const int64_t last = (batch - 1) * g.ld_b + (int64_t)(g.height - 1) * g.ld_h + (int64_t)(g.width - 1) * g.ld_w +
+                         (int64_t)(g.channels - 1) * g.ld_c;
+    return (last + 4) * 4 < (int64_t(1) << 31) - 1;
 }
 
 int permute_weight(axis_device device, const float *src, float *dst, const ConvShape &s, int mode,
@@ -1081,7 +1173,8 @@ int axis_conv2d_forward(axis_device device, const float *input, const int64_t in
     p.y_sr = out_channels;
     p.y_sj = 1;
     p.conv = geom(in.src, in.ld, height, width, in.channels, s.out_h, s.out_w, s.kw, s.sy, s.sx, s.py, s.px);
-    return run_gemm<true, false, 1, 0>(device, p, 1, out);
+    return buffer_reach(p.conv, batch) ? run_gemm<true, false, 4, 0>(device, p, 1, out)
+                                       : run_gemm<true, false, 1, 0>(device, p, 1, out);
 }
 
 int axis_conv2d_relu_pool_forward(axis_device device, const float *input,
@@ -1126,7 +1219,8 @@ int axis_conv2d_relu_pool_forward(axis_device device, const float *input,
     p.pool_w = pool[1];
     p.pool_ow = s.out_w;
     p.pool_cols = FastDiv((uint32_t)(s.out_w / pool[1]));
-    return run_gemm<true, false, 1, 1>(device, p, 1, nullptr);
+    return buffer_reach(p.conv, batch) ? run_gemm<true, false, 4, 1>(device, p, 1, nullptr)
+                                       : run_gemm<true, false, 1, 1>(device, p, 1, nullptr);
 }
 
 int axis_conv2d_backward_data(axis_device device, const float *gradient, const float *weight,
@@ -1160,7 +1254,8 @@ int axis_conv2d_backward_data(axis_device device, const float *gradient, const f
     channels_last(s.out_h, s.out_w, out_channels, ld);
     p.conv = geom(gradient, ld, s.out_h, s.out_w, out_channels, height, width, s.kw, 1, 1,
                   s.kh - 1 - s.py, s.kw - 1 - s.px);
-    return run_gemm<true, false, 1, 0>(device, p, 1, d_input);
+    return buffer_reach(p.conv, batch) ? run_gemm<true, false, 4, 0>(device, p, 1, d_input)
+                                       : run_gemm<true, false, 1, 0>(device, p, 1, d_input);
 }
 
 int axis_conv2d_backward_weight(axis_device device, const float *input,
