@@ -455,15 +455,18 @@ struct ConvColsStepLoader : Staging<BT, BK, NT, false, VEC> {
         const uint32_t b = geom.oh_div.div(q);
         const int32_t oy0 = (int32_t)(q - b * (uint32_t)geom.out_h);
         const int32_t oys = oy0 * geom.sy, oxs = ox0 * geom.sx;
-        const uint32_t base = b * (uint32_t)geom.ld_b + (uint32_t)oys * (uint32_t)geom.ld_h +
-                              (uint32_t)oxs * (uint32_t)geom.ld_w;
+        // Buffer base at the step origin moved back by the padding, so that every valid lane's
+        // offset (at least -py rows and -px columns from the origin) is non-negative.
+        const int64_t shift = (int64_t)geom.py * geom.ld_h + (int64_t)geom.px * geom.ld_w;
+        const int64_t base = (int64_t)b * geom.ld_b + (int64_t)oys * geom.ld_h + (int64_t)oxs * geom.ld_w - shift;
+        const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(geom.src + base);
         const int64_t room = r_end - r0;  // pixels of this step inside the reduction
 #pragma unroll
         for (int e = 0; e < S::kVecs; ++e) {
             const bool valid = t_ok && s0 + e * kRowStep < room &&
                                (uint32_t)(oys + iy_rel[e]) < (uint32_t)geom.height &&
                                (uint32_t)(oxs + ix_rel[e]) < (uint32_t)geom.width;
-            load_into<VEC>(this->reg + e * VEC, geom.src + (valid ? base + rel[e] : 0u), valid);
+            buffer_into<VEC>(this->reg + e * VEC, rsrc, valid ? (rel[e] + (uint32_t)shift) * 4u : kOutside);
         }
     }
 };
