@@ -663,6 +663,77 @@ __global__ void __launch_bounds__(WM *WN * 64)
         const int pw = ow / kw;
         const int windows = BM / (kh * kw);
         const int64_t pooled_row0 = i0 / ow / kh;
+        if constexpr (FM == 2 && TM == 64) {
+            if (kh == 2 && kw == 2 && (ow == 16 || ow == 32)) {
+                // A whole 2x2 window sits in one lane: tile rows 2i and 2i+1 (horizontal
+                // neighbours) are acc[0] / acc[1], and the pixel row below (ow rows further, i.e.
+                // i + ow/2) is register v + ow/4.  The wave's 64 rows are whole window rows, so
+                // each lane pools its windows from registers: no LDS and no barrier.
+                // With two column blocks a lane's columns are adjacent (2 * l32 + b): both windows
+                // go out as one 8-byte value store and one 2-byte winner store when n is even.
+                const bool paired = FN == 2 && (p.n & 1) == 0 && (reinterpret_cast<uintptr_t>(p.pooled) & 7) == 0 &&
+                                    (reinterpret_cast<uintptr_t>(p.argmax) & 1) == 0;
+                float addv[FN];
+                bool okv[FN], biasv[FN];
+#pragma unroll
+                for (int b = 0; b < FN; ++b) {
+                    const int64_t col = j0 + wn * TN + col_in(b, l32);
+                    okv[b] = col < p.n;
+                    biasv[b] = p.bias != nullptr && okv[b];
+                    addv[b] = biasv[b] ? p.bias[col] : 0.0f;
+                }
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    // top-row registers: pixel row (2i) / ow even within the wave
+                    if (ow == 32 ? v >= 8 : ((v >> 2) & 1) != 0) continue;
+                    const int i = (v >> 2) * 8 + half * 4 + (v & 3);
+                    const int y = 2 * i / ow;
+                    const int64_t row = i0 + wm * TM + 2 * i;  // window's top-left pixel
+                    if (row >= p.m) continue;
+                    const int vb = ow == 32 ? v + 8 : v + 4;
+                    const int wr = (wm * TM) / (2 * ow) + y / 2;
+                    const int px = (2 * i - y * ow) / 2;
+                    float best[FN];
+                    int winner[FN];
+#pragma unroll
+                    for (int b = 0; b < FN; ++b) {
+                        best[b] = -INFINITY;
+                        winner[b] = 255;
+                        auto take = [&](float z, int at) {
+                            z = biasv[b] ? z + addv[b] : z;
+                            z = z > 0.0f ? z : 0.0f;
+                            if (z >= -FLT_MAX && z <= FLT_MAX && z > best[b]) {
+                                best[b] = z;
+                                winner[b] = at;
+                            }
+                        };
+                        take(acc[0][b][v], 0);
+                        take(acc[1][b][v], 1);
+                        take(acc[0][b][vb], 2);
+                        take(acc[1][b][vb], 3);
+                    }
+                    const int64_t col0 = j0 + wn * TN + col_in(0, l32);
+                    const int64_t out = ((pooled_row0 + wr) * pw + px) * p.n + col0;
+                    if (paired && okv[0]) {  // n even and col0 even: col0 + 1 < n as well
+                        float2 value;
+                        value.x = winner[0] == 255 ? __builtin_nanf("") : best[0];
+                        value.y = winner[FN - 1] == 255 ? __builtin_nanf("") : best[FN - 1];
+                        *reinterpret_cast<float2 *>(p.pooled + out) = value;
+                        *reinterpret_cast<uint16_t *>(p.argmax + out) =
+                            (uint16_t)(winner[0] | (winner[FN - 1] << 8));
+                    } else {
+#pragma unroll
+                        for (int b = 0; b < FN; ++b) {
+                            if (!okv[b]) continue;
+                            const int64_t o = out + (col_in(b, l32) - col_in(0, l32));
+                            p.pooled[o] = winner[b] == 255 ? __builtin_nanf("") : best[b];
+                            p.argmax[o] = (uint8_t)winner[b];
+                        }
+                    }
+                }
+                return;
+            }
+        }
 #pragma unroll
         for (int h = 0; h < WN; ++h) {
             __syncthreads();

@@ -607,6 +607,8 @@ FUSED_CASES = [
     ("nhwc", 3, 64, 8, 8, 128, (2, 2)),   # conv3-like, large tiles
     ("nhwc", 2, 5, 8, 8, 20, (2, 2)),     # scalar gathers, partial column tile
     ("nhwc", 2, 8, 8, 8, 72, (2, 4)),     # wide windows, two column tiles
+    ("nhwc", 2, 64, 32, 32, 128, (2, 2)), # conv2-like: 32-wide output, windows pooled in registers
+    ("nhwc", 2, 16, 16, 16, 256, (2, 2)), # 16-wide output in registers, two column tiles
 ]
 
 
