@@ -1,0 +1,494 @@
+// Convolutions whose whole patch reduction fits one short MFMA pass (channels * kh * kw <= 31,
+// stride 1): the first layer of an image network, e.g. 3 channels under a 3x3 kernel (27 terms).
+// The reference lowers them like every other convolution (convolution.rs:211-235: unfold ->
+// contract -> merge -> + bias; backward through Rule::MatmulRight, tensor.rs:5650-5680); with so
+// short a reduction the general implicit GEMM spends most of its time padding the reduction to its
+// 32-deep tiles and staging operands, so these kernels keep the whole reduction resident instead:
+//
+// * A block owns a band of pooling windows (R window rows x S window columns of one image) and
+//   stages the input rows the band reads, halo included, in LDS as planes [channel][row][column]
+//   with zeros outside the image.  Tap (c, ky, kx) of a pixel is then one LDS word at a fixed
+//   offset from the pixel, and the reduction runs in the reference's patch order (c, ky, kx).
+// * Pixels are numbered window-major (pixel 4w + 2*ky + kx is position (ky, kx) of window w), so
+//   the four consecutive rows a lane holds in each register group of a 32x32 MFMA block are one
+//   whole 2x2 window: bias, ReLU and the max pool (first strictly greater finite value, ky major)
+//   run in registers, and only pooled values and winner bytes reach HBM.
+// * The weight gradient of such a layer is computed straight from the pooled gradient, the
+//   pooled values and the winner bytes: the full-resolution pre-activation gradient (ReLU and
+//   pool backward) exists only in LDS, one band at a time.  Each 16x16x4 MFMA step reduces over
+//   the four pixels of one window.  A plane of ones in the staged input makes row `channels*kh*kw`
+//   of the product the bias gradient (the column sum of the same values).
+#include <cfloat>
+
+#include "common.hpp"
+#include "conv_small.hpp"
+#include "fastdiv.hpp"
+
+namespace {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+struct SmallConvArgs {
+    const float *x;
+    int64_t ld_b;
+    int32_t ld_c, ld_h, ld_w;
+    int32_t height, width, c_in, kh, kw, py, px;
+    int32_t out_h, out_w, n;
+    int32_t k;                   // c_in * kh * kw
+    int32_t win_rows, win_cols;  // ceil(out_h / 2), ceil(out_w / 2)
+    int32_t band_r, band_s;      // windows per band: R rows x S columns
+    int32_t bands_y, bands_x;    // bands per image along rows / columns
+    int32_t bands;
+    int32_t strip_h, strip_w, plane;  // staged rows (2R + kh - 1), columns (2S + kw - 1)
+    FastDiv s_div, bx_div, by_div, strip_w_div;
+    const float *w;     // [(c, ky, kx), n]
+    const float *bias;  // [n] or null
+    float *out;         // plain output [batch, out_h, out_w, n]
+    float *pooled;      // pooled output [batch, out_h/2, out_w/2, n]
+    uint8_t *argmax;
+    bool wide;          // outputs allow paired 8-byte stores (and 2-byte winner stores)
+    bool vec;           // gradient tensors allow 16-byte loads (n % 4 == 0, aligned)
+};
+
+struct Band {
+    uint32_t img;
+    int32_t wr0, wc0;  // first window row / column
+};
+
+__device__ __forceinline__ Band decode_band(const SmallConvArgs &a, uint32_t band) {
+    Band b;
+    const uint32_t q = a.bx_div.div(band);
+    b.wc0 = (int32_t)(band - q * (uint32_t)a.bands_x) * a.band_s;
+    b.img = a.by_div.div(q);
+    b.wr0 = (int32_t)(q - b.img * (uint32_t)a.bands_y) * a.band_r;
+    return b;
+}
+
+// Stages planes 0..c_in-1 of the band's input rows: strip[c][r][col] = x[img, 2*wr0 - py + r,
+// 2*wc0 - px + col, c], zero outside the image.
+__device__ __forceinline__ void fill_strip(const SmallConvArgs &a, const Band &b, float *strip, int tid) {
+    const int32_t iy0 = 2 * b.wr0 - a.py, ix0 = 2 * b.wc0 - a.px;
+    const int32_t cells = a.strip_h * a.strip_w;
+    const float *img = a.x + (int64_t)b.img * a.ld_b;
+    for (int32_t t = tid; t < cells; t += 256) {
+        const int32_t r = (int32_t)a.strip_w_div.div((uint32_t)t);
+        const int32_t col = t - r * a.strip_w;
+        const int32_t iy = iy0 + r, ix = ix0 + col;
+        const bool ok = (uint32_t)iy < (uint32_t)a.height && (uint32_t)ix < (uint32_t)a.width;
+        const float *src = img + (ok ? (int64_t)iy * a.ld_h + (int64_t)ix * a.ld_w : 0);
+        for (int32_t c = 0; c < a.c_in; ++c) strip[c * a.plane + t] = ok ? src[(int64_t)c * a.ld_c] : 0.0f;
+    }
+}
+
+// LDS offset of patch term k = (c, ky, kx) from its pixel; terms past the reduction read plane
+// `spare` (zeros in the forward, ones in the weight gradient).
+__device__ __forceinline__ int32_t term_offset(const SmallConvArgs &a, int32_t k, int32_t spare) {
+    if (k >= a.k) return spare * a.plane;
+    const int32_t taps = a.kh * a.kw;
+    const int32_t c = k / taps;
+    const int32_t t = k - c * taps;
+    const int32_t ky = t / a.kw;
+    return c * a.plane + ky * a.strip_w + (t - ky * a.kw);
+}
+
+// Forward: KP k-pairs of v_mfma_f32_32x32x2_f32 per pixel tile (2*KP >= k), 32 pixels (8
+// windows) by 64 output channels per wave.  POOL: bias + ReLU + 2x2 max pool in registers;
+// otherwise the plain convolution + bias.
+template <int KP, bool POOL>
+__global__ void __launch_bounds__(256, 4) small_conv_forward_kernel(SmallConvArgs a) {
+    extern __shared__ float strip[];  // planes 0..c_in-1: input; plane c_in: zeros
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l32 = lane & 31, half = lane >> 5;
+    const int32_t col0 = (int32_t)blockIdx.y * 64;
+
+    // MFMA B operand of k-pair j: W[2j + half][col0 + 2*l32 + b] (column block b holds the odd /
+    // even columns, so a lane's two columns are adjacent in the output).  A operand: LDS offset
+    // of term 2j + half from the pixel.
+    float wreg[KP][2];
+    int32_t off[KP];
+#pragma unroll
+    for (int j = 0; j < KP; ++j) {
+        const int32_t k = 2 * j + half;
+        off[j] = term_offset(a, k, a.c_in);
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const int32_t n = col0 + 2 * l32 + b;
+            wreg[j][b] = (k < a.k && n < a.n) ? a.w[(int64_t)k * a.n + n] : 0.0f;
+        }
+    }
+    float bias_v[2];
+    bool col_ok[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+        const int32_t n = col0 + 2 * l32 + b;
+        col_ok[b] = n < a.n;
+        bias_v[b] = (a.bias != nullptr && col_ok[b]) ? a.bias[n] : 0.0f;
+    }
+    const bool with_bias = a.bias != nullptr;
+    const bool paired = a.wide && col_ok[1];
+    for (int32_t t = tid; t < a.plane; t += 256) strip[a.c_in * a.plane + t] = 0.0f;
+
+    const int32_t band_windows = a.band_r * a.band_s;
+    const int32_t tiles = (band_windows + 7) / 8;
+    for (uint32_t band = blockIdx.x; band < (uint32_t)a.bands; band += gridDim.x) {
+        const Band bd = decode_band(a, band);
+        __syncthreads();  // the previous band's reads are done
+        fill_strip(a, bd, strip, tid);
+        __syncthreads();
+        for (int32_t tile = wave; tile < tiles; tile += 4) {
+            // Row i = l32: window tile*8 + i/4, position i%4 = (ky, kx) of the window.
+            int32_t wi = tile * 8 + (l32 >> 2);
+            wi = wi < band_windows ? wi : band_windows - 1;
+            const int32_t pr = (int32_t)a.s_div.div((uint32_t)wi);
+            const int32_t pc = wi - pr * a.band_s;
+            const float *px0 = strip + (2 * pr + ((l32 >> 1) & 1)) * a.strip_w + 2 * pc + (l32 & 1);
+            floatx16 acc[2];
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[b][v] = 0.0f;
+#pragma unroll
+            for (int j = 0; j < KP; ++j) {
+                const float av = px0[off[j]];
+#pragma unroll
+                for (int b = 0; b < 2; ++b)
+                    acc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, wreg[j][b], acc[b], 0, 0, 0);
+            }
+            // Accumulator register v: row i = 8*(v/4) + 4*half + v%4, i.e. window
+            // tile*8 + 2*(v/4) + half, position v%4.
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int32_t wt = tile * 8 + 2 * q + half;
+                if (wt >= band_windows || !col_ok[0]) continue;
+                const int32_t wr = (int32_t)a.s_div.div((uint32_t)wt);
+                const int32_t wc = wt - wr * a.band_s;
+                if constexpr (POOL) {
+                    if (bd.wr0 + wr >= a.win_rows || bd.wc0 + wc >= a.win_cols) continue;
+                    float best[2];
+                    int winner[2];
+#pragma unroll
+                    for (int b = 0; b < 2; ++b) {
+                        best[b] = -INFINITY;
+                        winner[b] = 255;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            float z = acc[b][4 * q + e];
+                            z = with_bias ? z + bias_v[b] : z;
+                            z = z > 0.0f ? z : 0.0f;
+                            if (z <= FLT_MAX && z > best[b]) {
+                                best[b] = z;
+                                winner[b] = e;
+                            }
+                        }
+                    }
+                    const int64_t pix = ((int64_t)bd.img * a.win_rows + bd.wr0 + wr) * a.win_cols + bd.wc0 + wc;
+                    const int64_t o = pix * a.n + col0 + 2 * l32;
+                    if (paired) {
+                        float2 value;
+                        value.x = winner[0] == 255 ? __builtin_nanf("") : best[0];
+                        value.y = winner[1] == 255 ? __builtin_nanf("") : best[1];
+                        *reinterpret_cast<float2 *>(a.pooled + o) = value;
+                        *reinterpret_cast<uint16_t *>(a.argmax + o) = (uint16_t)(winner[0] | (winner[1] << 8));
+                    } else {
+#pragma unroll
+                        for (int b = 0; b < 2; ++b) {
+                            if (!col_ok[b]) continue;
+                            a.pooled[o + b] = winner[b] == 255 ? __builtin_nanf("") : best[b];
+                            a.argmax[o + b] = (uint8_t)winner[b];
+                        }
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int32_t y = 2 * (bd.wr0 + wr) + (e >> 1), x = 2 * (bd.wc0 + wc) + (e & 1);
+                        if (y >= a.out_h || x >= a.out_w) continue;
+                        const int64_t o = (((int64_t)bd.img * a.out_h + y) * a.out_w + x) * a.n + col0 + 2 * l32;
+                        const float v0 = with_bias ? acc[0][4 * q + e] + bias_v[0] : acc[0][4 * q + e];
+                        const float v1 = with_bias ? acc[1][4 * q + e] + bias_v[1] : acc[1][4 * q + e];
+                        if (paired) {
+                            *reinterpret_cast<float2 *>(a.out + o) = make_float2(v0, v1);
+                        } else {
+                            a.out[o] = v0;
+                            if (col_ok[1]) a.out[o + 1] = v1;
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
+
+// Weight and bias gradient through ReLU -> 2x2 max pool: per band, the pre-activation gradient of
+// the band's windows is expanded into LDS as dy[window][position][64 columns] (0.0f + g at the
+// window's winner when the pooled value is positive, else 0 -- the values axis_relu_pool_backward
+// writes), then C^T[n][t] += sum over the window's 4 pixels of dy[p][n] * X[p][t] on
+// v_mfma_f32_16x16x4_f32 (A = dy^T: lane -> (n = l%16, p = l/16); B = X: lane -> (p = l/16,
+// t = l%16)).  Term t = k is the ones plane: the bias gradient.  Each block writes its partial
+// C^T as [32 terms][n]; partials are summed in block order afterwards.
+__global__ void __launch_bounds__(256, 4) small_conv_pool_wgrad_kernel(SmallConvArgs a, const float *__restrict__ g,
+                                                                         const float *__restrict__ pooled,
+                                                                         const uint8_t *__restrict__ argmax,
+                                                                         float *__restrict__ partial) {
+    extern __shared__ float lds[];
+    float *const strip = lds;                                   // planes 0..c_in-1: input; c_in: ones
+    float *const dy = lds + ((a.c_in + 1) * a.plane + 3) / 4 * 4;  // [window][4][64]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nl = lane & 15, pos = lane >> 4;
+    const int32_t col0 = (int32_t)blockIdx.y * 64;
+    const int32_t toff[2] = {term_offset(a, nl, a.c_in), term_offset(a, nl + 16, a.c_in)};
+    for (int32_t t = tid; t < a.plane; t += 256) strip[a.c_in * a.plane + t] = 1.0f;
+
+    floatx4 acc[4][2];
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[nb][kb][v] = 0.0f;
+
+    const int32_t band_windows = a.band_r * a.band_s;
+    const bool vec = a.vec;
+    for (uint32_t band = blockIdx.x; band < (uint32_t)a.bands; band += gridDim.x) {
+        const Band bd = decode_band(a, band);
+        __syncthreads();
+        fill_strip(a, bd, strip, tid);
+        // 16 column vectors of 4 per window
+        for (int32_t t = tid; t < band_windows * 16; t += 256) {
+            const int32_t wi = t >> 4, c4 = (t & 15) * 4;
+            const int32_t wr = (int32_t)a.s_div.div((uint32_t)wi);
+            const int32_t wc = wi - wr * a.band_s;
+            const bool win_ok = bd.wr0 + wr < a.win_rows && bd.wc0 + wc < a.win_cols;
+            const int64_t pix = ((int64_t)bd.img * a.win_rows + bd.wr0 + wr) * a.win_cols + bd.wc0 + wc;
+            const int64_t base = pix * a.n + col0 + c4;
+            float gv[4] = {0.0f, 0.0f, 0.0f, 0.0f}, pv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            int av[4] = {255, 255, 255, 255};
+            if (win_ok && vec && col0 + c4 < a.n) {
+                const floatx4 g4 = *reinterpret_cast<const floatx4 *>(g + base);
+                const floatx4 p4 = *reinterpret_cast<const floatx4 *>(pooled + base);
+                const uint32_t a4 = *reinterpret_cast<const uint32_t *>(argmax + base);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    gv[e] = g4[e];
+                    pv[e] = p4[e];
+                    av[e] = (int)((a4 >> (8 * e)) & 0xffu);
+                }
+            } else if (win_ok) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (col0 + c4 + e < a.n) {
+                        gv[e] = g[base + e];
+                        pv[e] = pooled[base + e];
+                        av[e] = argmax[base + e];
+                    }
+            }
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                floatx4 o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[e] = (av[e] == p && pv[e] > 0.0f) ? 0.0f + gv[e] : 0.0f;
+                *reinterpret_cast<floatx4 *>(dy + (wi * 4 + p) * 64 + c4) = o;
+            }
+        }
+        __syncthreads();
+        for (int32_t wi = wave; wi < band_windows; wi += 4) {
+            const int32_t wr = (int32_t)a.s_div.div((uint32_t)wi);
+            const int32_t wc = wi - wr * a.band_s;
+            const float *px0 = strip + (2 * wr + (pos >> 1)) * a.strip_w + 2 * wc + (pos & 1);
+            const float x0 = px0[toff[0]], x1 = px0[toff[1]];
+            const float *dyw = dy + (wi * 4 + pos) * 64 + nl;
+#pragma unroll
+            for (int nb = 0; nb < 4; ++nb) {
+                const float d = dyw[16 * nb];
+                acc[nb][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(d, x0, acc[nb][0], 0, 0, 0);
+                acc[nb][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(d, x1, acc[nb][1], 0, 0, 0);
+            }
+        }
+    }
+    // The four waves' sums meet in LDS ([wave][term][64 columns], over the gradient expansion) and
+    // are added in wave order.  D register v of lane l: column 4*(l/16) + v (+16 nb), term l%16
+    // (+16 kb).
+    __syncthreads();
+    float *const red = dy;
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) red[(wave * 32 + nl + 16 * kb) * 64 + 16 * nb + 4 * pos + v] = acc[nb][kb][v];
+    __syncthreads();
+    float *dst = partial + (int64_t)blockIdx.x * 32 * a.n;
+    for (int32_t e = tid; e < 32 * 64; e += 256) {
+        const int32_t t = e >> 6, col = col0 + (e & 63);
+        const float sum = ((red[e] + red[2048 + e]) + red[4096 + e]) + red[6144 + e];
+        if (col < a.n) dst[(int64_t)t * a.n + col] = sum;
+    }
+}
+
+// d_weight[t][n] (t < k) and d_bias[n] (t = k) = sum over blocks of partial[block][t][n], in block
+// order per lane and a fixed pairwise tree over the 256 lanes: the same association on every run.
+__global__ void __launch_bounds__(256) small_conv_combine_kernel(const float *__restrict__ partial, int32_t blocks,
+                                                                 int32_t n, int32_t k, float *__restrict__ d_weight,
+                                                                 float *__restrict__ d_bias) {
+    __shared__ float s[256];
+    const int32_t e = blockIdx.x;  // t * n + column
+    float v = 0.0f;
+    for (int32_t b = threadIdx.x; b < blocks; b += 256) v += partial[((int64_t)b * 32) * n + e];
+    s[threadIdx.x] = v;
+    __syncthreads();
+    for (int h = 128; h > 0; h >>= 1) {
+        if ((int)threadIdx.x < h) s[threadIdx.x] = s[threadIdx.x] + s[threadIdx.x + h];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        if (e < k * n)
+            d_weight[e] = s[0];
+        else if (d_bias)
+            d_bias[e - k * n] = s[0];
+    }
+}
+
+// Windows per band: S columns (at most 32) by R rows, R * S <= cap.
+void band_shape(SmallConvArgs &a, int64_t batch, int32_t cap) {
+    a.band_s = a.win_cols < 32 ? a.win_cols : 32;
+    a.band_r = cap / a.band_s;
+    if (a.band_r < 1) a.band_r = 1;
+    if (a.band_r > a.win_rows) a.band_r = a.win_rows;
+    a.bands_x = (a.win_cols + a.band_s - 1) / a.band_s;
+    a.bands_y = (a.win_rows + a.band_r - 1) / a.band_r;
+    a.bands = (int32_t)(batch * a.bands_x * a.bands_y);
+    a.strip_h = 2 * a.band_r + a.kh - 1;
+    a.strip_w = 2 * a.band_s + a.kw - 1;
+    a.plane = a.strip_h * a.strip_w;
+    a.s_div = FastDiv((uint32_t)a.band_s);
+    a.bx_div = FastDiv((uint32_t)a.bands_x);
+    a.by_div = FastDiv((uint32_t)a.bands_y);
+    a.strip_w_div = FastDiv((uint32_t)a.strip_w);
+}
+
+int make_args(const axis::SmallConvShape &s, const float *input, const int64_t ld[4], const float *weight,
+              const float *bias, int32_t cap, SmallConvArgs &a) {
+    a = SmallConvArgs{};
+    a.x = input;
+    if (ld) {
+        a.ld_b = ld[0];
+        a.ld_c = (int32_t)ld[1];
+        a.ld_h = (int32_t)ld[2];
+        a.ld_w = (int32_t)ld[3];
+    }
+    a.height = s.height;
+    a.width = s.width;
+    a.c_in = s.channels;
+    a.kh = s.kh;
+    a.kw = s.kw;
+    a.py = s.py;
+    a.px = s.px;
+    a.out_h = s.out_h;
+    a.out_w = s.out_w;
+    a.n = s.out_channels;
+    a.k = s.channels * s.kh * s.kw;
+    a.win_rows = (s.out_h + 1) / 2;
+    a.win_cols = (s.out_w + 1) / 2;
+    a.w = weight;
+    a.bias = bias;
+    band_shape(a, s.batch, cap);
+    return AXIS_OK;
+}
+
+size_t strip_bytes(const SmallConvArgs &a) {
+    return sizeof(float) * (size_t)(((a.c_in + 1) * a.plane + 3) / 4 * 4);
+}
+
+// The weight gradient's expansion [window][4][64], also the four waves' [32][64] sums at the end.
+size_t gradient_bytes(const SmallConvArgs &a) {
+    const size_t expansion = (size_t)a.band_r * a.band_s * 4 * 64;
+    return sizeof(float) * (expansion > 4 * 32 * 64 ? expansion : 4 * 32 * 64);
+}
+
+unsigned persistent_blocks(axis_device device, int64_t bands, int64_t columns) {
+    const int64_t slots = (int64_t)device->multiprocessors * 4 / (columns > 0 ? columns : 1);
+    int64_t per = (bands + (slots > 0 ? slots : 1) - 1) / (slots > 0 ? slots : 1);
+    if (per < 1) per = 1;
+    return (unsigned)((bands + per - 1) / per);
+}
+
+template <bool POOL>
+int launch_forward(axis_device device, const SmallConvArgs &a) {
+    const int kp = (a.k + 1) / 2;
+    const unsigned columns = (unsigned)((a.n + 63) / 64);
+    dim3 grid(persistent_blocks(device, a.bands, columns), columns);
+    const size_t lds = strip_bytes(a);
+    hipStream_t st = device->stream;
+#define AXIS_SMALL_FWD(KPV)                                                      \
+    if (kp <= KPV) {                                                             \
+        small_conv_forward_kernel<KPV, POOL><<<grid, 256, lds, st>>>(a);         \
+        return axis::launch_status("small_conv_forward_kernel");                 \
+    }
+    AXIS_SMALL_FWD(2)
+    AXIS_SMALL_FWD(4)
+    AXIS_SMALL_FWD(6)
+    AXIS_SMALL_FWD(8)
+    AXIS_SMALL_FWD(10)
+    AXIS_SMALL_FWD(12)
+    AXIS_SMALL_FWD(14)
+    AXIS_SMALL_FWD(16)
+#undef AXIS_SMALL_FWD
+    return axis::fail(AXIS_ERROR_INVALID, "small convolution reduction too long");
+}
+
+}  // namespace
+
+namespace axis {
+
+bool small_conv_applies(const SmallConvShape &s) {
+    if (s.sy != 1 || s.sx != 1 || s.out_h < 1 || s.out_w < 1) return false;
+    if ((int64_t)s.channels * s.kh * s.kw > 31) return false;
+    if (s.py > s.kh - 1 || s.px > s.kw - 1) return false;
+    if (s.batch * ((s.out_h + 1) / 2) * ((s.out_w + 1) / 2) >= INT32_MAX) return false;
+    // four blocks per CU: the staged band (and the backward's gradient expansion) within 40 KiB
+    SmallConvArgs fwd, bwd;
+    make_args(s, nullptr, nullptr, nullptr, nullptr, 64, fwd);
+    make_args(s, nullptr, nullptr, nullptr, nullptr, 32, bwd);
+    const size_t limit = 40 * 1024;
+    return strip_bytes(fwd) <= limit && strip_bytes(bwd) + gradient_bytes(bwd) <= limit;
+}
+
+int small_conv_forward(axis_device device, const SmallConvShape &s, const float *input, const int64_t ld[4],
+                       const float *weight, const float *bias, float *out, float *pooled, uint8_t *argmax) {
+    SmallConvArgs a;
+    if (int st = make_args(s, input, ld, weight, bias, 64, a)) return st;
+    a.out = out;
+    a.pooled = pooled;
+    a.argmax = argmax;
+    a.wide = (a.n & 1) == 0 && (pooled ? (reinterpret_cast<uintptr_t>(pooled) & 7) == 0 &&
+                                              (reinterpret_cast<uintptr_t>(argmax) & 1) == 0
+                                        : (reinterpret_cast<uintptr_t>(out) & 7) == 0);
+    TimedLaunch timed(device, "gemm", 2.0 * (double)s.batch * s.out_h * s.out_w * s.out_channels * a.k);
+    return pooled ? launch_forward<true>(device, a) : launch_forward<false>(device, a);
+}
+
+int small_conv_pool_backward_weight(axis_device device, const SmallConvShape &s, const float *input,
+                                    const int64_t ld[4], const float *gradient, const float *pooled,
+                                    const uint8_t *argmax, float *d_weight, float *d_bias) {
+    SmallConvArgs a;
+    if (int st = make_args(s, input, ld, nullptr, nullptr, 32, a)) return st;
+    a.vec = (a.n & 3) == 0 && aligned16(gradient) && aligned16(pooled) &&
+            (reinterpret_cast<uintptr_t>(argmax) & 3) == 0;
+    const unsigned columns = (unsigned)((a.n + 63) / 64);
+    const unsigned blocks = persistent_blocks(device, a.bands, columns);
+    Scratch partial;
+    if (int st = partial.get(device, sizeof(float) * (size_t)blocks * 32 * (size_t)a.n)) return st;
+    const size_t lds = strip_bytes(a) + gradient_bytes(a);
+    {
+        TimedLaunch timed(device, "gemm", 2.0 * (double)s.batch * s.out_h * s.out_w * s.out_channels * a.k);
+        small_conv_pool_wgrad_kernel<<<dim3(blocks, columns), 256, lds, device->stream>>>(a, gradient, pooled, argmax,
+                                                                                          partial.as<float>());
+        if (int st = launch_status("small_conv_pool_wgrad_kernel")) return st;
+    }
+    const int32_t outputs = (a.k + (d_bias ? 1 : 0)) * a.n;
+    small_conv_combine_kernel<<<outputs, 256, 0, device->stream>>>(partial.as<float>(), (int32_t)blocks, a.n, a.k,
+                                                                   d_weight, d_bias);
+    return launch_status("small_conv_combine_kernel");
+}
+
+}  // namespace axis

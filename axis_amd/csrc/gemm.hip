@@ -31,6 +31,7 @@
 #include <type_traits>
 
 #include "common.hpp"
+#include "conv_small.hpp"
 #include "fastdiv.hpp"
 
 namespace {
@@ -1095,6 +1096,11 @@ int conv_shape(int64_t batch, int32_t height, int32_t width, int32_t channels, i
     return AXIS_OK;
 }
 
+axis::SmallConvShape small_shape(const ConvShape &s) {
+    return axis::SmallConvShape{s.batch, s.height, s.width, s.channels, s.out_channels, s.kh, s.kw,
+                                s.sy,    s.sx,     s.py,    s.px,       s.out_h,        s.out_w};
+}
+
 // Strides of a channel-innermost contiguous [batch, height, width, channels] tensor.
 void channels_last(int32_t height, int32_t width, int32_t channels, int64_t ld[4]) {
     ld[0] = (int64_t)height * width * channels;
@@ -1292,6 +1298,11 @@ int axis_conv2d_forward(axis_device device, const float *input, const int64_t in
     ConvShape s{};
     if (int st = conv_shape(batch, height, width, channels, out_channels, kernel, stride, padding, &s))
         return st;
+    if (axis::small_conv_applies(small_shape(s))) {
+        int64_t ld[4];
+        if (int st = input_strides(input_strides_, batch, height, width, channels, ld)) return st;
+        return axis::small_conv_forward(device, small_shape(s), input, ld, weight, bias, out, nullptr, nullptr);
+    }
     GatherInput in;
     if (int st = in.prepare(device, input, input_strides_, batch, height, width, channels)) return st;
     const int64_t patch = (int64_t)in.channels * s.kh * s.kw;
@@ -1330,6 +1341,9 @@ int axis_conv2d_relu_pool_forward(axis_device device, const float *input,
                  "pool window must be positive with fewer than 255 positions");
     AXIS_REQUIRE(s.out_h % pool[0] == 0 && s.out_w % pool[1] == 0,
                  "fused pooling needs windows that tile the convolution output exactly");
+    if (pool[0] == 2 && pool[1] == 2 && axis::small_conv_applies(small_shape(s)))
+        return axis::small_conv_forward(device, small_shape(s), input, ld_check, weight, bias, nullptr, pooled,
+                                        argmax);
     AXIS_REQUIRE(128 % (pool[0] * s.out_w) == 0,
                  "fused pooling needs pool height x output width to divide 128");
     GatherInput in;
@@ -1426,6 +1440,38 @@ int axis_conv2d_backward_weight(axis_device device, const float *input,
                            : run_gemm<false, false, 2, 0>(device, p, 1, ordered.as<float>());
     if (st) return st;
     return permute_weight(device, ordered.as<float>(), d_weight, s, 2, in.channels);
+}
+
+
+int axis_conv2d_relu_pool_backward_weight(axis_device device, const float *input,
+                                          const int64_t input_strides_[4], const float *gradient,
+                                          const float *pooled, const uint8_t *argmax, float *d_weight,
+                                          float *d_bias, int64_t batch, int32_t height, int32_t width,
+                                          int32_t channels, int32_t out_channels, const int32_t kernel[2],
+                                          const int32_t stride[2], const int32_t padding[2],
+                                          const int32_t pool[2]) {
+    AXIS_ENTER(device);
+    AXIS_REQUIRE(input && gradient && pooled && argmax && d_weight && pool, "null convolution buffer");
+    ConvShape s{};
+    if (int st = conv_shape(batch, height, width, channels, out_channels, kernel, stride, padding, &s))
+        return st;
+    int64_t ld[4];
+    if (int st = input_strides(input_strides_, batch, height, width, channels, ld)) return st;
+    AXIS_REQUIRE(pool[0] >= 1 && pool[1] >= 1 && pool[0] * pool[1] < 255 && s.out_h % pool[0] == 0 &&
+                     s.out_w % pool[1] == 0,
+                 "fused pooling needs windows that tile the convolution output exactly");
+    if (pool[0] == 2 && pool[1] == 2 && axis::small_conv_applies(small_shape(s)))
+        return axis::small_conv_pool_backward_weight(device, small_shape(s), input, ld, gradient, pooled, argmax,
+                                                     d_weight, d_bias);
+    // Any other shape: the pre-activation gradient through axis_relu_pool_backward, then the
+    // weight gradient of the convolution.
+    axis::Scratch d_pre;
+    if (int st = d_pre.get(device, sizeof(float) * (size_t)(batch * s.out_h * s.out_w * out_channels))) return st;
+    if (int st = axis_relu_pool_backward(device, gradient, pooled, argmax, d_pre.as<float>(), d_bias, batch, s.out_h,
+                                         s.out_w, out_channels, pool))
+        return st;
+    return axis_conv2d_backward_weight(device, input, input_strides_, d_pre.as<float>(), d_weight, batch, height,
+                                       width, channels, out_channels, kernel, stride, padding);
 }
 
 }  // extern "C"

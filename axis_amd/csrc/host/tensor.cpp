@@ -891,6 +891,9 @@ void Tensor::backward() const {
     // Bias gradients produced together with a ReLU backward (one pass over the activation), keyed
     // by the bias-add node whose BiasBroadcast edge they answer.
     std::unordered_map<uint64_t, Buffer> fused_bias;
+    // Weight gradients produced together with a ReLU/pool backward, keyed by the convolution's
+    // pre-activation node: that node then carries no adjoint buffer.
+    std::unordered_map<uint64_t, Buffer> fused_weight;
     adjoints[id()] = dev.filled(1, 1.0f);
     std::vector<std::pair<Tensor, Buffer>> leaves;
     for (auto it = order.rbegin(); it != order.rend(); ++it) {
@@ -992,6 +995,12 @@ void Tensor::backward() const {
                     break;
                 }
                 case Rule::ConvWeight: {
+                    auto fused = fused_weight.find(nd.id());
+                    if (fused != fused_weight.end()) {
+                        c = fused->second;
+                        fused_weight.erase(fused);
+                        break;
+                    }
                     const ConvGeometry &q = r.conv;
                     c = dev.alloc((int64_t)q.channels * q.kernel[0] * q.kernel[1] * q.out_channels);
                     check(axis_conv2d_backward_weight(dev.h(), r.a->f32(), q.strides(), g->f32(), c->f32(), q.batch,
@@ -1004,19 +1013,44 @@ void Tensor::backward() const {
                     // The pre-activation node's bias gradient comes out of the same pass when that
                     // node has exactly one BiasBroadcast edge and no other reader.
                     const PoolGeometry &p = r.pool;
-                    c = dev.alloc(p.outer * p.height * p.width * p.channels);
                     const std::shared_ptr<Node> &x = e.input.n;
                     const Rule *bias_rule = nullptr;
+                    const Rule *weight_rule = nullptr;
+                    bool others = false;
                     if (uses[x->id] == 1 && x->edges) {
-                        int biases = 0;
-                        for (auto &xe : *x->edges)
+                        int biases = 0, weights = 0;
+                        for (auto &xe : *x->edges) {
                             if (xe.rule.kind == Rule::BiasBroadcast) bias_rule = &xe.rule, ++biases;
+                            else if (xe.rule.kind == Rule::ConvWeight) weight_rule = &xe.rule, ++weights;
+                            else others = true;
+                        }
                         if (biases != 1) bias_rule = nullptr;
+                        if (weights != 1) weight_rule = nullptr, others = true;
                     }
+                    if (bias_rule && !(bias_rule->inner == p.channels &&
+                                       bias_rule->outer == p.outer * p.height * p.width))
+                        bias_rule = nullptr, others = true;
+                    if (weight_rule && !others && weight_rule->conv.out_channels == p.channels &&
+                        weight_rule->conv.batch == p.outer) {
+                        // The convolution's only gradients are its weight and bias (its input
+                        // needs none): both straight from the pooled gradient, without the
+                        // pre-activation gradient.
+                        const ConvGeometry &q = weight_rule->conv;
+                        Buffer dw = dev.alloc((int64_t)q.channels * q.kernel[0] * q.kernel[1] * q.out_channels);
+                        Buffer db = bias_rule ? dev.alloc(p.channels) : Buffer();
+                        check(axis_conv2d_relu_pool_backward_weight(
+                                  dev.h(), weight_rule->a->f32(), q.strides(), g->f32(), r.b->f32(),
+                                  static_cast<const uint8_t *>(r.a->ptr), dw->f32(), db ? db->f32() : nullptr,
+                                  q.batch, q.height, q.width, q.channels, q.out_channels, q.kernel, q.stride,
+                                  q.padding, p.kernel),
+                              "conv2d_relu_pool_backward_weight");
+                        fused_weight[x->id] = dw;
+                        if (db) fused_bias[x->id] = db;
+                        break;  // c stays empty: every edge of x is answered from the maps
+                    }
+                    c = dev.alloc(p.outer * p.height * p.width * p.channels);
                     Buffer db;
-                    if (bias_rule && bias_rule->inner == p.channels &&
-                        bias_rule->outer == p.outer * p.height * p.width)
-                        db = dev.alloc(p.channels);
+                    if (bias_rule) db = dev.alloc(p.channels);
                     check(axis_relu_pool_backward(dev.h(), g->f32(), r.b->f32(),
                                                   static_cast<const uint8_t *>(r.a->ptr), c->f32(),
                                                   db ? db->f32() : nullptr, p.outer, p.height, p.width,

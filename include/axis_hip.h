@@ -284,8 +284,9 @@ int axis_broadcast_middle(axis_device device, const float *gradient, float *out,
  * contiguous [batch, height, width, channels]); weight in the reference's layout
  * [(channel, ky, kx), out_channels]; bias [out_channels] or NULL;
  * out [batch, out_h, out_w, out_channels] (the reference's unfold output order).  The patch
- * reduction runs in (ky, kx, channel) order on fp32 MFMA, so results agree with the explicit path
- * to fp32 tolerance. */
+ * reduction runs in (ky, kx, channel) order on fp32 MFMA -- in (channel, ky, kx) order for short
+ * layers (stride 1, channels * kh * kw <= 31) -- so results agree with the explicit path to fp32
+ * tolerance. */
 int axis_conv2d_forward(axis_device device, const float *input, const int64_t input_strides[4],
                         const float *weight, const float *bias, float *out, int64_t batch,
                         int32_t height, int32_t width, int32_t channels, int32_t out_channels,
@@ -295,8 +296,10 @@ int axis_conv2d_forward(axis_device device, const float *input, const int64_t in
  * tensor.rs:2136-2147, convolution.rs:1357-1370) with the pre-activation never written.
  * pooled and argmax are [batch, out_h/pool[0], out_w/pool[1], out_channels]; argmax holds the
  * window-local winner ky*pool[1]+kx (255 with a NaN output when no finite value exists), as
- * axis_max_pool2d.  Requires out_h % pool[0] == 0, out_w % pool[1] == 0 and
- * 128 % (pool[0] * out_w) == 0. */
+ * axis_max_pool2d.  Requires out_h % pool[0] == 0, out_w % pool[1] == 0 and, unless the
+ * layer is short (stride 1, channels * kh * kw <= 31, 2x2 pool), 128 % (pool[0] * out_w) == 0.
+ * Short layers reduce in the reference's patch order (channel, ky, kx), as axis_conv2d_forward
+ * does for them, so the two entries agree bit for bit there. */
 int axis_conv2d_relu_pool_forward(axis_device device, const float *input,
                                   const int64_t input_strides[4], const float *weight,
                                   const float *bias, float *pooled, uint8_t *argmax, int64_t batch,
@@ -320,6 +323,23 @@ int axis_conv2d_backward_weight(axis_device device, const float *input,
                                 float *d_weight, int64_t batch, int32_t height, int32_t width,
                                 int32_t channels, int32_t out_channels, const int32_t kernel[2],
                                 const int32_t stride[2], const int32_t padding[2]);
+/* Weight and bias gradients of Conv2d -> ReLU -> MaxPool2d (the composition
+ * axis_conv2d_relu_pool_forward computes) straight from the pool's outputs: the reference's
+ * Rule::Minimum gather + mask and Rule::Relu (tensor.rs:5679-5683, :2136-2147) into the
+ * convolution's Rule::MatmulRight (tensor.rs:5650-5680) and the bias's column sum
+ * (tensor.rs:706-778).  Equals axis_relu_pool_backward followed by axis_conv2d_backward_weight
+ * (to fp32 tolerance; deterministic run to run); when stride is 1, channels * kh * kw <= 31 and
+ * the pool is 2x2, the pre-activation gradient is never written to device memory.  gradient,
+ * pooled and argmax are [batch, out_h/pool[0], out_w/pool[1], out_channels]; d_weight
+ * [(channel, ky, kx), out_channels]; d_bias [out_channels] or NULL; input strides as in
+ * axis_conv2d_forward. */
+int axis_conv2d_relu_pool_backward_weight(axis_device device, const float *input,
+                                          const int64_t input_strides[4], const float *gradient,
+                                          const float *pooled, const uint8_t *argmax, float *d_weight,
+                                          float *d_bias, int64_t batch, int32_t height, int32_t width,
+                                          int32_t channels, int32_t out_channels, const int32_t kernel[2],
+                                          const int32_t stride[2], const int32_t padding[2],
+                                          const int32_t pool[2]);
 /* Backward of ReLU -> non-overlapping max pool given the pool's outputs (Rule::Minimum gather +
  * mask, col2im, tensor.rs:5679-5683; Rule::Relu, tensor.rs:2136-2147): d_pre
  * [outer, height, width, channels] holds 0.0f + gradient at each window's winner when the pooled

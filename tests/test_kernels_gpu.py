@@ -609,6 +609,9 @@ FUSED_CASES = [
     ("nhwc", 2, 8, 8, 8, 72, (2, 4)),     # wide windows, two column tiles
     ("nhwc", 2, 64, 32, 32, 128, (2, 2)), # conv2-like: 32-wide output, windows pooled in registers
     ("nhwc", 2, 16, 16, 16, 256, (2, 2)), # 16-wide output in registers, two column tiles
+    ("nchw", 2, 3, 64, 64, 64, (2, 2)),   # conv1 at full image size (short reduction)
+    ("nchw", 1, 3, 14, 72, 96, (2, 2)),   # short reduction: 36 windows per row, partial column group
+    ("nhwc", 2, 2, 6, 10, 32, (2, 2)),    # short reduction, bands of several window rows
 ]
 
 
@@ -679,6 +682,78 @@ def test_conv2d_relu_pool_rejects_partial_windows(dev):
     with pytest.raises(hip.AxisError, match="divide 128"):
         dev.call("axis_conv2d_relu_pool_forward", buf.vp, None, buf.vp, None, buf.vp, arg.vp, I64(1), I32(8),
                  I32(96), I32(4), I32(8), *geo, (I32 * 2)(2, 2))
+
+
+RELU_POOL_WGRAD_CASES = [
+    # layout, b, c, h, w, n, padding, bias
+    ("nchw", 2, 3, 16, 16, 64, 1, True),    # conv1 of the CNN (short reduction, fused)
+    ("nchw", 1, 3, 64, 64, 64, 1, True),    # conv1 at full image size
+    ("nhwc", 3, 2, 12, 20, 96, 1, True),    # two column groups, the second partial
+    ("nchw", 2, 1, 10, 70, 32, 1, False),   # 35 windows per row: two bands across; no bias
+    ("nchw", 2, 3, 18, 18, 64, 0, True),    # no padding
+    ("nhwc", 2, 8, 8, 8, 16, 1, True),      # 72-term reduction: composed from the separate entries
+]
+
+
+@pytest.mark.parametrize("case", range(len(RELU_POOL_WGRAD_CASES)))
+def test_conv2d_relu_pool_backward_weight(dev, oracle, case):
+    layout, b, c, h, w, n, p, with_bias = RELU_POOL_WGRAD_CASES[case]
+    k = 3
+    oh, ow = h + 2 * p - k + 1, w + 2 * p - k + 1
+    rng = np.random.default_rng(70 + case)
+    x = rng.uniform(-1, 1, b * c * h * w).astype(np.float32)
+    weight = rng.standard_normal(c * k * k * n).astype(np.float32) * 0.3
+    bias = rng.standard_normal(n).astype(np.float32) * 0.1
+    if layout == "nchw":
+        dims = [("batch", b), ("c", c), ("height", h), ("width", w)]
+        strides = (I64 * 4)(c * h * w, h * w, w, 1)
+    else:
+        dims = [("batch", b), ("height", h), ("width", w), ("c", c)]
+        strides = None
+    geo = [(I32 * 2)(k, k), (I32 * 2)(1, 1), (I32 * 2)(p, p)]
+    win = (I32 * 2)(2, 2)
+    pooled_len = b * (oh // 2) * (ow // 2) * n
+    dx, dw, db = up(dev, x), up(dev, weight), up(dev, bias)
+    pooled, arg = dev.empty(pooled_len), dev.empty(pooled_len, np.uint8)
+    dev.call("axis_conv2d_relu_pool_forward", dx.vp, strides, dw.vp, db.vp, pooled.vp, arg.vp, I64(b), I32(h),
+             I32(w), I32(c), I32(n), *geo, win)
+    pv, av = dev.read(pooled, pooled_len), dev.read(arg, pooled_len, np.uint8)
+    g = rng.standard_normal(pooled_len).astype(np.float32)
+    g[::13] = 0.0
+    dg = up(dev, g)
+    # the pre-activation gradient the pooled tensors imply: g at each positive window's winner
+    d_pre = np.zeros((b, oh // 2, ow // 2, n, 4), np.float32)
+    sel = (pv > 0).reshape(b, oh // 2, ow // 2, n)
+    a4 = av.reshape(b, oh // 2, ow // 2, n)
+    for pos in range(4):
+        d_pre[..., pos] = np.where(sel & (a4 == pos), np.float32(0) + g.reshape(b, oh // 2, ow // 2, n), 0.0)
+    d_pre = d_pre.reshape(b, oh // 2, ow // 2, n, 2, 2).transpose(0, 1, 4, 2, 5, 3).reshape(-1)
+    _, patches = _oracle_conv(oracle, x, weight, None, dims, b, c, n, k, 1, p, oh, ow)
+    m = b * oh * ow
+    ref_w = oracle.matmul_right_backward(patches, d_pre, 1, m, c * k * k, n)
+    ref_b = oracle.bias_gradient(d_pre, m, n)
+    gw, gb = dev.empty(c * k * k * n), dev.empty(n)
+    dev.call("axis_conv2d_relu_pool_backward_weight", dx.vp, strides, dg.vp, pooled.vp, arg.vp, gw.vp,
+             gb.vp if with_bias else None, I64(b), I32(h), I32(w), I32(c), I32(n), *geo, win)
+    got_w = dev.read(gw, c * k * k * n)
+    assert rel_err(got_w, ref_w) < 1e-5
+    if with_bias:
+        got_b = dev.read(gb, n)
+        mag = np.abs(d_pre.reshape(-1, n)).sum(axis=0).astype(np.float64)
+        assert np.all(np.abs(got_b.astype(np.float64) - ref_b) <= 2e-6 * mag + 1e-30)
+    # the same as the separate entries (pre-activation gradient, then weight gradient)
+    pre, sep_b, sep_w = dev.empty(m * n), dev.empty(n), dev.empty(c * k * k * n)
+    dev.call("axis_relu_pool_backward", dg.vp, pooled.vp, arg.vp, pre.vp, sep_b.vp, I64(b), I32(oh), I32(ow),
+             I32(n), win)
+    assert np.array_equal(dev.read(pre, m * n).view(np.uint32), d_pre.view(np.uint32))
+    dev.call("axis_conv2d_backward_weight", dx.vp, strides, pre.vp, sep_w.vp, I64(b), I32(h), I32(w), I32(c),
+             I32(n), *geo)
+    assert rel_err(got_w, dev.read(sep_w, c * k * k * n)) < 1e-5
+    # deterministic run to run
+    gw2 = dev.empty(c * k * k * n)
+    dev.call("axis_conv2d_relu_pool_backward_weight", dx.vp, strides, dg.vp, pooled.vp, arg.vp, gw2.vp, None,
+             I64(b), I32(h), I32(w), I32(c), I32(n), *geo, win)
+    assert np.array_equal(dev.read(gw2, c * k * k * n).view(np.uint32), got_w.view(np.uint32))
 
 
 @pytest.mark.parametrize("b,h,w,c,pool", [(5, 16, 18, 64, (2, 2)), (3, 10, 12, 6, (2, 3)), (2, 8, 8, 20, (4, 4)),
