@@ -65,19 +65,40 @@ __device__ __forceinline__ Band decode_band(const SmallConvArgs &a, uint32_t ban
     return b;
 }
 
-// Stages planes 0..c_in-1 of the band's input rows: strip[c][r][col] = x[img, 2*wr0 - py + r,
-// 2*wc0 - px + col, c], zero outside the image.
-__device__ __forceinline__ void fill_strip(const SmallConvArgs &a, const Band &b, float *strip, int tid) {
+// Staging of planes 0..c_in-1 of a band's input rows: strip[c][r][col] = x[img, 2*wr0 - py + r,
+// 2*wc0 - px + col, c], zero outside the image.  A band holds at most 512 cells (rows x columns)
+// of at most 4 channels, so each thread carries two cells of the next band in registers while the
+// current band computes.
+struct StripRegs {
+    float v[2][4];
+};
+
+__device__ __forceinline__ void load_strip(const SmallConvArgs &a, const Band &b, int tid, StripRegs &r) {
     const int32_t iy0 = 2 * b.wr0 - a.py, ix0 = 2 * b.wc0 - a.px;
     const int32_t cells = a.strip_h * a.strip_w;
     const float *img = a.x + (int64_t)b.img * a.ld_b;
-    for (int32_t t = tid; t < cells; t += 256) {
-        const int32_t r = (int32_t)a.strip_w_div.div((uint32_t)t);
-        const int32_t col = t - r * a.strip_w;
-        const int32_t iy = iy0 + r, ix = ix0 + col;
-        const bool ok = (uint32_t)iy < (uint32_t)a.height && (uint32_t)ix < (uint32_t)a.width;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int32_t t = tid + 256 * i;
+        const int32_t row = (int32_t)a.strip_w_div.div((uint32_t)t);
+        const int32_t iy = iy0 + row, ix = ix0 + t - row * a.strip_w;
+        const bool ok = t < cells && (uint32_t)iy < (uint32_t)a.height && (uint32_t)ix < (uint32_t)a.width;
         const float *src = img + (ok ? (int64_t)iy * a.ld_h + (int64_t)ix * a.ld_w : 0);
-        for (int32_t c = 0; c < a.c_in; ++c) strip[c * a.plane + t] = ok ? src[(int64_t)c * a.ld_c] : 0.0f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) r.v[i][c] = (ok && c < a.c_in) ? src[(int64_t)c * a.ld_c] : 0.0f;
+    }
+}
+
+__device__ __forceinline__ void store_strip(const SmallConvArgs &a, float *strip, int tid, const StripRegs &r) {
+    const int32_t cells = a.strip_h * a.strip_w;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int32_t t = tid + 256 * i;
+        if (t < cells) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                if (c < a.c_in) strip[c * a.plane + t] = r.v[i][c];
+        }
     }
 }
 
@@ -90,6 +111,31 @@ __device__ __forceinline__ int32_t term_offset(const SmallConvArgs &a, int32_t k
     const int32_t t = k - c * taps;
     const int32_t ky = t / a.kw;
     return c * a.plane + ky * a.strip_w + (t - ky * a.kw);
+}
+
+// Max pool of one window of ReLU(y_e) (e = position, ky major) with the reference's rule: the
+// first strictly greater finite value, NaN and 255 when none is finite.  ReLU maps NaN and every
+// non-positive value to +0, so the candidates are +0, positive finite values and +inf; without
+// +inf the winner is the first position equal to the maximum.
+__device__ __forceinline__ void pool_window(const float y[4], float &best, int &winner) {
+    float r[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r[e] = y[e] > 0.0f ? y[e] : 0.0f;
+    best = __builtin_fmaxf(__builtin_fmaxf(__builtin_fmaxf(r[0], r[1]), r[2]), r[3]);
+    winner = r[2] == best ? 2 : 3;
+    winner = r[1] == best ? 1 : winner;
+    winner = r[0] == best ? 0 : winner;
+    if (best > FLT_MAX) {  // an infinite candidate: the exact scan
+        best = -INFINITY;
+        winner = 255;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (r[e] <= FLT_MAX && r[e] > best) {
+                best = r[e];
+                winner = e;
+            }
+        if (winner == 255) best = __builtin_nanf("");
+    }
 }
 
 // Forward: KP k-pairs of v_mfma_f32_32x32x2_f32 per pixel tile (2*KP >= k), 32 pixels (8
@@ -131,10 +177,15 @@ __global__ void __launch_bounds__(256, 4) small_conv_forward_kernel(SmallConvArg
 
     const int32_t band_windows = a.band_r * a.band_s;
     const int32_t tiles = (band_windows + 7) / 8;
+    // A band row holds whole tiles: every window of a tile is in one window row.
+    const bool row_tiles = a.band_s % 8 == 0;
+    StripRegs pre;
+    if (blockIdx.x < (uint32_t)a.bands) load_strip(a, decode_band(a, blockIdx.x), tid, pre);
     for (uint32_t band = blockIdx.x; band < (uint32_t)a.bands; band += gridDim.x) {
         const Band bd = decode_band(a, band);
         __syncthreads();  // the previous band's reads are done
-        fill_strip(a, bd, strip, tid);
+        store_strip(a, strip, tid, pre);
+        if (band + gridDim.x < (uint32_t)a.bands) load_strip(a, decode_band(a, band + gridDim.x), tid, pre);
         __syncthreads();
         for (int32_t tile = wave; tile < tiles; tile += 4) {
             // Row i = l32: window tile*8 + i/4, position i%4 = (ky, kx) of the window.
@@ -155,46 +206,45 @@ __global__ void __launch_bounds__(256, 4) small_conv_forward_kernel(SmallConvArg
                 for (int b = 0; b < 2; ++b)
                     acc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, wreg[j][b], acc[b], 0, 0, 0);
             }
+            if (!col_ok[0]) continue;
             // Accumulator register v: row i = 8*(v/4) + 4*half + v%4, i.e. window
             // tile*8 + 2*(v/4) + half, position v%4.
+            const int32_t w_first = tile * 8 + half;
+            const int32_t r_first = (int32_t)a.s_div.div((uint32_t)w_first);
+            const int32_t c_first = w_first - r_first * a.band_s;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const int32_t wt = tile * 8 + 2 * q + half;
-                if (wt >= band_windows || !col_ok[0]) continue;
-                const int32_t wr = (int32_t)a.s_div.div((uint32_t)wt);
-                const int32_t wc = wt - wr * a.band_s;
+                const int32_t wt = w_first + 2 * q;
+                if (wt >= band_windows) continue;
+                int32_t wr, wc;
+                if (row_tiles) {
+                    wr = r_first;
+                    wc = c_first + 2 * q;
+                } else {
+                    wr = (int32_t)a.s_div.div((uint32_t)wt);
+                    wc = wt - wr * a.band_s;
+                }
                 if constexpr (POOL) {
                     if (bd.wr0 + wr >= a.win_rows || bd.wc0 + wc >= a.win_cols) continue;
                     float best[2];
                     int winner[2];
 #pragma unroll
                     for (int b = 0; b < 2; ++b) {
-                        best[b] = -INFINITY;
-                        winner[b] = 255;
+                        float y[4];
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            float z = acc[b][4 * q + e];
-                            z = with_bias ? z + bias_v[b] : z;
-                            z = z > 0.0f ? z : 0.0f;
-                            if (z <= FLT_MAX && z > best[b]) {
-                                best[b] = z;
-                                winner[b] = e;
-                            }
-                        }
+                        for (int e = 0; e < 4; ++e) y[e] = acc[b][4 * q + e] + bias_v[b];
+                        pool_window(y, best[b], winner[b]);
                     }
                     const int64_t pix = ((int64_t)bd.img * a.win_rows + bd.wr0 + wr) * a.win_cols + bd.wc0 + wc;
                     const int64_t o = pix * a.n + col0 + 2 * l32;
                     if (paired) {
-                        float2 value;
-                        value.x = winner[0] == 255 ? __builtin_nanf("") : best[0];
-                        value.y = winner[1] == 255 ? __builtin_nanf("") : best[1];
-                        *reinterpret_cast<float2 *>(a.pooled + o) = value;
+                        *reinterpret_cast<float2 *>(a.pooled + o) = make_float2(best[0], best[1]);
                         *reinterpret_cast<uint16_t *>(a.argmax + o) = (uint16_t)(winner[0] | (winner[1] << 8));
                     } else {
 #pragma unroll
                         for (int b = 0; b < 2; ++b) {
                             if (!col_ok[b]) continue;
-                            a.pooled[o + b] = winner[b] == 255 ? __builtin_nanf("") : best[b];
+                            a.pooled[o + b] = best[b];
                             a.argmax[o + b] = (uint8_t)winner[b];
                         }
                     }
@@ -225,7 +275,65 @@ __global__ void __launch_bounds__(256, 4) small_conv_forward_kernel(SmallConvArg
 // writes), then C^T[n][t] += sum over the window's 4 pixels of dy[p][n] * X[p][t] on
 // v_mfma_f32_16x16x4_f32 (A = dy^T: lane -> (n = l%16, p = l/16); B = X: lane -> (p = l/16,
 // t = l%16)).  Term t = k is the ones plane: the bias gradient.  Each block writes its partial
-// C^T as [32 terms][n]; partials are summed in block order afterwards.
+// C^T as [32 terms][n]; partials are summed in block order afterwards.  Columns of position p
+// are stored XOR 16p, so the four position groups of a wave read different LDS banks.
+struct GradRegs {
+    floatx4 g[2], p[2];
+    uint32_t w[2];
+};
+
+__device__ __forceinline__ void load_grad(const SmallConvArgs &a, const Band &bd, int tid, int32_t col0,
+                                          const float *__restrict__ g, const float *__restrict__ pooled,
+                                          const uint8_t *__restrict__ argmax, GradRegs &r) {
+    const int32_t band_windows = a.band_r * a.band_s;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int32_t t = tid + 256 * i;
+        const int32_t wi = t >> 4, c4 = (t & 15) * 4;
+        const int32_t wr = (int32_t)a.s_div.div((uint32_t)wi);
+        const int32_t wc = wi - wr * a.band_s;
+        const bool win_ok = wi < band_windows && bd.wr0 + wr < a.win_rows && bd.wc0 + wc < a.win_cols;
+        const int64_t pix = ((int64_t)bd.img * a.win_rows + bd.wr0 + wr) * a.win_cols + bd.wc0 + wc;
+        const int64_t base = pix * a.n + col0 + c4;
+        r.g[i] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        r.p[i] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        r.w[i] = 0xffffffffu;
+        if (win_ok && a.vec && col0 + c4 < a.n) {
+            r.g[i] = *reinterpret_cast<const floatx4 *>(g + base);
+            r.p[i] = *reinterpret_cast<const floatx4 *>(pooled + base);
+            r.w[i] = *reinterpret_cast<const uint32_t *>(argmax + base);
+        } else if (win_ok && !a.vec) {
+            uint32_t packed = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const bool ok = col0 + c4 + e < a.n;
+                r.g[i][e] = ok ? g[base + e] : 0.0f;
+                r.p[i][e] = ok ? pooled[base + e] : 0.0f;
+                packed |= (uint32_t)(ok ? argmax[base + e] : 255) << (8 * e);
+            }
+            r.w[i] = packed;
+        }
+    }
+}
+
+__device__ __forceinline__ void store_grad(const SmallConvArgs &a, float *dy, int tid, const GradRegs &r) {
+    const int32_t band_windows = a.band_r * a.band_s;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int32_t t = tid + 256 * i;
+        const int32_t wi = t >> 4, c4 = (t & 15) * 4;
+        if (wi >= band_windows) continue;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            floatx4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                o[e] = (((r.w[i] >> (8 * e)) & 0xffu) == (uint32_t)p && r.p[i][e] > 0.0f) ? 0.0f + r.g[i][e] : 0.0f;
+            *reinterpret_cast<floatx4 *>(dy + (wi * 4 + p) * 64 + (c4 ^ (16 * p))) = o;
+        }
+    }
+}
+
 __global__ void __launch_bounds__(256, 4) small_conv_pool_wgrad_kernel(SmallConvArgs a, const float *__restrict__ g,
                                                                          const float *__restrict__ pooled,
                                                                          const uint8_t *__restrict__ argmax,
@@ -248,47 +356,21 @@ __global__ void __launch_bounds__(256, 4) small_conv_pool_wgrad_kernel(SmallConv
             for (int v = 0; v < 4; ++v) acc[nb][kb][v] = 0.0f;
 
     const int32_t band_windows = a.band_r * a.band_s;
-    const bool vec = a.vec;
+    StripRegs pre;
+    GradRegs gpre;
+    if (blockIdx.x < (uint32_t)a.bands) {
+        const Band first = decode_band(a, blockIdx.x);
+        load_strip(a, first, tid, pre);
+        load_grad(a, first, tid, col0, g, pooled, argmax, gpre);
+    }
     for (uint32_t band = blockIdx.x; band < (uint32_t)a.bands; band += gridDim.x) {
-        const Band bd = decode_band(a, band);
         __syncthreads();
-        fill_strip(a, bd, strip, tid);
-        // 16 column vectors of 4 per window
-        for (int32_t t = tid; t < band_windows * 16; t += 256) {
-            const int32_t wi = t >> 4, c4 = (t & 15) * 4;
-            const int32_t wr = (int32_t)a.s_div.div((uint32_t)wi);
-            const int32_t wc = wi - wr * a.band_s;
-            const bool win_ok = bd.wr0 + wr < a.win_rows && bd.wc0 + wc < a.win_cols;
-            const int64_t pix = ((int64_t)bd.img * a.win_rows + bd.wr0 + wr) * a.win_cols + bd.wc0 + wc;
-            const int64_t base = pix * a.n + col0 + c4;
-            float gv[4] = {0.0f, 0.0f, 0.0f, 0.0f}, pv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-            int av[4] = {255, 255, 255, 255};
-            if (win_ok && vec && col0 + c4 < a.n) {
-                const floatx4 g4 = *reinterpret_cast<const floatx4 *>(g + base);
-                const floatx4 p4 = *reinterpret_cast<const floatx4 *>(pooled + base);
-                const uint32_t a4 = *reinterpret_cast<const uint32_t *>(argmax + base);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    gv[e] = g4[e];
-                    pv[e] = p4[e];
-                    av[e] = (int)((a4 >> (8 * e)) & 0xffu);
-                }
-            } else if (win_ok) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (col0 + c4 + e < a.n) {
-                        gv[e] = g[base + e];
-                        pv[e] = pooled[base + e];
-                        av[e] = argmax[base + e];
-                    }
-            }
-#pragma unroll
-            for (int p = 0; p < 4; ++p) {
-                floatx4 o;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) o[e] = (av[e] == p && pv[e] > 0.0f) ? 0.0f + gv[e] : 0.0f;
-                *reinterpret_cast<floatx4 *>(dy + (wi * 4 + p) * 64 + c4) = o;
-            }
+        store_strip(a, strip, tid, pre);
+        store_grad(a, dy, tid, gpre);
+        if (band + gridDim.x < (uint32_t)a.bands) {
+            const Band next = decode_band(a, band + gridDim.x);
+            load_strip(a, next, tid, pre);
+            load_grad(a, next, tid, col0, g, pooled, argmax, gpre);
         }
         __syncthreads();
         for (int32_t wi = wave; wi < band_windows; wi += 4) {
@@ -299,7 +381,7 @@ __global__ void __launch_bounds__(256, 4) small_conv_pool_wgrad_kernel(SmallConv
             const float *dyw = dy + (wi * 4 + pos) * 64 + nl;
 #pragma unroll
             for (int nb = 0; nb < 4; ++nb) {
-                const float d = dyw[16 * nb];
+                const float d = dyw[16 * (nb ^ pos)];
                 acc[nb][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(d, x0, acc[nb][0], 0, 0, 0);
                 acc[nb][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(d, x1, acc[nb][1], 0, 0, 0);
             }
@@ -348,12 +430,16 @@ __global__ void __launch_bounds__(256) small_conv_combine_kernel(const float *__
     }
 }
 
-// Windows per band: S columns (at most 32) by R rows, R * S <= cap.
+// Windows per band: S columns (at most 32) by R rows, R * S <= cap, with at most 512 staged
+// cells (rows x columns), the capacity of the threads' prefetch registers.
 void band_shape(SmallConvArgs &a, int64_t batch, int32_t cap) {
+    auto cells = [&](int32_t r, int32_t s) { return (2 * r + a.kh - 1) * (2 * s + a.kw - 1); };
     a.band_s = a.win_cols < 32 ? a.win_cols : 32;
+    while (a.band_s > 1 && cells(1, a.band_s) > 512) a.band_s = (a.band_s + 1) / 2;
     a.band_r = cap / a.band_s;
     if (a.band_r < 1) a.band_r = 1;
     if (a.band_r > a.win_rows) a.band_r = a.win_rows;
+    while (a.band_r > 1 && cells(a.band_r, a.band_s) > 512) --a.band_r;
     a.bands_x = (a.win_cols + a.band_s - 1) / a.band_s;
     a.bands_y = (a.win_rows + a.band_r - 1) / a.band_r;
     a.bands = (int32_t)(batch * a.bands_x * a.bands_y);
@@ -442,7 +528,7 @@ namespace axis {
 
 bool small_conv_applies(const SmallConvShape &s) {
     if (s.sy != 1 || s.sx != 1 || s.out_h < 1 || s.out_w < 1) return false;
-    if ((int64_t)s.channels * s.kh * s.kw > 31) return false;
+    if ((int64_t)s.channels * s.kh * s.kw > 31 || s.channels > 4) return false;
     if (s.py > s.kh - 1 || s.px > s.kw - 1) return false;
     if (s.batch * ((s.out_h + 1) / 2) * ((s.out_w + 1) / 2) >= INT32_MAX) return false;
     // four blocks per CU: the staged band (and the backward's gradient expansion) within 40 KiB
@@ -450,7 +536,8 @@ bool small_conv_applies(const SmallConvShape &s) {
     make_args(s, nullptr, nullptr, nullptr, nullptr, 64, fwd);
     make_args(s, nullptr, nullptr, nullptr, nullptr, 32, bwd);
     const size_t limit = 40 * 1024;
-    return strip_bytes(fwd) <= limit && strip_bytes(bwd) + gradient_bytes(bwd) <= limit;
+    return fwd.plane <= 512 && bwd.plane <= 512 && strip_bytes(fwd) <= limit &&
+           strip_bytes(bwd) + gradient_bytes(bwd) <= limit;
 }
 
 int small_conv_forward(axis_device device, const SmallConvShape &s, const float *input, const int64_t ld[4],

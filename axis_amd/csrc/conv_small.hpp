@@ -13,7 +13,8 @@ struct SmallConvShape {
     int32_t height, width, channels, out_channels, kh, kw, sy, sx, py, px, out_h, out_w;
 };
 
-// stride 1, channels * kh * kw <= 31, padding < kernel, and the staged band fits in LDS.
+// stride 1, channels <= 4, channels * kh * kw <= 31, padding < kernel, and the staged band fits
+// the prefetch registers and LDS.
 bool small_conv_applies(const SmallConvShape &s);
 
 // Convolution + bias into out [batch, out_h, out_w, n] (pooled == null), or bias + ReLU + 2x2
