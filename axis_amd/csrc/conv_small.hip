@@ -23,6 +23,7 @@
 #include "common.hpp"
 #include "conv_small.hpp"
 #include "fastdiv.hpp"
+#include "pool_rule.hpp"
 
 namespace {
 
@@ -111,31 +112,6 @@ __device__ __forceinline__ int32_t term_offset(const SmallConvArgs &a, int32_t k
     const int32_t t = k - c * taps;
     const int32_t ky = t / a.kw;
     return c * a.plane + ky * a.strip_w + (t - ky * a.kw);
-}
-
-// Max pool of one window of ReLU(y_e) (e = position, ky major) with the reference's rule: the
-// first strictly greater finite value, NaN and 255 when none is finite.  ReLU maps NaN and every
-// non-positive value to +0, so the candidates are +0, positive finite values and +inf; without
-// +inf the winner is the first position equal to the maximum.
-__device__ __forceinline__ void pool_window(const float y[4], float &best, int &winner) {
-    float r[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) r[e] = y[e] > 0.0f ? y[e] : 0.0f;
-    best = __builtin_fmaxf(__builtin_fmaxf(__builtin_fmaxf(r[0], r[1]), r[2]), r[3]);
-    winner = r[2] == best ? 2 : 3;
-    winner = r[1] == best ? 1 : winner;
-    winner = r[0] == best ? 0 : winner;
-    if (best > FLT_MAX) {  // an infinite candidate: the exact scan
-        best = -INFINITY;
-        winner = 255;
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-            if (r[e] <= FLT_MAX && r[e] > best) {
-                best = r[e];
-                winner = e;
-            }
-        if (winner == 255) best = __builtin_nanf("");
-    }
 }
 
 // Forward: KP k-pairs of v_mfma_f32_32x32x2_f32 per pixel tile (2*KP >= k), 32 pixels (8
@@ -233,7 +209,7 @@ __global__ void __launch_bounds__(256, 4) small_conv_forward_kernel(SmallConvArg
                         float y[4];
 #pragma unroll
                         for (int e = 0; e < 4; ++e) y[e] = acc[b][4 * q + e] + bias_v[b];
-                        pool_window(y, best[b], winner[b]);
+                        relu_pool_window4(y, best[b], winner[b]);
                     }
                     const int64_t pix = ((int64_t)bd.img * a.win_rows + bd.wr0 + wr) * a.win_cols + bd.wc0 + wc;
                     const int64_t o = pix * a.n + col0 + 2 * l32;

@@ -33,6 +33,7 @@
 #include "common.hpp"
 #include "conv_small.hpp"
 #include "fastdiv.hpp"
+#include "pool_rule.hpp"
 
 namespace {
 
@@ -46,10 +47,23 @@ struct ConvGeom {
     int32_t ld_c, ld_h, ld_w;
     int32_t height, width, channels;  // gathered tensor
     int32_t out_h, out_w;             // output pixel grid the reduction/rows enumerate
-    int32_t kw, sy, sx, py, px;
+    int32_t kh, kw, sy, sx, py, px;
     FastDiv c_div, kw_div, ow_div, oh_div;
     bool tap_steps;                   // channels % 32 == 0: a 32-deep K step stays in one tap
+    // Rows mode, 2x2 pooling epilogue: tile row t holds position t % 4 (ky major) of the tile's
+    // window t / 4, windows numbered row-major over the tile's window rows (pw per row).  A tile
+    // starts on an even output row and holds whole window rows.
+    bool window_major;
+    FastDiv pw_div;
 };
+
+// Output pixel of tile row t for a tile starting at pixel t0.
+__device__ __forceinline__ int64_t tile_pixel(const ConvGeom &g, int64_t t0, int t) {
+    if (!g.window_major) return t0 + t;
+    const uint32_t w = (uint32_t)t >> 2, pos = (uint32_t)t & 3u;
+    const uint32_t wr = g.pw_div.div(w), wc = w - wr * g.pw_div.d;
+    return t0 + (int64_t)(2 * wr + (pos >> 1)) * g.out_w + 2 * wc + (pos & 1u);
+}
 
 struct GemmParams {
     const float *x;
@@ -110,13 +124,20 @@ __device__ __forceinline__ void buffer_into(float *reg, __amdgpu_buffer_rsrc_t r
     }
 }
 
-// LDS staging shared by every loader: [r][t] layout with a pitch that keeps both the fill and
-// the MFMA operand reads free of bank conflicts.
+// LDS staging shared by every loader: [r][t] layout, row pitch BT + 4 (16-byte aligned rows),
+// and column t of row r stored at t ^ swizzle(r) with swizzle(r) = 8 * ((r / 4) % 8).  The XOR
+// moves whole aligned groups of 8 columns, so the MFMA operand reads (4 or 2 consecutive columns
+// of one row per lane) stay single 16- or 8-byte reads, and one k-quad (4 rows) shares one
+// swizzle.  It spreads the transposing stores of r-contiguous operands (a lane writes rows
+// 4j..4j+3 of one column) over distinct banks.
+__device__ __forceinline__ constexpr int stage_swizzle(int r) { return 8 * ((r >> 2) & 7); }
+
 template <int BT, int BK, int NT, bool RCONTIG, int VEC>
 struct Staging {
+    static_assert(BT % 64 == 0, "the swizzle permutes columns inside aligned groups of 64");
     static constexpr int kElems = BT * BK / NT;  // floats per thread
     static constexpr int kVecs = kElems / VEC;
-    static constexpr int LD = RCONTIG ? BT + 2 : BT + 4;
+    static constexpr int LD = BT + 4;
     static constexpr int kPer = RCONTIG ? BK / VEC : BT / VEC;  // vectors per contiguous line
     float reg[kElems];
 
@@ -128,20 +149,29 @@ struct Staging {
                 const int rr = (idx % kPer) * VEC;
                 const int tt = idx / kPer;
 #pragma unroll
-                for (int c = 0; c < VEC; ++c) lds[(rr + c) * LD + tt] = reg[e * VEC + c];
+                for (int c = 0; c < VEC; ++c) lds[(rr + c) * LD + (tt ^ stage_swizzle(rr + c))] = reg[e * VEC + c];
             } else {
                 const int tt = (idx % kPer) * VEC;
                 const int rr = idx / kPer;
                 if (VEC == 4) {
                     floatx4 v = {reg[e * 4 + 0], reg[e * 4 + 1], reg[e * 4 + 2], reg[e * 4 + 3]};
-                    *reinterpret_cast<floatx4 *>(lds + rr * LD + tt) = v;
+                    *reinterpret_cast<floatx4 *>(lds + rr * LD + (tt ^ stage_swizzle(rr))) = v;
                 } else {
-                    lds[rr * LD + tt] = reg[e];
+                    lds[rr * LD + (tt ^ stage_swizzle(rr))] = reg[e];
                 }
             }
         }
     }
 };
+
+// A wave-uniform pointer moved to scalar registers, so that buffer resources built from it need no
+// per-lane loop (the compiler cannot always prove such values uniform).
+__device__ __forceinline__ const float *uniform_ptr(const float *p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return reinterpret_cast<const float *>(((uint64_t)hi << 32) | lo);
+}
 
 // Dense operand: element (t, r) at base[t * s_t + r * s_r], read through buffer loads.  A lane's
 // (t, r) within each of its vectors differs from the vector's first lane by the same small
@@ -184,7 +214,7 @@ struct DenseLoader : Staging<BT, BK, NT, RCONTIG, VEC> {
             split(wave * 64 + e * NT, t_w, r_w);
             r_wave[e] = r_w;
             t_ok[e] = t0 + t_w + t_l < t_end;
-            vbase[e] = b + (t0 + t_w) * st + (int64_t)r_w * sr;
+            vbase[e] = uniform_ptr(b + (t0 + t_w) * st + (int64_t)r_w * sr);
         }
     }
     __device__ __forceinline__ void load(const ConvGeom &, int64_t r0, int64_t r_end, int) {
@@ -193,7 +223,8 @@ struct DenseLoader : Staging<BT, BK, NT, RCONTIG, VEC> {
 #pragma unroll
         for (int e = 0; e < S::kVecs; ++e) {
             const bool valid = t_ok[e] && r_wave[e] + r_lane < room;
-            buffer_into<VEC>(this->reg + e * VEC, make_rsrc(vbase[e] + step), valid ? lane_off * 4u : kOutside);
+            buffer_into<VEC>(this->reg + e * VEC, make_rsrc(uniform_ptr(vbase[e] + step)),
+                             valid ? lane_off * 4u : kOutside);
         }
     }
 };
@@ -251,7 +282,7 @@ struct ConvRowsLoader : Staging<BT, BK, NT, true, VEC> {
         rr = (tid % S::kPer) * VEC;  // NT is a multiple of kPer, so rr is the same for every e
 #pragma unroll
         for (int e = 0; e < S::kVecs; ++e) {
-            const int64_t gt = t0 + (tid + e * NT) / S::kPer;
+            const int64_t gt = tile_pixel(geom, t0, (tid + e * NT) / S::kPer);
             // Rows past the end get an origin far outside the image, so every tap is padding;
             // computed branch-free so the per-row arrays stay in registers.
             const bool live = gt < t_end;
@@ -285,21 +316,23 @@ struct ConvRowsLoader : Staging<BT, BK, NT, true, VEC> {
     }
 };
 
-// Rows mode through buffer loads, for gathered tensors whose offsets fit 31-bit byte offsets.
-// When the channel count is a multiple of BK (geom.tap_steps), a K step covers BK channels of one
-// tap, so the step's tap decode is wave-uniform and each vector costs two bounds tests.
+// Rows mode through buffer loads, for gathered tensors whose offsets fit 31-bit byte offsets and
+// kernels of at most 32 taps.  Each row keeps its window origin's offset and a mask of the taps
+// that fall inside the image (bit ky*kw + kx), so a K step tests one bit per vector.  When the
+// channel count is a multiple of BK (geom.tap_steps), a K step covers BK channels of one tap and
+// the step's tap decode is wave-uniform.
 template <int BT, int BK, int NT, int VEC>
 struct ConvRowsBufferLoader : Staging<BT, BK, NT, true, VEC> {
     using S = Staging<BT, BK, NT, true, VEC>;
     uint32_t origin[S::kVecs];   // b*ld_b + iy0*ld_h + ix0*ld_w (mod 2^32; exact when valid)
-    int32_t iy0[S::kVecs], ix0[S::kVecs];
+    uint32_t inside[S::kVecs];   // taps of the row's window inside the image (0 for rows past the end)
     int rr;
 
     __device__ __forceinline__ void init(const ConvGeom &geom, int64_t t0, int64_t t_end, int tid) {
         rr = (tid % S::kPer) * VEC;
 #pragma unroll
         for (int e = 0; e < S::kVecs; ++e) {
-            const int64_t gt = t0 + (tid + e * NT) / S::kPer;
+            const int64_t gt = tile_pixel(geom, t0, (tid + e * NT) / S::kPer);
             const bool live = gt < t_end;
             const uint32_t pix = live ? (uint32_t)gt : 0u;
             const uint32_t q = geom.ow_div.div(pix);
@@ -307,39 +340,41 @@ struct ConvRowsBufferLoader : Staging<BT, BK, NT, true, VEC> {
             const uint32_t b = geom.oh_div.div(q);
             const int32_t oy = (int32_t)(q - b * (uint32_t)geom.out_h);
             const int32_t y0 = oy * geom.sy - geom.py;
-            ix0[e] = ox * geom.sx - geom.px;
-            origin[e] = b * (uint32_t)geom.ld_b + (uint32_t)y0 * (uint32_t)geom.ld_h +
-                        (uint32_t)ix0[e] * (uint32_t)geom.ld_w;
-            iy0[e] = live ? y0 : -(1 << 30);
+            const int32_t x0 = ox * geom.sx - geom.px;
+            origin[e] = b * (uint32_t)geom.ld_b + (uint32_t)y0 * (uint32_t)geom.ld_h + (uint32_t)x0 * (uint32_t)geom.ld_w;
+            uint32_t cols = 0, taps = 0;
+            for (int32_t kx = 0; kx < geom.kw; ++kx)
+                cols |= (uint32_t)((uint32_t)(x0 + kx) < (uint32_t)geom.width) << kx;
+            for (int32_t ky = 0; ky < geom.kh; ++ky)
+                taps |= ((uint32_t)(y0 + ky) < (uint32_t)geom.height ? cols : 0u) << (ky * geom.kw);
+            inside[e] = live ? taps : 0u;
         }
     }
     __device__ __forceinline__ void load(const ConvGeom &geom, int64_t r0, int64_t r_end, int) {
         const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(geom.src);
-        int32_t ky, kx;
-        uint32_t delta;
+        uint32_t pos, delta;
         bool r_ok;
         if (geom.tap_steps) {
             // r_end is a multiple of BK here, so every k of the step is inside the reduction
-            const uint32_t pos = geom.c_div.div((uint32_t)r0);
+            pos = geom.c_div.div((uint32_t)r0);
             const int32_t c0 = (int32_t)((uint32_t)r0 - pos * (uint32_t)geom.channels);
-            ky = (int32_t)geom.kw_div.div(pos);
-            kx = (int32_t)pos - ky * geom.kw;
+            const int32_t ky = (int32_t)geom.kw_div.div(pos);
+            const int32_t kx = (int32_t)pos - ky * geom.kw;
             delta = (uint32_t)(ky * geom.ld_h + kx * geom.ld_w + (c0 + rr) * geom.ld_c);
             r_ok = true;
         } else {
             const int64_t gr = r0 + rr;
             r_ok = gr < r_end;
             const uint32_t g = r_ok ? (uint32_t)gr : 0u;
-            const uint32_t pos = geom.c_div.div(g);
+            pos = geom.c_div.div(g);
             const int32_t c = (int32_t)(g - pos * (uint32_t)geom.channels);
-            ky = (int32_t)geom.kw_div.div(pos);
-            kx = (int32_t)pos - ky * geom.kw;
+            const int32_t ky = (int32_t)geom.kw_div.div(pos);
+            const int32_t kx = (int32_t)pos - ky * geom.kw;
             delta = (uint32_t)(ky * geom.ld_h + kx * geom.ld_w + c * geom.ld_c);
         }
 #pragma unroll
         for (int e = 0; e < S::kVecs; ++e) {
-            const bool valid = r_ok && (uint32_t)(iy0[e] + ky) < (uint32_t)geom.height &&
-                               (uint32_t)(ix0[e] + kx) < (uint32_t)geom.width;
+            const bool valid = r_ok && ((inside[e] >> pos) & 1u) != 0;
             buffer_into<VEC>(this->reg + e * VEC, rsrc, valid ? (origin[e] + delta) * 4u : kOutside);
         }
     }
@@ -490,13 +525,21 @@ __device__ __forceinline__ float finish_value(const float *bias, const float *d,
 // XMODE: 0 dense X, 1 convolution rows mode, 2 convolution cols mode, 3 cols mode over aligned
 // pixel steps, 4 rows mode through buffer loads.
 // EPI: 0 store C (+ bias), 1 bias + ReLU + max pool of whole windows (rows are output pixels).
+// Blocks per CU the register budget is held to (three large, four tall, five small tiles).
+constexpr int gemm_blocks_per_cu(int bm, int bn) { return bm == 128 && bn == 128 ? 3 : bm == 128 ? 4 : 5; }
+
 template <int BM, int BN, int BK, int WM, int WN, bool XR, bool YR, int VX, int VY, int XMODE, int EPI>
-__global__ void __launch_bounds__(WM *WN * 64)
+__global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
     gemm_kernel(GemmParams p) {
     constexpr int NT = WM * WN * 64;
     static_assert(XMODE != 4 || BK == 32, "the buffer rows loader's tap steps are 32 deep");
     constexpr int TM = BM / WM, TN = BN / WN;
-    constexpr int FM = TM / 32, FN = TN / 32;
+    // 16x16 MFMA blocks per wave side.  Block a of a wave holds the wave's tile rows FM*i + a
+    // (i = 0..15) and block b its columns FN*j + b, so for one k a lane's FM (FN) operands are
+    // consecutive staged columns: one 16- or 8-byte LDS read.
+    constexpr int FM = TM / 16, FN = TN / 16;
+    static_assert((FM == 2 || FM == 4) && (FN == 2 || FN == 4), "wave tiles 32 or 64 wide");
+    static_assert(EPI == 0 || FM == 4, "the pooling epilogue takes 64-row wave tiles");
     using LX = std::conditional_t<
         XMODE == 0, DenseLoader<BM, BK, NT, XR, VX>,
         std::conditional_t<
@@ -504,7 +547,7 @@ __global__ void __launch_bounds__(WM *WN * 64)
             std::conditional_t<XMODE == 2, ConvColsLoader<BM, BK, NT, VX>,
                                std::conditional_t<XMODE == 3, ConvColsStepLoader<BM, BK, NT, VX>,
                                                   ConvRowsBufferLoader<BM, BK, NT, VX>>>>>;
-    using LY = std::conditional_t<XMODE == 0, DensePointerLoader<BN, BK, NT, YR, VY>, DenseLoader<BN, BK, NT, YR, VY>>;
+    using LY = DenseLoader<BN, BK, NT, YR, VY>;
     constexpr int kStage = BK * LX::LD + BK * LY::LD;
     constexpr int kPoolPitch = TN + 1;
     constexpr int kEpilogue = EPI == 1 ? BM * kPoolPitch : 0;
@@ -532,13 +575,13 @@ __global__ void __launch_bounds__(WM *WN * 64)
     const int64_t r_begin = (int64_t)split * p.k_chunk;
     const int64_t r_end = r_begin + p.k_chunk < p.k ? r_begin + p.k_chunk : p.k;
 
-    floatx16 acc[FM][FN];
+    floatx4 acc[FM][FN];
 #pragma unroll
     for (int a = 0; a < FM; ++a)
 #pragma unroll
         for (int b = 0; b < FN; ++b)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.f;
+            for (int v = 0; v < 4; ++v) acc[a][b][v] = 0.f;
 
     LX lx;
     LY ly;
@@ -555,24 +598,28 @@ __global__ void __launch_bounds__(WM *WN * 64)
     }
     __syncthreads();
 
-    const int half = lane >> 5;  // which k of the pair this lane feeds
-    const int l32 = lane & 31;
-    // MFMA operands of one k pair.  With two 32-blocks per wave side, block a takes rows 2i + a,
-    // so both operands are one 8-byte LDS read at an immediate offset from a single base.
+    // v_mfma_f32_16x16x4_f32: lane l feeds k = l / 16 of the quad, A row i = l % 16, B column
+    // j = l % 16; its result registers v hold rows 4 * (l / 16) + v of column l % 16.
+    const int quad = lane >> 4;
+    const int l16 = lane & 15;
+    // MFMA operands of the k-quad starting at kk (its four rows share one swizzle).
     auto read_operands = [&](int kk, float *av, float *bv) {
-        if constexpr (FM == 2) {
-            const float2 v = *reinterpret_cast<const float2 *>(xs + (kk + half) * LX::LD + wm * TM + 2 * l32);
+        const int sw = stage_swizzle(kk);
+        const float *xa = xs + (kk + quad) * LX::LD + ((wm * TM + FM * l16) ^ sw);
+        const float *yb = ys + (kk + quad) * LY::LD + ((wn * TN + FN * l16) ^ sw);
+        if constexpr (FM == 4) {
+            const floatx4 v = *reinterpret_cast<const floatx4 *>(xa);
+            av[0] = v[0], av[1] = v[1], av[2] = v[2], av[3] = v[3];
+        } else {
+            const float2 v = *reinterpret_cast<const float2 *>(xa);
             av[0] = v.x, av[1] = v.y;
-        } else {
-#pragma unroll
-            for (int a = 0; a < FM; ++a) av[a] = xs[(kk + half) * LX::LD + wm * TM + a * 32 + l32];
         }
-        if constexpr (FN == 2) {
-            const float2 v = *reinterpret_cast<const float2 *>(ys + (kk + half) * LY::LD + wn * TN + 2 * l32);
-            bv[0] = v.x, bv[1] = v.y;
+        if constexpr (FN == 4) {
+            const floatx4 v = *reinterpret_cast<const floatx4 *>(yb);
+            bv[0] = v[0], bv[1] = v[1], bv[2] = v[2], bv[3] = v[3];
         } else {
-#pragma unroll
-            for (int b = 0; b < FN; ++b) bv[b] = ys[(kk + half) * LY::LD + wn * TN + b * 32 + l32];
+            const float2 v = *reinterpret_cast<const float2 *>(yb);
+            bv[0] = v.x, bv[1] = v.y;
         }
     };
     for (int64_t r0 = r_begin; r0 < r_end; r0 += BK) {
@@ -581,21 +628,21 @@ __global__ void __launch_bounds__(WM *WN * 64)
             lx.load(p.conv, r0 + BK, r_end, tid);
             ly.load(p.conv, r0 + BK, r_end, tid);
         }
-        // The operands of the next k pair are read before this pair's MFMAs issue, and the
+        // The operands of the next k-quad are read before this quad's MFMAs issue, and the
         // scheduling barriers keep that order: each LDS read has a whole MFMA group to land
         // (left to itself the compiler sinks every read to just before its use).
         float av[2][FM], bv[2][FN];
         read_operands(0, av[0], bv[0]);
 #pragma unroll
-        for (int kk = 0; kk < BK; kk += 2) {
-            const int cur = (kk / 2) & 1;
-            if (kk + 2 < BK) read_operands(kk + 2, av[cur ^ 1], bv[cur ^ 1]);
+        for (int kk = 0; kk < BK; kk += 4) {
+            const int cur = (kk / 4) & 1;
+            if (kk + 4 < BK) read_operands(kk + 4, av[cur ^ 1], bv[cur ^ 1]);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int a = 0; a < FM; ++a)
 #pragma unroll
                 for (int b = 0; b < FN; ++b)
-                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[cur][a], bv[cur][b], acc[a][b], 0, 0, 0);
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[cur][a], bv[cur][b], acc[a][b], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
         }
         __syncthreads();
@@ -606,12 +653,11 @@ __global__ void __launch_bounds__(WM *WN * 64)
         }
     }
 
-    // Accumulator layout of the 32x32 block: lane -> column l32; register v -> row
-    // 8*(v/4) + 4*(lane/32) + (v%4), both mapped into the wave's tile by the block placement
-    // above (rows 2i + a when FM == 2, else a*32 + i; columns likewise).  The bias (one value per
-    // column) is added only when the reduction is not split; split sums add it once at the end.
-    auto row_in = [](int a, int i) { return FM == 2 ? 2 * i + a : a * 32 + i; };
-    auto col_in = [](int b, int l) { return FN == 2 ? 2 * l + b : b * 32 + l; };
+    // acc[a][b][v] is tile row wm*TM + FM*(4*quad + v) + a, column wn*TN + FN*l16 + b: a lane's
+    // FN columns are adjacent.  The bias (one value per column) is added only when the reduction
+    // is not split; split sums add it once at the end.
+    auto row_of = [&](int a, int v) { return wm * TM + FM * (4 * quad + v) + a; };
+    const int col_l = wn * TN + FN * l16;  // tile column of the lane's first column
     if constexpr (EPI == 0) {
         float *c = p.c + batch * p.c_batch + (int64_t)split * p.c_split;
         // bias / axpby apply to whole sums only; split sums finish them at the end
@@ -619,141 +665,125 @@ __global__ void __launch_bounds__(WM *WN * 64)
         const float *bias = whole ? p.bias : nullptr;
         const float *d = whole ? p.d : nullptr;
         const int64_t out_base = batch * p.m * p.n;
-        if (FN == 2 && (p.n & 1) == 0) {
-            // the two column blocks of a lane are adjacent columns: one 8-byte store per row
-            const int64_t col = j0 + wn * TN + 2 * l32;
+        const int64_t col = j0 + col_l;
+        if (p.n % FN == 0 && (reinterpret_cast<uintptr_t>(c) & (4 * FN - 1)) == 0) {
+            // one FN-wide vector store per row (col < n implies all FN columns are)
             if (col < p.n) {
 #pragma unroll
                 for (int a = 0; a < FM; ++a)
 #pragma unroll
-                    for (int v = 0; v < 16; ++v) {
-                        const int64_t row = i0 + wm * TM + row_in(a, (v >> 2) * 8 + half * 4 + (v & 3));
-                        if (row < p.m) {
-                            const int64_t idx = row * p.n + col;
+                    for (int v = 0; v < 4; ++v) {
+                        const int64_t row = i0 + row_of(a, v);
+                        if (row >= p.m) continue;
+                        const int64_t idx = row * p.n + col;
+                        if constexpr (FN == 4) {
+                            floatx4 o;
+#pragma unroll
+                            for (int b = 0; b < 4; ++b)
+                                o[b] = finish_value(bias, d, p.alpha, p.beta, acc[a][b][v], out_base + idx + b, col + b);
+                            *reinterpret_cast<floatx4 *>(c + idx) = o;
+                        } else {
                             float2 o;
                             o.x = finish_value(bias, d, p.alpha, p.beta, acc[a][0][v], out_base + idx, col);
-                            o.y = finish_value(bias, d, p.alpha, p.beta, acc[a][FN - 1][v], out_base + idx + 1,
-                                               col + 1);
+                            o.y = finish_value(bias, d, p.alpha, p.beta, acc[a][1][v], out_base + idx + 1, col + 1);
                             *reinterpret_cast<float2 *>(c + idx) = o;
                         }
                     }
             }
         } else {
 #pragma unroll
-            for (int a = 0; a < FM; ++a)
+            for (int b = 0; b < FN; ++b) {
+                if (col + b >= p.n) continue;
 #pragma unroll
-                for (int b = 0; b < FN; ++b) {
-                    const int64_t col = j0 + wn * TN + col_in(b, l32);
-                    if (col >= p.n) continue;
+                for (int a = 0; a < FM; ++a)
 #pragma unroll
-                    for (int v = 0; v < 16; ++v) {
-                        const int64_t row = i0 + wm * TM + row_in(a, (v >> 2) * 8 + half * 4 + (v & 3));
+                    for (int v = 0; v < 4; ++v) {
+                        const int64_t row = i0 + row_of(a, v);
                         if (row < p.m)
-                            c[row * p.n + col] =
-                                finish_value(bias, d, p.alpha, p.beta, acc[a][b][v], out_base + row * p.n + col, col);
+                            c[row * p.n + col + b] = finish_value(bias, d, p.alpha, p.beta, acc[a][b][v],
+                                                                  out_base + row * p.n + col + b, col + b);
                     }
-                }
+            }
         }
     } else {
         // The block's BM rows are whole rows of pooling windows (the host guarantees
         // BM % (pool_h * pool_ow) == 0 and an exact tiling), so every window is complete here.
-        // One column half (the waves with wn == h) at a time goes through LDS as
-        // relu(acc + bias); then all threads reduce windows: first strictly greater finite value
-        // in window order (ky major, kx minor), winner 255 and NaN when no value qualifies.
         const int kh = p.pool_h, kw = p.pool_w, ow = p.pool_ow;
         const int pw = ow / kw;
         const int windows = BM / (kh * kw);
         const int64_t pooled_row0 = i0 / ow / kh;
-        if constexpr (FM == 2 && TM == 64) {
-            if (kh == 2 && kw == 2 && (ow == 16 || ow == 32)) {
-                // A whole 2x2 window sits in one lane: tile rows 2i and 2i+1 (horizontal
-                // neighbours) are acc[0] / acc[1], and the pixel row below (ow rows further, i.e.
-                // i + ow/2) is register v + ow/4.  The wave's 64 rows are whole window rows, so
-                // each lane pools its windows from registers: no LDS and no barrier.
-                // With two column blocks a lane's columns are adjacent (2 * l32 + b): both windows
-                // go out as one 8-byte value store and one 2-byte winner store when n is even.
-                const bool paired = FN == 2 && (p.n & 1) == 0 && (reinterpret_cast<uintptr_t>(p.pooled) & 7) == 0 &&
-                                    (reinterpret_cast<uintptr_t>(p.argmax) & 1) == 0;
-                float addv[FN];
-                bool okv[FN], biasv[FN];
+        if (p.conv.window_major) {
+            // 2x2 windows, tile rows window-major: acc[a][b][v] is position a of the wave's window
+            // 4 * quad + v, so each lane pools whole windows from its own registers (no LDS, no
+            // barrier) and writes its FN adjacent columns as one vector of values and one of
+            // winner bytes.
+            float addv[FN];
+            bool okv[FN];
+#pragma unroll
+            for (int b = 0; b < FN; ++b) {
+                const int64_t col = j0 + col_l + b;
+                okv[b] = col < p.n;
+                addv[b] = (p.bias != nullptr && okv[b]) ? p.bias[col] : 0.0f;
+            }
+            const bool vec = p.n % FN == 0 && (reinterpret_cast<uintptr_t>(p.pooled) & (4 * FN - 1)) == 0 &&
+                             (reinterpret_cast<uintptr_t>(p.argmax) & (FN - 1)) == 0;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int w = wm * (TM / 4) + 4 * quad + v;  // window inside the tile
+                const int wr = (int)p.pool_cols.div((uint32_t)w), wc = w - wr * pw;
+                if (i0 + (int64_t)wr * 2 * ow >= p.m) continue;
+                float best[FN];
+                int winner[FN];
 #pragma unroll
                 for (int b = 0; b < FN; ++b) {
-                    const int64_t col = j0 + wn * TN + col_in(b, l32);
-                    okv[b] = col < p.n;
-                    biasv[b] = p.bias != nullptr && okv[b];
-                    addv[b] = biasv[b] ? p.bias[col] : 0.0f;
-                }
+                    float y[4];
 #pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    // top-row registers: pixel row (2i) / ow even within the wave
-                    if (ow == 32 ? v >= 8 : ((v >> 2) & 1) != 0) continue;
-                    const int i = (v >> 2) * 8 + half * 4 + (v & 3);
-                    const int y = 2 * i / ow;
-                    const int64_t row = i0 + wm * TM + 2 * i;  // window's top-left pixel
-                    if (row >= p.m) continue;
-                    const int vb = ow == 32 ? v + 8 : v + 4;
-                    const int wr = (wm * TM) / (2 * ow) + y / 2;
-                    const int px = (2 * i - y * ow) / 2;
-                    float best[FN];
-                    int winner[FN];
+                    for (int e = 0; e < 4; ++e) y[e] = acc[e][b][v] + addv[b];
+                    relu_pool_window4(y, best[b], winner[b]);
+                }
+                const int64_t out = ((pooled_row0 + wr) * pw + wc) * p.n + j0 + col_l;
+                if (vec && okv[0]) {
+                    if constexpr (FN == 4) {
+                        *reinterpret_cast<floatx4 *>(p.pooled + out) = floatx4{best[0], best[1], best[2], best[3]};
+                        *reinterpret_cast<uint32_t *>(p.argmax + out) =
+                            (uint32_t)winner[0] | ((uint32_t)winner[1] << 8) | ((uint32_t)winner[2] << 16) |
+                            ((uint32_t)winner[3] << 24);
+                    } else {
+                        *reinterpret_cast<float2 *>(p.pooled + out) = make_float2(best[0], best[1]);
+                        *reinterpret_cast<uint16_t *>(p.argmax + out) = (uint16_t)(winner[0] | (winner[1] << 8));
+                    }
+                } else {
 #pragma unroll
                     for (int b = 0; b < FN; ++b) {
-                        best[b] = -INFINITY;
-                        winner[b] = 255;
-                        auto take = [&](float z, int at) {
-                            z = biasv[b] ? z + addv[b] : z;
-                            z = z > 0.0f ? z : 0.0f;
-                            if (z >= -FLT_MAX && z <= FLT_MAX && z > best[b]) {
-                                best[b] = z;
-                                winner[b] = at;
-                            }
-                        };
-                        take(acc[0][b][v], 0);
-                        take(acc[1][b][v], 1);
-                        take(acc[0][b][vb], 2);
-                        take(acc[1][b][vb], 3);
-                    }
-                    const int64_t col0 = j0 + wn * TN + col_in(0, l32);
-                    const int64_t out = ((pooled_row0 + wr) * pw + px) * p.n + col0;
-                    if (paired && okv[0]) {  // n even and col0 even: col0 + 1 < n as well
-                        float2 value;
-                        value.x = winner[0] == 255 ? __builtin_nanf("") : best[0];
-                        value.y = winner[FN - 1] == 255 ? __builtin_nanf("") : best[FN - 1];
-                        *reinterpret_cast<float2 *>(p.pooled + out) = value;
-                        *reinterpret_cast<uint16_t *>(p.argmax + out) =
-                            (uint16_t)(winner[0] | (winner[FN - 1] << 8));
-                    } else {
-#pragma unroll
-                        for (int b = 0; b < FN; ++b) {
-                            if (!okv[b]) continue;
-                            const int64_t o = out + (col_in(b, l32) - col_in(0, l32));
-                            p.pooled[o] = winner[b] == 255 ? __builtin_nanf("") : best[b];
-                            p.argmax[o] = (uint8_t)winner[b];
-                        }
+                        if (!okv[b]) continue;
+                        p.pooled[out + b] = best[b];
+                        p.argmax[out + b] = (uint8_t)winner[b];
                     }
                 }
-                return;
             }
+            return;
         }
+        // Other windows: one column half (the waves with wn == h) at a time goes through LDS as
+        // relu(acc + bias); then all threads reduce windows: first strictly greater finite value
+        // in window order (ky major, kx minor), winner 255 and NaN when no value qualifies.
 #pragma unroll
         for (int h = 0; h < WN; ++h) {
             __syncthreads();
             if (wn == h) {
 #pragma unroll
-                for (int a = 0; a < FM; ++a)
+                for (int b = 0; b < FN; ++b) {
+                    const int cl = FN * l16 + b;
+                    const int64_t col = j0 + h * TN + cl;
+                    const bool with_bias = p.bias != nullptr && col < p.n;
+                    const float add = with_bias ? p.bias[col] : 0.0f;
 #pragma unroll
-                    for (int b = 0; b < FN; ++b) {
-                        const int cl = col_in(b, l32);
-                        const int64_t col = j0 + h * TN + cl;
-                        const bool with_bias = p.bias != nullptr && col < p.n;
-                        const float add = with_bias ? p.bias[col] : 0.0f;
+                    for (int a = 0; a < FM; ++a)
 #pragma unroll
-                        for (int v = 0; v < 16; ++v) {
-                            const int rl = wm * TM + row_in(a, (v >> 2) * 8 + half * 4 + (v & 3));
+                        for (int v = 0; v < 4; ++v) {
                             const float z = with_bias ? acc[a][b][v] + add : acc[a][b][v];
-                            lds[rl * kPoolPitch + cl] = z > 0.0f ? z : 0.0f;
+                            lds[row_of(a, v) * kPoolPitch + cl] = z > 0.0f ? z : 0.0f;
                         }
-                    }
+                }
             }
             __syncthreads();
             // Thread items: column cl (fixed per thread) of windows w, w + NT/TN, ...
@@ -772,15 +802,8 @@ __global__ void __launch_bounds__(WM *WN * 64)
                         winner = at;
                     }
                 };
-                if (kh == 2 && kw == 2) {
-                    take(win[0], 0);
-                    take(win[kPoolPitch], 1);
-                    take(win[ow * kPoolPitch], 2);
-                    take(win[(ow + 1) * kPoolPitch], 3);
-                } else {
-                    for (int ky = 0; ky < kh; ++ky)
-                        for (int kx = 0; kx < kw; ++kx) take(win[(ky * ow + kx) * kPoolPitch], ky * kw + kx);
-                }
+                for (int ky = 0; ky < kh; ++ky)
+                    for (int kx = 0; kx < kw; ++kx) take(win[(ky * ow + kx) * kPoolPitch], ky * kw + kx);
                 const int64_t out = ((pooled_row0 + wr) * pw + px) * p.n + col;
                 p.pooled[out] = winner == 255 ? __builtin_nanf("") : best;
                 p.argmax[out] = (uint8_t)winner;
@@ -1126,7 +1149,7 @@ int input_strides(const int64_t *given, int64_t batch, int32_t height, int32_t w
 }
 
 ConvGeom geom(const float *src, const int64_t ld[4], int32_t height, int32_t width, int32_t channels,
-              int32_t out_h, int32_t out_w, int32_t kw, int32_t sy, int32_t sx, int32_t py, int32_t px) {
+              int32_t out_h, int32_t out_w, int32_t kh, int32_t kw, int32_t sy, int32_t sx, int32_t py, int32_t px) {
     ConvGeom g{};
     g.src = src;
     g.ld_b = ld[0];
@@ -1138,6 +1161,7 @@ ConvGeom geom(const float *src, const int64_t ld[4], int32_t height, int32_t wid
     g.channels = channels;
     g.out_h = out_h;
     g.out_w = out_w;
+    g.kh = kh;
     g.kw = kw;
     g.sy = sy;
     g.sx = sx;
@@ -1152,11 +1176,12 @@ ConvGeom geom(const float *src, const int64_t ld[4], int32_t height, int32_t wid
 }
 
 // Rows mode reads through 31-bit byte offsets when every element of the gathered tensor is
-// within reach of them (the buffer loader); larger tensors keep 64-bit addresses.
+// within reach of them and the kernel has at most 32 taps (the buffer loader); other
+// convolutions keep 64-bit addresses.
 bool buffer_reach(const ConvGeom &g, int64_t batch) {
     const int64_t last = (batch - 1) * g.ld_b + (int64_t)(g.height - 1) * g.ld_h + (int64_t)(g.width - 1) * g.ld_w +
                          (int64_t)(g.channels - 1) * g.ld_c;
-    return (last + 4) * 4 < (int64_t(1) << 31) - 1;
+    return (last + 4) * 4 < (int64_t(1) << 31) - 1 && g.kh * g.kw <= 32;
 }
 
 int permute_weight(axis_device device, const float *src, float *dst, const ConvShape &s, int mode,
@@ -1318,7 +1343,7 @@ int axis_conv2d_forward(axis_device device, const float *input, const int64_t in
     p.k_work = (int64_t)channels * s.kh * s.kw;
     p.y_sr = out_channels;
     p.y_sj = 1;
-    p.conv = geom(in.src, in.ld, height, width, in.channels, s.out_h, s.out_w, s.kw, s.sy, s.sx, s.py, s.px);
+    p.conv = geom(in.src, in.ld, height, width, in.channels, s.out_h, s.out_w, s.kh, s.kw, s.sy, s.sx, s.py, s.px);
     return buffer_reach(p.conv, batch) ? run_gemm<true, false, 4, 0>(device, p, 1, out)
                                        : run_gemm<true, false, 1, 0>(device, p, 1, out);
 }
@@ -1361,13 +1386,16 @@ int axis_conv2d_relu_pool_forward(axis_device device, const float *input,
     p.k_work = (int64_t)channels * s.kh * s.kw;
     p.y_sr = out_channels;
     p.y_sj = 1;
-    p.conv = geom(in.src, in.ld, height, width, in.channels, s.out_h, s.out_w, s.kw, s.sy, s.sx, s.py, s.px);
+    p.conv = geom(in.src, in.ld, height, width, in.channels, s.out_h, s.out_w, s.kh, s.kw, s.sy, s.sx, s.py, s.px);
     p.pooled = pooled;
     p.argmax = argmax;
     p.pool_h = pool[0];
     p.pool_w = pool[1];
     p.pool_ow = s.out_w;
     p.pool_cols = FastDiv((uint32_t)(s.out_w / pool[1]));
+    // 2x2 windows: tile rows window-major, pooled in registers
+    p.conv.window_major = pool[0] == 2 && pool[1] == 2;
+    p.conv.pw_div = p.pool_cols;
     return buffer_reach(p.conv, batch) ? run_gemm<true, false, 4, 1>(device, p, 1, nullptr)
                                        : run_gemm<true, false, 1, 1>(device, p, 1, nullptr);
 }
@@ -1401,7 +1429,7 @@ int axis_conv2d_backward_data(axis_device device, const float *gradient, const f
     p.y_sj = 1;
     int64_t ld[4];
     channels_last(s.out_h, s.out_w, out_channels, ld);
-    p.conv = geom(gradient, ld, s.out_h, s.out_w, out_channels, height, width, s.kw, 1, 1,
+    p.conv = geom(gradient, ld, s.out_h, s.out_w, out_channels, height, width, s.kh, s.kw, 1, 1,
                   s.kh - 1 - s.py, s.kw - 1 - s.px);
     return buffer_reach(p.conv, batch) ? run_gemm<true, false, 4, 0>(device, p, 1, d_input)
                                        : run_gemm<true, false, 1, 0>(device, p, 1, d_input);
@@ -1431,7 +1459,7 @@ int axis_conv2d_backward_weight(axis_device device, const float *input,
     p.k_work = (int64_t)((double)p.k * (double)channels / (double)in.channels);
     p.y_sr = out_channels;
     p.y_sj = 1;
-    p.conv = geom(in.src, in.ld, height, width, in.channels, s.out_h, s.out_w, s.kw, s.sy, s.sx, s.py, s.px);
+    p.conv = geom(in.src, in.ld, height, width, in.channels, s.out_h, s.out_w, s.kh, s.kw, s.sy, s.sx, s.py, s.px);
     // Every tile shape is 32 deep: when 32-pixel steps never straddle an image and cut its rows
     // the same way each time, the cheaper step loader applies.
     const int64_t image = (int64_t)s.out_h * s.out_w;
