@@ -433,11 +433,22 @@ __global__ void __launch_bounds__(kBlock) reduce_middle_kernel(const float *__re
     if (t >= outer * inner) return;
     const int64_t o = t / inner, i = t % inner;
     const float *base = a + o * reduce * inner + i;
+    // Sequential sums in the plan's order; the loads of 32 terms are issued before their adds so
+    // each thread keeps 32 reads in flight instead of one.
+    constexpr int kBatch = 32;
     float total = 0.0f;
     for (int64_t r0 = 0; r0 < reduce; r0 += axis::kGroupedChunk) {
         const int64_t r1 = r0 + axis::kGroupedChunk < reduce ? r0 + axis::kGroupedChunk : reduce;
         float partial = 0.0f;
-        for (int64_t r = r0; r < r1; ++r) partial = partial + base[r * inner];
+        int64_t r = r0;
+        for (; r + kBatch <= r1; r += kBatch) {
+            float v[kBatch];
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) v[u] = base[(r + u) * inner];
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) partial = partial + v[u];
+        }
+        for (; r < r1; ++r) partial = partial + base[r * inner];
         total = total + partial;
     }
     out[t] = total * factor;

@@ -229,45 +229,6 @@ struct DenseLoader : Staging<BT, BK, NT, RCONTIG, VEC> {
     }
 };
 
-// The same operand through 64-bit addresses: each of the thread's vectors keeps its own pointer at
-// r = 0 and a K step adds the wave-uniform r0 * s_r.  Dense products read their second operand
-// this way: with the buffer loader it ran 6% slower on 8192^3 NN products (other shapes equal).
-template <int BT, int BK, int NT, bool RCONTIG, int VEC>
-struct DensePointerLoader : Staging<BT, BK, NT, RCONTIG, VEC> {
-    using S = Staging<BT, BK, NT, RCONTIG, VEC>;
-    const float *ptr[S::kVecs];
-    int32_t rr[S::kVecs];   // r offset of each vector inside the tile
-    bool t_ok[S::kVecs];
-    int64_t s_r;
-
-    __device__ __forceinline__ void init(const float *b, int64_t st, int64_t sr, int64_t t0,
-                                         int64_t t_end, int tid) {
-        s_r = sr;
-#pragma unroll
-        for (int e = 0; e < S::kVecs; ++e) {
-            const int idx = tid + e * NT;
-            int tt, r;
-            if (RCONTIG) {
-                r = (idx % S::kPer) * VEC;
-                tt = idx / S::kPer;
-            } else {
-                tt = (idx % S::kPer) * VEC;
-                r = idx / S::kPer;
-            }
-            const int64_t gt = t0 + tt;
-            t_ok[e] = gt < t_end;
-            rr[e] = r;
-            ptr[e] = b + (t_ok[e] ? gt : 0) * st + (int64_t)r * sr;
-        }
-    }
-    __device__ __forceinline__ void load(const ConvGeom &, int64_t r0, int64_t r_end, int) {
-        const int64_t step = r0 * s_r;
-#pragma unroll
-        for (int e = 0; e < S::kVecs; ++e)
-            load_into<VEC>(this->reg + e * VEC, ptr[e] + step, t_ok[e] && r0 + rr[e] < r_end);
-    }
-};
-
 // Convolution operand, rows mode: t = output pixel, r = (ky*kw + kx)*channels + channel.
 // Per row: the offset of its window origin and the origin's coordinates (for the padding test);
 // per K step: one decode of the thread's r into a 32-bit offset shared by every row.
@@ -949,15 +910,18 @@ struct Choice {
     size_t lds_pad = 0;
 };
 
-Choice choose(int64_t m, int64_t n, int64_t batch, int64_t cus, bool pool_epilogue) {
+Choice choose(int64_t m, int64_t n, int64_t k, int64_t batch, int64_t cus, bool pool_epilogue) {
     const Choice large{Shape::Large, 128, 128, 32, 3}, tall{Shape::Tall, 128, 64, 32, 4},
         small{Shape::Small, 64, 64, 32, 5};
     if (m < 128 && !pool_epilogue) return small;
     if (n < 128) return n <= 64 || pool_epilogue ? tall : small;
+    const int64_t tiles = ((m + 127) / 128) * ((n + 127) / 128) * batch;
+    // A short reduction over few large tiles (e.g. a classifier layer) would leave most CUs idle
+    // and each block only a few K steps: four times as many small tiles finish sooner.
+    if (!pool_epilogue && tiles * 2 < cus && k <= 2048) return small;
     // Large tiles run three to a CU.  When that leaves each CU one lone block in its last round
     // (of a few), that block runs at one wave per SIMD; holding them to two per CU (padding the
     // dynamic LDS past a third of the CU's 160 KiB) fills every round instead.
-    const int64_t tiles = ((m + 127) / 128) * ((n + 127) / 128) * batch;
     const int64_t per_cu = (tiles + cus - 1) / cus;
     if (tiles % cus == 0 && per_cu % large.per_cu == 1 && per_cu < 4 * large.per_cu) {
         Choice two = large;
@@ -993,18 +957,19 @@ int sum_splits(axis_device device, const float *partial, float *out, int64_t len
 template <bool XR, bool YR, int XMODE, int EPI>
 int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out) {
     const int64_t cus = device->multiprocessors;
-    const Choice ch = choose(p.m, p.n, batch, cus, EPI == 1);
+    const Choice ch = choose(p.m, p.n, p.k, batch, cus, EPI == 1);
     const int BK = ch.bk;
     p.tiles_m = static_cast<int32_t>((p.m + ch.bm - 1) / ch.bm);
     p.tiles_n = static_cast<int32_t>((p.n + ch.bn - 1) / ch.bn);
     const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n * batch;
     // Split the reduction when the tiles alone cannot fill the chip: aim at one full round of
     // resident blocks so no round runs nearly empty.  The pooling epilogue needs whole sums.
-    // The partial slices stay within 64 MiB.
+    // Reductions under 16 K steps are not split (the extra sum launch would cost more than it
+    // saves).  The partial slices stay within 64 MiB.
     const int64_t slots = cus * ch.per_cu;
     const int64_t out_len = batch * p.m * p.n;
     int64_t splits = 1;
-    if (EPI == 0 && tiles < slots && p.k >= 8 * BK) {
+    if (EPI == 0 && tiles < slots && p.k >= 16 * BK) {
         splits = std::min<int64_t>({slots / tiles, p.k / (BK * 4), (int64_t(16) << 20) / out_len});
         splits = std::max<int64_t>(splits, 1);
     }
