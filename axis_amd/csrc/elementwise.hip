@@ -403,17 +403,34 @@ __global__ void __launch_bounds__(kBlock) column_chunk_kernel(const float *__res
                                                               float *__restrict__ masked_out,
                                                               float *__restrict__ partial,
                                                               int64_t rows, int64_t width,
-                                                              int64_t pairs) {
+                                                              int64_t pairs, float *__restrict__ out) {
     const int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x;
     if (t >= pairs) return;
     const int64_t q = t / width;
     const int64_t c = t - q * width;
     const int64_t r0 = q * axis::kGroupedChunk;
     const int64_t r1 = r0 + axis::kGroupedChunk < rows ? r0 + axis::kGroupedChunk : rows;
+    // Rows in order; the loads of 16 rows are issued before their adds.
+    constexpr int kBatch = 16;
     float sum = 0.0f;
-    int64_t idx = r0 * width + c;
-#pragma unroll 8
-    for (int64_t r = r0; r < r1; ++r, idx += width) {
+    int64_t r = r0;
+    for (; r + kBatch <= r1; r += kBatch) {
+        float v[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) v[u] = g[(r + u) * width + c];
+        if (MASK) {
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+                const int64_t idx = (r + u) * width + c;
+                v[u] = relu_input[idx] > 0.0f ? v[u] : 0.0f;
+                masked_out[idx] = v[u];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) sum = sum + v[u];
+    }
+    for (; r < r1; ++r) {
+        const int64_t idx = r * width + c;
         float v = g[idx];
         if (MASK) {
             v = relu_input[idx] > 0.0f ? v : 0.0f;
@@ -421,7 +438,11 @@ __global__ void __launch_bounds__(kBlock) column_chunk_kernel(const float *__res
         }
         sum = sum + v;
     }
-    partial[q * width + c] = sum;
+    // A single chunk is also the whole sum: the combine's 0 + p0 (scale 1) written here.
+    if (out)
+        out[c] = 0.0f + sum;
+    else
+        partial[q * width + c] = sum;
 }
 
 // out[o][i] = factor * sum_r a[o][r][i] in the reference's chunked order.
@@ -695,15 +716,18 @@ int axis_bias_gradient(axis_device device, const float *gradient, const float *r
     const int64_t pairs = chunks * width;
     AXIS_REQUIRE(pairs / kBlock < INT32_MAX && width < INT32_MAX, "bias_gradient too large");
     axis::Scratch partial;
-    if (int s = partial.get(device, sizeof(float) * (size_t)pairs)) return s;
+    if (chunks > 1)
+        if (int s = partial.get(device, sizeof(float) * (size_t)pairs)) return s;
+    float *direct = chunks == 1 ? out : nullptr;
     const unsigned grid = axis::blocks_for(pairs, kBlock, INT32_MAX);
     if (relu_input)
         column_chunk_kernel<true><<<grid, kBlock, 0, device->stream>>>(
-            gradient, relu_input, masked_out, partial.as<float>(), rows, width, pairs);
+            gradient, relu_input, masked_out, partial.as<float>(), rows, width, pairs, direct);
     else
         column_chunk_kernel<false><<<grid, kBlock, 0, device->stream>>>(
-            gradient, nullptr, nullptr, partial.as<float>(), rows, width, pairs);
+            gradient, nullptr, nullptr, partial.as<float>(), rows, width, pairs, direct);
     if (int s = axis::launch_status("column_chunk_kernel")) return s;
+    if (chunks == 1) return AXIS_OK;
     axis::column_combine_kernel<<<(unsigned)width, 256, 0, device->stream>>>(partial.as<float>(), chunks,
                                                                            width, 1.0f, out);
     return axis::launch_status("column_combine_kernel");

@@ -65,6 +65,16 @@ __device__ __forceinline__ int64_t tile_pixel(const ConvGeom &g, int64_t t0, int
     return t0 + (int64_t)(2 * wr + (pos >> 1)) * g.out_w + 2 * wc + (pos & 1u);
 }
 
+// Second operand read straight from a convolution weight in the reference's [(c, ky, kx), n]
+// layout: the reduction index is r = pos * R + q (pos = ky * kw + kx, R rows per tap, R a
+// multiple of the K step), and a K step starting at r0 = pos * R + q0 begins at element
+// q0 * qa + pos * pb + pc, its rows s_r apart.
+struct TapSteps {
+    bool on;
+    FastDiv r_div;   // R
+    int64_t qa, pb, pc;
+};
+
 struct GemmParams {
     const float *x;
     const float *y;
@@ -89,6 +99,10 @@ struct GemmParams {
     uint8_t *argmax;
     int32_t pool_h, pool_w, pool_ow;
     FastDiv pool_cols;         // pooled columns per output row (pool_ow / pool_w)
+    TapSteps ytaps;            // Y read as a tap-major convolution weight
+    // Output rows ordered (pos, c) with perm_c channels and perm_taps taps are written as rows
+    // c * perm_taps + pos (the reference's weight layout); 0 = rows as computed.
+    int32_t perm_c, perm_taps;
 };
 
 template <int VEC>
@@ -187,6 +201,7 @@ struct DenseLoader : Staging<BT, BK, NT, RCONTIG, VEC> {
     uint32_t lane_off;             // this lane's element offset from its vector's first lane
     int32_t r_lane;
     int64_t s_r;
+    TapSteps taps{};               // tap-major steps (convolution weights), if on
 
     static __device__ __forceinline__ void split(int idx, int &tt, int &r) {
         if (RCONTIG) {
@@ -218,7 +233,12 @@ struct DenseLoader : Staging<BT, BK, NT, RCONTIG, VEC> {
         }
     }
     __device__ __forceinline__ void load(const ConvGeom &, int64_t r0, int64_t r_end, int) {
-        const int64_t step = r0 * s_r;
+        int64_t step = r0 * s_r;
+        if (taps.on) {
+            const uint32_t pos = taps.r_div.div((uint32_t)r0);
+            const int64_t q0 = r0 - (int64_t)pos * taps.r_div.d;
+            step = q0 * taps.qa + (int64_t)pos * taps.pb + taps.pc;
+        }
         const int32_t room = (int32_t)(r_end - r0 < BK ? r_end - r0 : BK);  // k left in this step
 #pragma unroll
         for (int e = 0; e < S::kVecs; ++e) {
@@ -551,6 +571,7 @@ __global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
     else
         lx.init(p.conv, i0, p.m, tid);
     ly.init(p.y + batch * p.y_batch, p.y_sj, p.y_sr, j0, p.n, tid);
+    ly.taps = p.ytaps;
     if (r_begin < r_end) {
         lx.load(p.conv, r_begin, r_end, tid);
         ly.load(p.conv, r_begin, r_end, tid);
@@ -782,7 +803,7 @@ __global__ void __launch_bounds__(256) split_sum_kernel(const float *__restrict_
                                                         int32_t splits, int64_t split_stride,
                                                         const float *__restrict__ bias, int64_t n,
                                                         const float *__restrict__ d, float alpha,
-                                                        float beta) {
+                                                        float beta, int32_t perm_c, int32_t perm_taps) {
     __shared__ float acc[4][64];
     const int lane = threadIdx.x & 63, group = threadIdx.x >> 6;
     const int64_t i = (int64_t)blockIdx.x * 64 + lane;
@@ -793,7 +814,12 @@ __global__ void __launch_bounds__(256) split_sum_kernel(const float *__restrict_
     __syncthreads();
     if (group == 0 && i < len) {
         const float total = ((acc[0][lane] + acc[1][lane]) + acc[2][lane]) + acc[3][lane];
-        out[i] = finish_value(bias, d, alpha, beta, total, i, i % n);
+        int64_t at = i;
+        if (perm_c) {  // row (pos, c) -> c * taps + pos
+            const int64_t row = i / n, col = i - row * n;
+            at = ((row % perm_c) * perm_taps + row / perm_c) * n + col;
+        }
+        out[at] = finish_value(bias, d, alpha, beta, total, i, i % n);
     }
 }
 
@@ -935,11 +961,12 @@ Choice choose(int64_t m, int64_t n, int64_t k, int64_t batch, int64_t cus, bool 
 // Deterministic sum of reduction slices (+ bias): up to 32 slices in one pass; beyond that, ranges
 // of 32 consecutive slices first, then the range sums -- a fixed association for a given count.
 int sum_splits(axis_device device, const float *partial, float *out, int64_t len, int64_t splits,
-               const float *bias, int64_t n, const float *d, float alpha, float beta) {
+               const float *bias, int64_t n, const float *d, float alpha, float beta, int32_t perm_c,
+               int32_t perm_taps) {
     const unsigned blocks = axis::blocks_for(len, 64, INT32_MAX);
     if (splits <= 32) {
         split_sum_kernel<<<blocks, 256, 0, device->stream>>>(partial, out, len, (int32_t)splits, len, bias, n, d,
-                                                             alpha, beta);
+                                                             alpha, beta, perm_c, perm_taps);
         return axis::launch_status("split_sum_kernel");
     }
     const int32_t span = 32;
@@ -950,7 +977,7 @@ int sum_splits(axis_device device, const float *partial, float *out, int64_t len
     split_range_kernel<<<grid, 256, 0, device->stream>>>(partial, mid.as<float>(), len, (int32_t)splits, span);
     if (int st = axis::launch_status("split_range_kernel")) return st;
     split_sum_kernel<<<blocks, 256, 0, device->stream>>>(mid.as<float>(), out, len, (int32_t)ranges, len, bias, n,
-                                                         d, alpha, beta);
+                                                         d, alpha, beta, perm_c, perm_taps);
     return axis::launch_status("split_sum_kernel");
 }
 
@@ -997,7 +1024,7 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out) {
     const bool vy = YR ? vec_ok(p.y, p.k, p.y_sj) && p.y_batch % 4 == 0
                        : vec_ok(p.y, p.n, p.y_sr) && p.y_batch % 4 == 0;
 
-    axis::Scratch partial;
+    axis::Scratch partial, ordered;
     if (splits > 1) {
         int status = partial.get(device, sizeof(float) * (size_t)(out_len * splits));
         if (status) return status;
@@ -1005,7 +1032,10 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out) {
         p.c_split = out_len;
         p.c_batch = p.m * p.n;
     } else {
-        p.c = out;
+        // an unsplit product with permuted rows is written in its own order, then moved
+        if (p.perm_c)
+            if (int status = ordered.get(device, sizeof(float) * (size_t)out_len)) return status;
+        p.c = p.perm_c ? ordered.as<float>() : out;
         p.c_split = 0;
         p.c_batch = p.m * p.n;
     }
@@ -1031,7 +1061,14 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out) {
     int status = axis::launch_status("gemm_kernel");
     if (status) return status;
     if (splits > 1)
-        status = sum_splits(device, partial.as<float>(), out, out_len, splits, p.bias, p.n, p.d, p.alpha, p.beta);
+        status = sum_splits(device, partial.as<float>(), out, out_len, splits, p.bias, p.n, p.d, p.alpha, p.beta,
+                            p.perm_c, p.perm_taps);
+    else if (p.perm_c) {
+        // mode 2 of the weight permutation with the taps as one axis
+        conv_weight_permute_kernel<<<axis::blocks_for(out_len, 256, 4096), 256, 0, device->stream>>>(
+            ordered.as<float>(), out, p.perm_c, p.perm_c, (int32_t)p.n, p.perm_taps, 1, 2);
+        status = axis::launch_status("conv_weight_permute_kernel");
+    }
     return status;
 }
 
@@ -1155,6 +1192,27 @@ int permute_weight(axis_device device, const float *src, float *dst, const ConvS
     conv_weight_permute_kernel<<<axis::blocks_for(total, 256, 4096), 256, 0, device->stream>>>(
         src, dst, s.channels, c_pad, s.out_channels, s.kh, s.kw, mode);
     return axis::launch_status("conv_weight_permute_kernel");
+}
+
+// The forward's second operand W'[(ky, kx, c), n]: read in place from the reference's
+// [(c, ky, kx), n] weight when the channels need no padding and a K step stays in one tap
+// (c % 32 == 0), otherwise permuted (and padded) into `permuted`.
+int forward_weight(axis_device device, const float *weight, const ConvShape &s, int32_t c_pad,
+                   axis::Scratch &permuted, GemmParams &p) {
+    const int64_t taps = (int64_t)s.kh * s.kw;
+    if (c_pad == s.channels && s.channels % 32 == 0) {
+        p.y = weight;
+        p.y_sj = 1;
+        p.y_sr = taps * s.out_channels;
+        p.ytaps = TapSteps{true, FastDiv((uint32_t)s.channels), taps * s.out_channels, s.out_channels, 0};
+        return AXIS_OK;
+    }
+    if (int st = permuted.get(device, sizeof(float) * (size_t)(c_pad * taps * s.out_channels))) return st;
+    if (int st = permute_weight(device, weight, permuted.as<float>(), s, 0, c_pad)) return st;
+    p.y = permuted.as<float>();
+    p.y_sr = s.out_channels;
+    p.y_sj = 1;
+    return AXIS_OK;
 }
 
 // The gathered input of a forward or weight-gradient launch: the caller's tensor when it is
@@ -1297,17 +1355,13 @@ int axis_conv2d_forward(axis_device device, const float *input, const int64_t in
     if (int st = in.prepare(device, input, input_strides_, batch, height, width, channels)) return st;
     const int64_t patch = (int64_t)in.channels * s.kh * s.kw;
     axis::Scratch permuted;
-    if (int st = permuted.get(device, sizeof(float) * (size_t)(patch * out_channels))) return st;
-    if (int st = permute_weight(device, weight, permuted.as<float>(), s, 0, in.channels)) return st;
     GemmParams p{};
-    p.y = permuted.as<float>();
+    if (int st = forward_weight(device, weight, s, in.channels, permuted, p)) return st;
     p.bias = bias;
     p.m = batch * s.out_h * s.out_w;
     p.n = out_channels;
     p.k = patch;
     p.k_work = (int64_t)channels * s.kh * s.kw;
-    p.y_sr = out_channels;
-    p.y_sj = 1;
     p.conv = geom(in.src, in.ld, height, width, in.channels, s.out_h, s.out_w, s.kh, s.kw, s.sy, s.sx, s.py, s.px);
     return buffer_reach(p.conv, batch) ? run_gemm<true, false, 4, 0>(device, p, 1, out)
                                        : run_gemm<true, false, 1, 0>(device, p, 1, out);
@@ -1340,17 +1394,13 @@ int axis_conv2d_relu_pool_forward(axis_device device, const float *input,
     if (int st = in.prepare(device, input, input_strides_, batch, height, width, channels)) return st;
     const int64_t patch = (int64_t)in.channels * s.kh * s.kw;
     axis::Scratch permuted;
-    if (int st = permuted.get(device, sizeof(float) * (size_t)(patch * out_channels))) return st;
-    if (int st = permute_weight(device, weight, permuted.as<float>(), s, 0, in.channels)) return st;
     GemmParams p{};
-    p.y = permuted.as<float>();
+    if (int st = forward_weight(device, weight, s, in.channels, permuted, p)) return st;
     p.bias = bias;
     p.m = batch * s.out_h * s.out_w;
     p.n = out_channels;
     p.k = patch;
     p.k_work = (int64_t)channels * s.kh * s.kw;
-    p.y_sr = out_channels;
-    p.y_sj = 1;
     p.conv = geom(in.src, in.ld, height, width, in.channels, s.out_h, s.out_w, s.kh, s.kw, s.sy, s.sx, s.py, s.px);
     p.pooled = pooled;
     p.argmax = argmax;
@@ -1376,26 +1426,26 @@ int axis_conv2d_backward_data(axis_device device, const float *gradient, const f
         return st;
     AXIS_REQUIRE(s.sy == 1 && s.sx == 1, "implicit convolution dgrad supports stride 1 only");
     AXIS_REQUIRE(s.py <= s.kh - 1 && s.px <= s.kw - 1, "implicit convolution dgrad needs padding < kernel");
-    const int64_t patch = (int64_t)channels * s.kh * s.kw;
-    axis::Scratch flipped;
-    if (int st = flipped.get(device, sizeof(float) * (size_t)(patch * out_channels))) return st;
-    if (int st = permute_weight(device, weight, flipped.as<float>(), s, 1, channels)) return st;
+    const int64_t taps = (int64_t)s.kh * s.kw;
     // d_input[b, y, x, c] = sum over (ky', kx', n) of gradient[b, y + ky' - (kh-1-py),
     // x + kx' - (kw-1-px), n] * W[(c, kh-1-ky', kw-1-kx'), n]: a stride-1 convolution of the
     // output gradient with the flipped, transposed kernel -- the reference's col2im of
     // gradient . W^T, summed in a different (fp32) order.
     GemmParams p{};
     p.x = gradient;
-    p.y = flipped.as<float>();
     p.m = batch * (int64_t)height * width;
     p.n = channels;
-    p.k = (int64_t)s.kh * s.kw * out_channels;
-    p.y_sr = channels;
-    p.y_sj = 1;
+    p.k = taps * out_channels;
     int64_t ld[4];
     channels_last(s.out_h, s.out_w, out_channels, ld);
     p.conv = geom(gradient, ld, s.out_h, s.out_w, out_channels, height, width, s.kh, s.kw, 1, 1,
                   s.kh - 1 - s.py, s.kw - 1 - s.px);
+    axis::Scratch flipped;
+    if (int st = flipped.get(device, sizeof(float) * (size_t)(taps * channels * out_channels))) return st;
+    if (int st = permute_weight(device, weight, flipped.as<float>(), s, 1, channels)) return st;
+    p.y = flipped.as<float>();
+    p.y_sr = channels;
+    p.y_sj = 1;
     return buffer_reach(p.conv, batch) ? run_gemm<true, false, 4, 0>(device, p, 1, d_input)
                                        : run_gemm<true, false, 1, 0>(device, p, 1, d_input);
 }
@@ -1413,9 +1463,17 @@ int axis_conv2d_backward_weight(axis_device device, const float *input,
     GatherInput in;
     if (int st = in.prepare(device, input, input_strides_, batch, height, width, channels)) return st;
     const int64_t patch = (int64_t)in.channels * s.kh * s.kw;
+    // Without channel padding the product's rows (ky, kx, c) go straight to the reference's
+    // (c, ky, kx) order as the reduction slices are summed.
+    const bool direct = in.channels == channels;
     axis::Scratch ordered;
-    if (int st = ordered.get(device, sizeof(float) * (size_t)(patch * out_channels))) return st;
+    if (!direct)
+        if (int st = ordered.get(device, sizeof(float) * (size_t)(patch * out_channels))) return st;
     GemmParams p{};
+    if (direct) {
+        p.perm_c = channels;
+        p.perm_taps = s.kh * s.kw;
+    }
     p.y = gradient;
     p.m = patch;
     p.n = out_channels;
@@ -1429,9 +1487,9 @@ int axis_conv2d_backward_weight(axis_device device, const float *input,
     // the same way each time, the cheaper step loader applies.
     const int64_t image = (int64_t)s.out_h * s.out_w;
     const bool aligned = (32 % s.out_w == 0 || s.out_w % 32 == 0) && image % 32 == 0;
-    const int st = aligned ? run_gemm<false, false, 3, 0>(device, p, 1, ordered.as<float>())
-                           : run_gemm<false, false, 2, 0>(device, p, 1, ordered.as<float>());
-    if (st) return st;
+    float *dst = direct ? d_weight : ordered.as<float>();
+    const int st = aligned ? run_gemm<false, false, 3, 0>(device, p, 1, dst) : run_gemm<false, false, 2, 0>(device, p, 1, dst);
+    if (st || direct) return st;
     return permute_weight(device, ordered.as<float>(), d_weight, s, 2, in.channels);
 }
 
