@@ -103,10 +103,11 @@ __device__ __forceinline__ void store_strip(const SmallConvArgs &a, float *strip
     }
 }
 
-// LDS offset of patch term k = (c, ky, kx) from its pixel; terms past the reduction read plane
-// `spare` (zeros in the forward, ones in the weight gradient).
-__device__ __forceinline__ int32_t term_offset(const SmallConvArgs &a, int32_t k, int32_t spare) {
-    if (k >= a.k) return spare * a.plane;
+// LDS offset of patch term k = (c, ky, kx) from its pixel; term a.k reads plane `at_k` and the
+// terms past it plane `past_k`.
+__device__ __forceinline__ int32_t term_offset(const SmallConvArgs &a, int32_t k, int32_t at_k, int32_t past_k) {
+    if (k == a.k) return at_k * a.plane;
+    if (k > a.k) return past_k * a.plane;
     const int32_t taps = a.kh * a.kw;
     const int32_t c = k / taps;
     const int32_t t = k - c * taps;
@@ -114,47 +115,49 @@ __device__ __forceinline__ int32_t term_offset(const SmallConvArgs &a, int32_t k
     return c * a.plane + ky * a.strip_w + (t - ky * a.kw);
 }
 
-// Forward: KP k-pairs of v_mfma_f32_32x32x2_f32 per pixel tile (2*KP >= k), 32 pixels (8
-// windows) by 64 output channels per wave.  POOL: bias + ReLU + 2x2 max pool in registers;
-// otherwise the plain convolution + bias.
+// Forward: KP k-pairs of v_mfma_f32_32x32x2_f32 per pixel tile (2*KP >= k + 1), 32 pixels (8
+// windows) by 64 output channels per wave.  Term k of the reduction is the bias: a plane of ones
+// in the staged input times a weight row holding the bias, so the products come out biased.
+// POOL: ReLU + 2x2 max pool in registers; otherwise the plain convolution + bias.
 template <int KP, bool POOL>
 __global__ void __launch_bounds__(256, 4) small_conv_forward_kernel(SmallConvArgs a) {
-    extern __shared__ float strip[];  // planes 0..c_in-1: input; plane c_in: zeros
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    extern __shared__ float strip[];  // planes 0..c_in-1: input; plane c_in: zeros; c_in + 1: ones
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l32 = lane & 31, half = lane >> 5;
     const int32_t col0 = (int32_t)blockIdx.y * 64;
 
     // MFMA B operand of k-pair j: W[2j + half][col0 + 2*l32 + b] (column block b holds the odd /
-    // even columns, so a lane's two columns are adjacent in the output).  A operand: LDS offset
-    // of term 2j + half from the pixel.
+    // even columns, so a lane's two columns are adjacent in the output), the bias at term k.
+    // A operand: LDS offset of term 2j + half from the pixel.
     float wreg[KP][2];
     int32_t off[KP];
 #pragma unroll
     for (int j = 0; j < KP; ++j) {
         const int32_t k = 2 * j + half;
-        off[j] = term_offset(a, k, a.c_in);
+        off[j] = term_offset(a, k, a.c_in + 1, a.c_in);
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
             const int32_t n = col0 + 2 * l32 + b;
-            wreg[j][b] = (k < a.k && n < a.n) ? a.w[(int64_t)k * a.n + n] : 0.0f;
+            float w = 0.0f;
+            if (n < a.n && k < a.k) w = a.w[(int64_t)k * a.n + n];
+            if (n < a.n && k == a.k && a.bias != nullptr) w = a.bias[n];
+            wreg[j][b] = w;
         }
     }
-    float bias_v[2];
     bool col_ok[2];
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-        const int32_t n = col0 + 2 * l32 + b;
-        col_ok[b] = n < a.n;
-        bias_v[b] = (a.bias != nullptr && col_ok[b]) ? a.bias[n] : 0.0f;
-    }
-    const bool with_bias = a.bias != nullptr;
+    for (int b = 0; b < 2; ++b) col_ok[b] = col0 + 2 * l32 + b < a.n;
     const bool paired = a.wide && col_ok[1];
-    for (int32_t t = tid; t < a.plane; t += 256) strip[a.c_in * a.plane + t] = 0.0f;
+    for (int32_t t = tid; t < a.plane; t += 256) {
+        strip[a.c_in * a.plane + t] = 0.0f;
+        strip[(a.c_in + 1) * a.plane + t] = 1.0f;
+    }
 
     const int32_t band_windows = a.band_r * a.band_s;
-    const int32_t tiles = (band_windows + 7) / 8;
-    // A band row holds whole tiles: every window of a tile is in one window row.
-    const bool row_tiles = a.band_s % 8 == 0;
+    const int32_t tiles = band_windows / 8;  // band_s is a multiple of 8: whole tiles per band row
+    const int64_t pool_step = 2 * (int64_t)a.n;  // output elements between windows 2 columns apart
+    // staged cell of row l32's pixel relative to its tile's first window
+    const int32_t lane_px = ((l32 >> 1) & 1) * a.strip_w + 2 * (l32 >> 2) + (l32 & 1);
     StripRegs pre;
     if (blockIdx.x < (uint32_t)a.bands) load_strip(a, decode_band(a, blockIdx.x), tid, pre);
     for (uint32_t band = blockIdx.x; band < (uint32_t)a.bands; band += gridDim.x) {
@@ -164,12 +167,11 @@ __global__ void __launch_bounds__(256, 4) small_conv_forward_kernel(SmallConvArg
         if (band + gridDim.x < (uint32_t)a.bands) load_strip(a, decode_band(a, band + gridDim.x), tid, pre);
         __syncthreads();
         for (int32_t tile = wave; tile < tiles; tile += 4) {
-            // Row i = l32: window tile*8 + i/4, position i%4 = (ky, kx) of the window.
-            int32_t wi = tile * 8 + (l32 >> 2);
-            wi = wi < band_windows ? wi : band_windows - 1;
-            const int32_t pr = (int32_t)a.s_div.div((uint32_t)wi);
-            const int32_t pc = wi - pr * a.band_s;
-            const float *px0 = strip + (2 * pr + ((l32 >> 1) & 1)) * a.strip_w + 2 * pc + (l32 & 1);
+            // Row i = l32: window tile*8 + i/4, position i%4 = (ky, kx) of the window.  The tile's
+            // windows sit in window row wr, columns c0 .. c0 + 7 of the band.
+            const int32_t wr = (int32_t)a.s_div.div((uint32_t)(tile * 8));
+            const int32_t c0 = tile * 8 - wr * a.band_s;
+            const float *px0 = strip + (2 * wr * a.strip_w + 2 * c0) + lane_px;
             floatx16 acc[2];
 #pragma unroll
             for (int b = 0; b < 2; ++b)
@@ -185,53 +187,49 @@ __global__ void __launch_bounds__(256, 4) small_conv_forward_kernel(SmallConvArg
             if (!col_ok[0]) continue;
             // Accumulator register v: row i = 8*(v/4) + 4*half + v%4, i.e. window
             // tile*8 + 2*(v/4) + half, position v%4.
-            const int32_t w_first = tile * 8 + half;
-            const int32_t r_first = (int32_t)a.s_div.div((uint32_t)w_first);
-            const int32_t c_first = w_first - r_first * a.band_s;
+            const int32_t c_first = c0 + half;
+            if (bd.wr0 + wr >= a.win_rows) continue;
+            if constexpr (POOL) {
+                // pooled element of the lane's first window; the others follow 2 columns apart
+                const int64_t o_first =
+                    (((int64_t)bd.img * a.win_rows + bd.wr0 + wr) * a.win_cols + bd.wc0 + c_first) * a.n + col0 +
+                    2 * l32;
+                float *pooled_at = a.pooled + o_first;
+                uint8_t *argmax_at = a.argmax + o_first;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int32_t wt = w_first + 2 * q;
-                if (wt >= band_windows) continue;
-                int32_t wr, wc;
-                if (row_tiles) {
-                    wr = r_first;
-                    wc = c_first + 2 * q;
-                } else {
-                    wr = (int32_t)a.s_div.div((uint32_t)wt);
-                    wc = wt - wr * a.band_s;
-                }
-                if constexpr (POOL) {
-                    if (bd.wr0 + wr >= a.win_rows || bd.wc0 + wc >= a.win_cols) continue;
+                for (int q = 0; q < 4; ++q, pooled_at += pool_step, argmax_at += pool_step) {
+                    if (bd.wc0 + c_first + 2 * q >= a.win_cols) continue;
                     float best[2];
                     int winner[2];
 #pragma unroll
                     for (int b = 0; b < 2; ++b) {
                         float y[4];
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) y[e] = acc[b][4 * q + e] + bias_v[b];
+                        for (int e = 0; e < 4; ++e) y[e] = acc[b][4 * q + e];
                         relu_pool_window4(y, best[b], winner[b]);
                     }
-                    const int64_t pix = ((int64_t)bd.img * a.win_rows + bd.wr0 + wr) * a.win_cols + bd.wc0 + wc;
-                    const int64_t o = pix * a.n + col0 + 2 * l32;
                     if (paired) {
-                        *reinterpret_cast<float2 *>(a.pooled + o) = make_float2(best[0], best[1]);
-                        *reinterpret_cast<uint16_t *>(a.argmax + o) = (uint16_t)(winner[0] | (winner[1] << 8));
+                        *reinterpret_cast<float2 *>(pooled_at) = make_float2(best[0], best[1]);
+                        *reinterpret_cast<uint16_t *>(argmax_at) = (uint16_t)(winner[0] | (winner[1] << 8));
                     } else {
 #pragma unroll
                         for (int b = 0; b < 2; ++b) {
                             if (!col_ok[b]) continue;
-                            a.pooled[o + b] = best[b];
-                            a.argmax[o + b] = (uint8_t)winner[b];
+                            pooled_at[b] = best[b];
+                            argmax_at[b] = (uint8_t)winner[b];
                         }
                     }
-                } else {
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int32_t wc = c_first + 2 * q;
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const int32_t y = 2 * (bd.wr0 + wr) + (e >> 1), x = 2 * (bd.wc0 + wc) + (e & 1);
                         if (y >= a.out_h || x >= a.out_w) continue;
                         const int64_t o = (((int64_t)bd.img * a.out_h + y) * a.out_w + x) * a.n + col0 + 2 * l32;
-                        const float v0 = with_bias ? acc[0][4 * q + e] + bias_v[0] : acc[0][4 * q + e];
-                        const float v1 = with_bias ? acc[1][4 * q + e] + bias_v[1] : acc[1][4 * q + e];
+                        const float v0 = acc[0][4 * q + e], v1 = acc[1][4 * q + e];
                         if (paired) {
                             *reinterpret_cast<float2 *>(a.out + o) = make_float2(v0, v1);
                         } else {
@@ -299,12 +297,20 @@ __device__ __forceinline__ void store_grad(const SmallConvArgs &a, float *dy, in
         const int32_t t = tid + 256 * i;
         const int32_t wi = t >> 4, c4 = (t & 15) * 4;
         if (wi >= band_windows) continue;
+        // position of each element's winner when its pooled value is positive (else none), and
+        // 0 + g, the value the scatter writes there
+        uint32_t sel[4];
+        float gz[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            sel[e] = r.p[i][e] > 0.0f ? (r.w[i] >> (8 * e)) & 0xffu : 0xffu;
+            gz[e] = 0.0f + r.g[i][e];
+        }
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
             floatx4 o;
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                o[e] = (((r.w[i] >> (8 * e)) & 0xffu) == (uint32_t)p && r.p[i][e] > 0.0f) ? 0.0f + r.g[i][e] : 0.0f;
+            for (int e = 0; e < 4; ++e) o[e] = sel[e] == (uint32_t)p ? gz[e] : 0.0f;
             *reinterpret_cast<floatx4 *>(dy + (wi * 4 + p) * 64 + (c4 ^ (16 * p))) = o;
         }
     }
@@ -317,10 +323,17 @@ __global__ void __launch_bounds__(256, 4) small_conv_pool_wgrad_kernel(SmallConv
     extern __shared__ float lds[];
     float *const strip = lds;                                   // planes 0..c_in-1: input; c_in: ones
     float *const dy = lds + ((a.c_in + 1) * a.plane + 3) / 4 * 4;  // [window][4][64]
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nl = lane & 15, pos = lane >> 4;
     const int32_t col0 = (int32_t)blockIdx.y * 64;
-    const int32_t toff[2] = {term_offset(a, nl, a.c_in), term_offset(a, nl + 16, a.c_in)};
+    // staged cells of the lane's two terms at position pos of a window, from the window's first
+    // cell; and the lane's gradient column in each column block (XOR-swizzled by position)
+    const int32_t lane_px = (pos >> 1) * a.strip_w + (pos & 1);
+    const int32_t xoff[2] = {lane_px + term_offset(a, nl, a.c_in, a.c_in),
+                             lane_px + term_offset(a, nl + 16, a.c_in, a.c_in)};
+    int32_t doff[4];
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) doff[nb] = pos * 64 + 16 * (nb ^ pos) + nl;
     for (int32_t t = tid; t < a.plane; t += 256) strip[a.c_in * a.plane + t] = 1.0f;
 
     floatx4 acc[4][2];
@@ -352,12 +365,12 @@ __global__ void __launch_bounds__(256, 4) small_conv_pool_wgrad_kernel(SmallConv
         for (int32_t wi = wave; wi < band_windows; wi += 4) {
             const int32_t wr = (int32_t)a.s_div.div((uint32_t)wi);
             const int32_t wc = wi - wr * a.band_s;
-            const float *px0 = strip + (2 * wr + (pos >> 1)) * a.strip_w + 2 * wc + (pos & 1);
-            const float x0 = px0[toff[0]], x1 = px0[toff[1]];
-            const float *dyw = dy + (wi * 4 + pos) * 64 + nl;
+            const float *pw = strip + 2 * wr * a.strip_w + 2 * wc;
+            const float x0 = pw[xoff[0]], x1 = pw[xoff[1]];
+            const float *dyw = dy + wi * 256;
 #pragma unroll
             for (int nb = 0; nb < 4; ++nb) {
-                const float d = dyw[16 * (nb ^ pos)];
+                const float d = dyw[doff[nb]];
                 acc[nb][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(d, x0, acc[nb][0], 0, 0, 0);
                 acc[nb][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(d, x1, acc[nb][1], 0, 0, 0);
             }
@@ -406,12 +419,14 @@ __global__ void __launch_bounds__(256) small_conv_combine_kernel(const float *__
     }
 }
 
-// Windows per band: S columns (at most 32) by R rows, R * S <= cap, with at most 512 staged
-// cells (rows x columns), the capacity of the threads' prefetch registers.
+// Windows per band: S columns (a multiple of 8, at most 32; windows past the image are skipped)
+// by R rows, R * S <= cap, with at most 512 staged cells (rows x columns), the capacity of the
+// threads' prefetch registers.
 void band_shape(SmallConvArgs &a, int64_t batch, int32_t cap) {
     auto cells = [&](int32_t r, int32_t s) { return (2 * r + a.kh - 1) * (2 * s + a.kw - 1); };
-    a.band_s = a.win_cols < 32 ? a.win_cols : 32;
-    while (a.band_s > 1 && cells(1, a.band_s) > 512) a.band_s = (a.band_s + 1) / 2;
+    a.band_s = (a.win_cols + 7) / 8 * 8;
+    if (a.band_s > 32) a.band_s = 32;
+    while (a.band_s > 8 && cells(1, a.band_s) > 512) a.band_s -= 8;
     a.band_r = cap / a.band_s;
     if (a.band_r < 1) a.band_r = 1;
     if (a.band_r > a.win_rows) a.band_r = a.win_rows;
@@ -457,8 +472,9 @@ int make_args(const axis::SmallConvShape &s, const float *input, const int64_t l
     return AXIS_OK;
 }
 
-size_t strip_bytes(const SmallConvArgs &a) {
-    return sizeof(float) * (size_t)(((a.c_in + 1) * a.plane + 3) / 4 * 4);
+// Staged planes: the input's channels plus `extra` constant planes.
+size_t strip_bytes(const SmallConvArgs &a, int extra) {
+    return sizeof(float) * (size_t)(((a.c_in + extra) * a.plane + 3) / 4 * 4);
 }
 
 // The weight gradient's expansion [window][4][64], also the four waves' [32][64] sums at the end.
@@ -476,10 +492,10 @@ unsigned persistent_blocks(axis_device device, int64_t bands, int64_t columns) {
 
 template <bool POOL>
 int launch_forward(axis_device device, const SmallConvArgs &a) {
-    const int kp = (a.k + 1) / 2;
+    const int kp = (a.k + 2) / 2;  // the k terms and the bias term
     const unsigned columns = (unsigned)((a.n + 63) / 64);
     dim3 grid(persistent_blocks(device, a.bands, columns), columns);
-    const size_t lds = strip_bytes(a);
+    const size_t lds = strip_bytes(a, 2);
     hipStream_t st = device->stream;
 #define AXIS_SMALL_FWD(KPV)                                                      \
     if (kp <= KPV) {                                                             \
@@ -512,8 +528,8 @@ bool small_conv_applies(const SmallConvShape &s) {
     make_args(s, nullptr, nullptr, nullptr, nullptr, 64, fwd);
     make_args(s, nullptr, nullptr, nullptr, nullptr, 32, bwd);
     const size_t limit = 40 * 1024;
-    return fwd.plane <= 512 && bwd.plane <= 512 && strip_bytes(fwd) <= limit &&
-           strip_bytes(bwd) + gradient_bytes(bwd) <= limit;
+    return fwd.plane <= 512 && bwd.plane <= 512 && strip_bytes(fwd, 2) <= limit &&
+           strip_bytes(bwd, 1) + gradient_bytes(bwd) <= limit;
 }
 
 int small_conv_forward(axis_device device, const SmallConvShape &s, const float *input, const int64_t ld[4],
@@ -541,7 +557,7 @@ int small_conv_pool_backward_weight(axis_device device, const SmallConvShape &s,
     const unsigned blocks = persistent_blocks(device, a.bands, columns);
     Scratch partial;
     if (int st = partial.get(device, sizeof(float) * (size_t)blocks * 32 * (size_t)a.n)) return st;
-    const size_t lds = strip_bytes(a) + gradient_bytes(a);
+    const size_t lds = strip_bytes(a, 1) + gradient_bytes(a);
     {
         TimedLaunch timed(device, "gemm", 2.0 * (double)s.batch * s.out_h * s.out_w * s.out_channels * a.k);
         small_conv_pool_wgrad_kernel<<<dim3(blocks, columns), 256, lds, device->stream>>>(a, gradient, pooled, argmax,
