@@ -20,6 +20,7 @@
 //   of the product the bias gradient (the column sum of the same values).
 #include <cfloat>
 
+#include "column_sum.hpp"
 #include "common.hpp"
 #include "conv_small.hpp"
 #include "fastdiv.hpp"
@@ -396,29 +397,6 @@ __global__ void __launch_bounds__(256, 4) small_conv_pool_wgrad_kernel(SmallConv
     }
 }
 
-// d_weight[t][n] (t < k) and d_bias[n] (t = k) = sum over blocks of partial[block][t][n], in block
-// order per lane and a fixed pairwise tree over the 256 lanes: the same association on every run.
-__global__ void __launch_bounds__(256) small_conv_combine_kernel(const float *__restrict__ partial, int32_t blocks,
-                                                                 int32_t n, int32_t k, float *__restrict__ d_weight,
-                                                                 float *__restrict__ d_bias) {
-    __shared__ float s[256];
-    const int32_t e = blockIdx.x;  // t * n + column
-    float v = 0.0f;
-    for (int32_t b = threadIdx.x; b < blocks; b += 256) v += partial[((int64_t)b * 32) * n + e];
-    s[threadIdx.x] = v;
-    __syncthreads();
-    for (int h = 128; h > 0; h >>= 1) {
-        if ((int)threadIdx.x < h) s[threadIdx.x] = s[threadIdx.x] + s[threadIdx.x + h];
-        __syncthreads();
-    }
-    if (threadIdx.x == 0) {
-        if (e < k * n)
-            d_weight[e] = s[0];
-        else if (d_bias)
-            d_bias[e - k * n] = s[0];
-    }
-}
-
 // Windows per band: S columns (a multiple of 8, at most 32; windows past the image are skipped)
 // by R rows, R * S <= cap, with at most 512 staged cells (rows x columns), the capacity of the
 // threads' prefetch registers.
@@ -564,10 +542,10 @@ int small_conv_pool_backward_weight(axis_device device, const SmallConvShape &s,
                                                                                           partial.as<float>());
         if (int st = launch_status("small_conv_pool_wgrad_kernel")) return st;
     }
-    const int32_t outputs = (a.k + (d_bias ? 1 : 0)) * a.n;
-    small_conv_combine_kernel<<<outputs, 256, 0, device->stream>>>(partial.as<float>(), (int32_t)blocks, a.n, a.k,
-                                                                   d_weight, d_bias);
-    return launch_status("small_conv_combine_kernel");
+    // d_weight[t][n] (t < k) and d_bias[n] (t = k) = the sum over blocks of partial[block][t][n]
+    const int64_t outputs = (int64_t)(a.k + (d_bias ? 1 : 0)) * a.n;
+    return column_block_sum(device->stream, partial.as<float>(), blocks, outputs, 32 * (int64_t)a.n,
+                            (int64_t)a.k * a.n, d_weight, d_bias);
 }
 
 }  // namespace axis

@@ -171,7 +171,7 @@ __global__ void __launch_bounds__(256) relu_pool_backward_kernel(
 // The same scatter with the bias gradient folded in.  A block walks a contiguous range of pooled
 // vectors with stride 256, so a lane keeps one channel vector (256 is a multiple of the vector
 // count per pixel) and sums the terms it writes; a fixed-order block reduction leaves one partial
-// per block and channel, summed afterwards by relu_pool_bias_combine_kernel in a fixed tree.  The
+// per block and channel, summed afterwards in a fixed order (axis::column_block_sum).  The
 // association differs from the reference's 512-row chunks (fp32 tolerance, not bit equality) but
 // is the same on every run.
 template <int VEC>
@@ -225,24 +225,6 @@ __global__ void __launch_bounds__(256) relu_pool_backward_bias_kernel(
         for (int l = cv; l < 256; l += per_pixel) sum += lane_sum[l][e];
         partial[(int64_t)blockIdx.x * a.channels + c] = sum;
     }
-}
-
-// d_bias[c] = sum over blocks of partial[b][c]: lanes add strided blocks in order, then a fixed
-// pairwise tree over the 256 lane sums.
-__global__ void __launch_bounds__(256) relu_pool_bias_combine_kernel(const float *__restrict__ partial,
-                                                                     int32_t blocks, int32_t channels,
-                                                                     float *__restrict__ out) {
-    __shared__ float s[256];
-    const int c = blockIdx.x;
-    float v = 0.0f;
-    for (int b = threadIdx.x; b < blocks; b += 256) v += partial[(int64_t)b * channels + c];
-    s[threadIdx.x] = v;
-    __syncthreads();
-    for (int half = 128; half > 0; half >>= 1) {
-        if ((int)threadIdx.x < half) s[threadIdx.x] = s[threadIdx.x] + s[threadIdx.x + half];
-        __syncthreads();
-    }
-    if (threadIdx.x == 0) out[c] = s[0];
 }
 
 // Bias-gradient chunks of the same d_pre without reading it: partial[q][c] sums rows
@@ -451,9 +433,8 @@ int axis_relu_pool_backward(axis_device device, const float *gradient, const flo
             relu_pool_backward_bias_kernel<1><<<nb, 256, 0, device->stream>>>(gradient, pooled, argmax, d_pre,
                                                                             partial.as<float>(), span, a);
         if (int s = axis::launch_status("relu_pool_backward_bias_kernel")) return s;
-        relu_pool_bias_combine_kernel<<<(unsigned)channels, 256, 0, device->stream>>>(partial.as<float>(), nb,
-                                                                                     channels, d_bias);
-        return axis::launch_status("relu_pool_bias_combine_kernel");
+        return axis::column_block_sum(device->stream, partial.as<float>(), nb, channels, channels, channels, d_bias,
+                                      nullptr);
     }
     if (vec)
         relu_pool_backward_kernel<4><<<axis::blocks_for(a.total, 256, INT32_MAX), 256, 0, device->stream>>>(

@@ -304,6 +304,25 @@ def build_mlp(ax, device, batch, sizes):
     return model, bt, feats
 
 
+def check_first_adam_step(oracle, name, v, g, p0, g_ref, p_ref, lr=1e-3):
+    """Parameters v after one Adam(lr) step from p0 with our gradients g, against the oracle's whole
+    step (p_ref from its gradients g_ref)."""
+    # The update is the reference's Adam arithmetic, bit for bit, given these gradients.
+    c1, c2 = 1 - oracle.powi(0.9, 1), 1 - oracle.powi(0.999, 1)
+    zero = np.zeros_like(p0)
+    exact = oracle.adam(p0, g, zero, zero, lr, 0.9, 0.999, c1, c2, 1e-8, 0.0)[0]
+    assert np.array_equal(v, exact), name
+    # Against the whole oracle step: Adam's first update is lr * g / (|g| + eps), which turns a
+    # rounding difference in a gradient element that nearly cancels into an O(lr) step difference;
+    # compare every element whose gradient agrees with the oracle's to 1% at 1e-5, and bound the
+    # rest by the largest possible first step.
+    gr = np.asarray(g_ref, np.float64)
+    sure = (np.abs(gr) >= 100.0 * np.abs(np.asarray(g, np.float64) - gr)) & (np.abs(gr) >= 1e-5)
+    assert sure.any(), name
+    assert rel_max(v[sure], p_ref[sure]) < 1e-5, name
+    assert np.abs(v - p_ref).max() <= 2.0 * lr * 1.0001, name
+
+
 def test_mlp_config1_step_matches_oracle(ax, device, oracle):
     sizes, batch = (784, 256, 256, 10), 128
     ref = oracle.mlp_step(batch, sizes)
@@ -325,7 +344,7 @@ def test_mlp_config1_step_matches_oracle(ax, device, oracle):
             g = grads[f"{2 * j}.{kind}"]
             assert rel_max(g, ref["grads"][key]) < 1e-4, (key, rel_max(g, ref["grads"][key]))
             v = model.parameter(f"{2 * j}.{kind}").tensor().to_vec()
-            assert rel_max(v, ref["params"][key]) < 1e-5, (key, rel_max(v, ref["params"][key]))
+            check_first_adam_step(oracle, key, v, g, ref["initial"][key], ref["grads"][key], ref["params"][key])
 
 
 def build_cnn(ax, device, batch, size, classes, ch):
@@ -371,25 +390,12 @@ def test_cnn_small_batch_step_matches_oracle(ax, device, oracle):
     assert abs(loss.item() - ref["loss"]) <= 1e-5 * max(1, abs(ref["loss"]))
     grads = {ours: model.parameter(ours).grad().to_vec() for ours in mapping}
     ax.Adam(1e-3).step(model)
-    c1, c2 = 1 - oracle.powi(0.9, 1), 1 - oracle.powi(0.999, 1)
     for ours, theirs in mapping.items():
         g = grads[ours]
         assert rel_max(g, ref["grads"][theirs]) < 1e-4, (theirs, rel_max(g, ref["grads"][theirs]))
         v = model.parameter(ours).tensor().to_vec()
-        # The update is the reference's Adam arithmetic, bit for bit, given these gradients.
-        p0 = ref["initial"][theirs]
-        zero = np.zeros_like(p0)
-        exact = oracle.adam(p0, g, zero, zero, 1e-3, 0.9, 0.999, c1, c2, 1e-8, 0.0)[0]
-        assert np.array_equal(v, exact), theirs
-        # Against the whole oracle step: Adam's first update is lr * g / (|g| + eps), which turns a
-        # rounding difference in a gradient element that nearly cancels into an O(lr) step
-        # difference; compare every element whose gradient agrees with the oracle's to 1%, and
-        # bound the rest by the largest possible first step.
-        gr = np.asarray(ref["grads"][theirs], np.float64)
-        sure = (np.abs(gr) >= 100.0 * np.abs(np.asarray(g, np.float64) - gr)) & (np.abs(gr) >= 1e-5)
-        assert sure.any(), theirs
-        assert rel_max(v[sure], ref["params"][theirs][sure]) < 1e-5, theirs
-        assert np.abs(v - ref["params"][theirs]).max() <= 2.0 * 1e-3 * 1.0001, theirs
+        check_first_adam_step(oracle, theirs, v, g, ref["initial"][theirs], ref["grads"][theirs],
+                              ref["params"][theirs])
 
 
 def test_cnn_full_config_invariants(ax, device, oracle):
