@@ -178,13 +178,17 @@ __global__ void __launch_bounds__(256, 4) small_conv_forward_kernel(SmallConvArg
             for (int b = 0; b < 2; ++b)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) acc[b][v] = 0.0f;
+            // every A operand of the tile is read before the MFMA chain starts (one LDS wait, not
+            // one per k-pair)
+            float av[KP];
 #pragma unroll
-            for (int j = 0; j < KP; ++j) {
-                const float av = px0[off[j]];
+            for (int j = 0; j < KP; ++j) av[j] = px0[off[j]];
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < KP; ++j)
 #pragma unroll
                 for (int b = 0; b < 2; ++b)
-                    acc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, wreg[j][b], acc[b], 0, 0, 0);
-            }
+                    acc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[j], wreg[j][b], acc[b], 0, 0, 0);
             if (!col_ok[0]) continue;
             // Accumulator register v: row i = 8*(v/4) + 4*half + v%4, i.e. window
             // tile*8 + 2*(v/4) + half, position v%4.
@@ -363,18 +367,30 @@ __global__ void __launch_bounds__(256, 4) small_conv_pool_wgrad_kernel(SmallConv
             load_grad(a, next, tid, col0, g, pooled, argmax, gpre);
         }
         __syncthreads();
-        for (int32_t wi = wave; wi < band_windows; wi += 4) {
-            const int32_t wr = (int32_t)a.s_div.div((uint32_t)wi);
-            const int32_t wc = wi - wr * a.band_s;
-            const float *pw = strip + 2 * wr * a.strip_w + 2 * wc;
-            const float x0 = pw[xoff[0]], x1 = pw[xoff[1]];
-            const float *dyw = dy + wi * 256;
+        // Windows wi and wi + 4 per pass (band_windows is a multiple of 8): both windows' operands
+        // are read before their 16 MFMAs issue.
+        for (int32_t wi = wave; wi < band_windows; wi += 8) {
+            float x[2][2], d[2][4];
 #pragma unroll
-            for (int nb = 0; nb < 4; ++nb) {
-                const float d = dyw[doff[nb]];
-                acc[nb][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(d, x0, acc[nb][0], 0, 0, 0);
-                acc[nb][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(d, x1, acc[nb][1], 0, 0, 0);
+            for (int h = 0; h < 2; ++h) {
+                const int32_t w = wi + 4 * h;
+                const int32_t wr = (int32_t)a.s_div.div((uint32_t)w);
+                const int32_t wc = w - wr * a.band_s;
+                const float *pw = strip + 2 * wr * a.strip_w + 2 * wc;
+                x[h][0] = pw[xoff[0]];
+                x[h][1] = pw[xoff[1]];
+                const float *dyw = dy + w * 256;
+#pragma unroll
+                for (int nb = 0; nb < 4; ++nb) d[h][nb] = dyw[doff[nb]];
             }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int nb = 0; nb < 4; ++nb) {
+                    acc[nb][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(d[h][nb], x[h][0], acc[nb][0], 0, 0, 0);
+                    acc[nb][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(d[h][nb], x[h][1], acc[nb][1], 0, 0, 0);
+                }
         }
     }
     // The four waves' sums meet in LDS ([wave][term][64 columns], over the gradient expansion) and
