@@ -308,9 +308,11 @@ struct ConvRowsBufferLoader : Staging<BT, BK, NT, true, VEC> {
     uint32_t origin[S::kVecs];   // b*ld_b + iy0*ld_h + ix0*ld_w (mod 2^32; exact when valid)
     uint32_t inside[S::kVecs];   // taps of the row's window inside the image (0 for rows past the end)
     int rr;
+    uint32_t lane_c;             // rr * ld_c: the thread's channel offset inside a tap step
 
     __device__ __forceinline__ void init(const ConvGeom &geom, int64_t t0, int64_t t_end, int tid) {
         rr = (tid % S::kPer) * VEC;
+        lane_c = (uint32_t)(rr * geom.ld_c);
 #pragma unroll
         for (int e = 0; e < S::kVecs; ++e) {
             const int64_t gt = tile_pixel(geom, t0, (tid + e * NT) / S::kPer);
@@ -337,11 +339,15 @@ struct ConvRowsBufferLoader : Staging<BT, BK, NT, true, VEC> {
         bool r_ok;
         if (geom.tap_steps) {
             // r_end is a multiple of BK here, so every k of the step is inside the reduction
+            // the step's tap and first channel are wave-uniform: scalar arithmetic, plus the
+            // thread's fixed channel offset
             pos = geom.c_div.div((uint32_t)r0);
             const int32_t c0 = (int32_t)((uint32_t)r0 - pos * (uint32_t)geom.channels);
             const int32_t ky = (int32_t)geom.kw_div.div(pos);
             const int32_t kx = (int32_t)pos - ky * geom.kw;
-            delta = (uint32_t)(ky * geom.ld_h + kx * geom.ld_w + (c0 + rr) * geom.ld_c);
+            delta = __builtin_amdgcn_readfirstlane((uint32_t)(ky * geom.ld_h + kx * geom.ld_w + c0 * geom.ld_c)) +
+                    lane_c;
+            pos = __builtin_amdgcn_readfirstlane(pos);
             r_ok = true;
         } else {
             const int64_t gr = r0 + rr;
