@@ -576,6 +576,88 @@ int dense_order(int32_t rank, const int64_t *extents, const int64_t *strides, in
     return AXIS_OK;
 }
 
+// ---------------------------------------------------------------- extreme over one axis
+
+// Tensor::min over one axis (tensor.rs:2880-2946: grouped_minimum over a forward plan that lists
+// each output's members in increasing coordinate along the axis, then the winner mask over the
+// gather plan, backend.rs:1365-1440, kernels :3019-3116) without the plans.  A thread per output:
+// the first strictly better FINITE value in axis order wins; NaN and an all-zero mask when none is
+// finite.  Outputs are row-major over the kept dims in dim order.
+struct ExtremeAxisArgs {
+    int32_t kept_rank;
+    FastDiv kept_place[kMaxReduceDims], kept_extent[kMaxReduceDims];
+    int64_t kept_src[kMaxReduceDims];
+    int64_t axis_extent, axis_stride, outputs;
+};
+
+__device__ __forceinline__ int64_t extreme_base(const ExtremeAxisArgs &x, int64_t o) {
+    int64_t off = 0;
+    for (int d = 0; d < x.kept_rank; ++d)
+        off += (int64_t)x.kept_extent[d].mod(x.kept_place[d].div((uint32_t)o)) * x.kept_src[d];
+    return off;
+}
+
+template <bool MAXIMUM>
+__global__ void __launch_bounds__(kBlock) extreme_axis_kernel(const float *__restrict__ a, float *__restrict__ out,
+                                                              float *__restrict__ mask, ExtremeAxisArgs x) {
+    const int64_t o = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (o >= x.outputs) return;
+    const int64_t base = extreme_base(x, o);
+    float best = MAXIMUM ? -INFINITY : INFINITY;
+    int64_t winner = -1;
+    for (int64_t c = 0; c < x.axis_extent; ++c) {
+        const float v = a[base + c * x.axis_stride];
+        const bool finite = v >= -FLT_MAX && v <= FLT_MAX;
+        if (finite && (MAXIMUM ? v > best : v < best)) {
+            best = v;
+            winner = c;
+        }
+    }
+    out[o] = winner >= 0 ? best : __builtin_nanf("");
+    for (int64_t c = 0; c < x.axis_extent; ++c) mask[base + c * x.axis_stride] = c == winner ? 1.0f : 0.0f;
+}
+
+// Its backward (Rule::Minimum, tensor.rs:5679-5683): the gather plan's grouped sum gives every
+// member (0 + g) * 1 of its output, and mask_gradient keeps it at the winner.
+__global__ void __launch_bounds__(kBlock) extreme_axis_backward_kernel(const float *__restrict__ g,
+                                                                       const float *__restrict__ mask,
+                                                                       float *__restrict__ out, ExtremeAxisArgs x) {
+    const int64_t o = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (o >= x.outputs) return;
+    const int64_t base = extreme_base(x, o);
+    const float expanded = (0.0f + g[o]) * 1.0f;
+    for (int64_t c = 0; c < x.axis_extent; ++c) {
+        const int64_t at = base + c * x.axis_stride;
+        out[at] = mask[at] > 0.0f ? expanded : 0.0f;
+    }
+}
+
+int extreme_axis_args(int32_t rank, const int64_t *extents, const int64_t *strides, int32_t axis,
+                      ExtremeAxisArgs &x) {
+    int order[kMaxReduceDims];
+    int64_t len = 0;
+    if (int st = dense_order(rank, extents, strides, order, &len)) return st;
+    AXIS_REQUIRE(axis >= 0 && axis < rank, "extreme_axis axis out of range");
+    x = ExtremeAxisArgs{};
+    x.axis_extent = extents[axis];
+    x.axis_stride = strides[axis];
+    x.outputs = len / extents[axis];
+    int64_t place = 1;
+    int kr = 0;
+    int kept[kMaxReduceDims];
+    for (int d = 0; d < rank; ++d)
+        if (d != axis) kept[kr++] = d;
+    x.kept_rank = kr;
+    for (int i = kr - 1; i >= 0; --i) {
+        const int d = kept[i];
+        x.kept_place[i] = FastDiv((uint32_t)place);
+        x.kept_extent[i] = FastDiv((uint32_t)extents[d]);
+        x.kept_src[i] = strides[d];
+        place *= extents[d];
+    }
+    return AXIS_OK;
+}
+
 struct BroadcastMiddle {
     const float *g;
     float *out;
@@ -849,6 +931,31 @@ int axis_reduce_axes_backward(axis_device device, const float *gradient, float *
     b.rank = rank;
     broadcast_axes_kernel<<<axis::blocks_for(len, kBlock, INT32_MAX), kBlock, 0, device->stream>>>(gradient, out, b);
     return axis::launch_status("broadcast_axes_kernel");
+}
+
+int axis_extreme_axis(axis_device device, const float *a, int32_t rank, const int64_t *extents,
+                      const int64_t *strides, int32_t axis, int32_t maximum, float *out, float *winner_mask) {
+    AXIS_ENTER(device);
+    AXIS_REQUIRE(a && out && winner_mask, "null extreme_axis buffer");
+    ExtremeAxisArgs x;
+    if (int st = extreme_axis_args(rank, extents, strides, axis, x)) return st;
+    const unsigned blocks = axis::blocks_for(x.outputs, kBlock, INT32_MAX);
+    if (maximum)
+        extreme_axis_kernel<true><<<blocks, kBlock, 0, device->stream>>>(a, out, winner_mask, x);
+    else
+        extreme_axis_kernel<false><<<blocks, kBlock, 0, device->stream>>>(a, out, winner_mask, x);
+    return axis::launch_status("extreme_axis_kernel");
+}
+
+int axis_extreme_axis_backward(axis_device device, const float *gradient, const float *winner_mask, int32_t rank,
+                               const int64_t *extents, const int64_t *strides, int32_t axis, float *out) {
+    AXIS_ENTER(device);
+    AXIS_REQUIRE(gradient && winner_mask && out, "null extreme_axis_backward buffer");
+    ExtremeAxisArgs x;
+    if (int st = extreme_axis_args(rank, extents, strides, axis, x)) return st;
+    extreme_axis_backward_kernel<<<axis::blocks_for(x.outputs, kBlock, INT32_MAX), kBlock, 0, device->stream>>>(
+        gradient, winner_mask, out, x);
+    return axis::launch_status("extreme_axis_backward_kernel");
 }
 
 int axis_broadcast_middle(axis_device device, const float *gradient, float *out, int64_t outer,

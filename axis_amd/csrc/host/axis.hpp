@@ -191,6 +191,8 @@ struct Rule {
         ConvWeight,  // weight gradient of an implicit-GEMM convolution (a = input)
         ReluPool,    // ReLU then non-overlapping max pool (a = argmax bytes, b = pooled values)
         ReduceAxes,  // sum over any axis set (extents/strides of the input, metadata = reduced flags)
+        BroadcastAxes,  // broadcast into new axes (extents/strides of the output, metadata = new-axis flags)
+        MinimumAxis,    // min over one axis without plans (a = winner mask; input geometry; metadata = {axis})
     } kind = Identity;
     float factor = 1.0f;
     Buffer a, b;  // saved operands (rhs / lhs / probability / input / winners / argmax)

@@ -317,10 +317,25 @@ Tensor Tensor::align(const Shape &target) const {
     std::vector<Edge> edges;
     if (requires_grad()) {
         int64_t width = trailing_broadcast(*this, target);
+        bool in_order = is_contiguous();
+        for (size_t own = 1; own < positions.size() && in_order; ++own) in_order = positions[own] > positions[own - 1];
         if (width > 0) {
             Rule rb = rule(Rule::BiasBroadcast);
             rb.outer = target.len / width;
             rb.inner = width;
+            edges.push_back(Edge{*this, rb});
+        } else if (in_order) {
+            // The reverse plan sums each input element's copies in increasing output position
+            // (tensor.rs:679-698, Plan::reverse); with the input's axes in the output's order and
+            // contiguous, that is the strided reduction over the new axes, without the plan.
+            Rule rb = rule(Rule::BroadcastAxes);
+            for (size_t index = 0; index < target.rank(); ++index) {
+                rb.extents.push_back(target.dims[index].extent);
+                rb.strides.push_back(layout.strides[index]);
+                bool own = false;
+                for (size_t p : positions) own = own || p == index;
+                rb.metadata.push_back(own ? 0 : 1);
+            }
             edges.push_back(Edge{*this, rb});
         } else {
             // align_reverse_plan (tensor.rs:679-698)
@@ -567,6 +582,24 @@ Tensor Tensor::min(const Axis &axis) const {
     for (auto &d : shape().dims)
         if (d.axis != axis) out_dims.push_back(d);
     Shape out_shape = Shape::make(out_dims);
+    if (shape().len <= (int64_t)INT32_MAX - 256) {
+        // The plans' order (each output's members by increasing coordinate along the axis) walked
+        // through the strides: no element-sized plan and no 16,777,216 cap.
+        Rule r = rule(Rule::MinimumAxis);
+        for (size_t i = 0; i < shape().rank(); ++i) {
+            r.extents.push_back(shape().dims[i].extent);
+            r.strides.push_back(layout().strides[i]);
+        }
+        r.metadata.push_back((int32_t)reduced);
+        Buffer value = device().alloc(out_shape.len);
+        r.a = device().alloc(shape().len);
+        check(axis_extreme_axis(device().h(), this->value()->f32(), (int32_t)shape().rank(), r.extents.data(),
+                                r.strides.data(), (int32_t)reduced, 0, value->f32(), r.a->f32()),
+              "min");
+        Tensor out = node(out_shape, Layout::contiguous(out_shape), value, device(), one_edge(*this, r), false);
+        profile("min", started);
+        return out;
+    }
     std::vector<int64_t> map((size_t)shape().len);
     HostPlan forward;
     check_plan_size(shape().len);
@@ -977,6 +1010,25 @@ void Tensor::backward() const {
                                                     r.extents.data(), r.strides.data(), r.metadata.data(),
                                                     r.factor),
                           "reduce_axes_backward");
+                    break;
+                }
+                case Rule::BroadcastAxes: {
+                    int64_t len = 1;
+                    for (size_t d = 0; d < r.extents.size(); ++d)
+                        if (!r.metadata[d]) len *= r.extents[d];
+                    c = dev.alloc(len);
+                    check(axis_reduce_axes(dev.h(), g->f32(), c->f32(), (int32_t)r.extents.size(), r.extents.data(),
+                                           r.strides.data(), r.metadata.data(), 1.0f),
+                          "align_backward");
+                    break;
+                }
+                case Rule::MinimumAxis: {
+                    int64_t len = 1;
+                    for (int64_t e : r.extents) len *= e;
+                    c = dev.alloc(len);
+                    check(axis_extreme_axis_backward(dev.h(), g->f32(), r.a->f32(), (int32_t)r.extents.size(),
+                                                     r.extents.data(), r.strides.data(), r.metadata[0], c->f32()),
+                          "min_backward");
                     break;
                 }
                 case Rule::MeanMiddle:

@@ -275,6 +275,19 @@ int axis_reduce_axes(axis_device device, const float *a, float *out, int32_t ran
 int axis_reduce_axes_backward(axis_device device, const float *gradient, float *out, int32_t rank,
                               const int64_t *extents, const int64_t *strides, const int32_t *reduced,
                               float factor);
+/* Tensor::min / max over one axis (tensor.rs:2880-2946: Device::grouped_minimum over the forward
+ * plan, then the winner mask over the gather plan, backend.rs:1365-1440, kernels :3019-3116)
+ * without the plans, so without their 16,777,216 cap.  The tensor is dense (rank <= 10 dims with
+ * the given extents and element strides); out is row-major over the other dims in dim order and
+ * holds the first strictly smaller (maximum != 0: greater) FINITE value along `axis`, NaN when
+ * none is finite; winner_mask (laid out like the input) is 1 at each output's winner, else 0 --
+ * bit-identical to axis_grouped_minimum/maximum over the reference's plans. */
+int axis_extreme_axis(axis_device device, const float *a, int32_t rank, const int64_t *extents,
+                      const int64_t *strides, int32_t axis, int32_t maximum, float *out, float *winner_mask);
+/* Its backward (Rule::Minimum, tensor.rs:5679-5683: grouped over the gather plan, then
+ * mask_gradient): out, laid out like the input, is 0 + gradient[output] at each winner, else 0. */
+int axis_extreme_axis_backward(axis_device device, const float *gradient, const float *winner_mask, int32_t rank,
+                               const int64_t *extents, const int64_t *strides, int32_t axis, float *out);
 /* Its Group-rule backward: out[o][r][i] = factor * gradient[o][i]. */
 int axis_broadcast_middle(axis_device device, const float *gradient, float *out, int64_t outer,
                           int64_t reduce, int64_t inner, float factor);

@@ -228,6 +228,35 @@ def test_reduce_past_the_plan_cap(ax, device):
     close("mean", r.to_vec(), expect.reshape(-1))
 
 
+@pytest.mark.parametrize("extents", [(3, 700, 5), (17, 2048, 512)])
+def test_align_backward_without_plan(ax, device, oracle, extents):
+    """A [a, c] operand broadcast over a middle axis: its gradient is the reverse plan's grouped sum
+    (tensor.rs:679-698), taken by the strided reduction -- bit-identical, and past the plan's
+    16,777,216 cap for the second shape."""
+    A, B, C = extents
+    a, b, c = ax.Axis("a"), ax.Axis("b"), ax.Axis("c")
+    rng = np.random.default_rng(A)
+    n = A * B * C
+    xv = rng.standard_normal(n).astype(np.float32)
+    wv = rng.standard_normal(n).astype(np.float32)
+    tv = rng.standard_normal(A * C).astype(np.float32)
+    x = ax.Tensor.from_slice(xv, [a.of(A), b.of(B), c.of(C)], device)
+    w = ax.Tensor.from_slice(wv, [a.of(A), b.of(B), c.of(C)], device)
+    t = ax.Tensor.from_slice(tv, [a.of(A), c.of(C)], device).with_grad()
+    y = x.add(t)
+    close("broadcast add", y.to_vec(), (xv.reshape(A, B, C) + tv.reshape(A, 1, C)).reshape(-1))
+    y.mul(w).sum([a, b, c]).backward()
+    got = t.grad().to_vec()
+    if n <= 16777216:
+        small = [("a", A), ("c", C)]
+        rev = oracle.align_reverse_plan(small, oracle.contiguous(small), [("a", A), ("b", B), ("c", C)])
+        assert np.array_equal(got, oracle.grouped(wv, None, rev, 1.0))
+    else:
+        # a 2048-term fp32 sum against float64
+        close("broadcast gradient", got, wv.reshape(A, B, C).astype(np.float64).sum(axis=1).reshape(-1),
+              atol=5e-4, rtol=1e-5)
+
+
 def test_normalized_l2_fixture(ax, device):
     # model/optim.rs:1492-1503
     v = ax.Axis("value")

@@ -480,6 +480,66 @@ def test_reduce_axes_bit_exact(dev, oracle, dims, order, axes, mean):
     assert np.array_equal(dev.read(back, n), oracle.grouped(got, None, rev, factor))
 
 
+EXTREME_AXIS_CASES = [
+    # dims, physical order, axis
+    ([("g", 6), ("w", 4)], ["g", "w"], "w"),
+    ([("a", 3), ("b", 5), ("c", 7)], ["c", "a", "b"], "b"),
+    ([("n", 2), ("oh", 5), ("ow", 5), ("ch", 3), ("win", 9)], ["n", "ch", "oh", "ow", "win"], "win"),
+    ([("n", 2), ("oh", 4), ("ow", 4), ("ch", 8), ("win", 4)], ["win", "n", "oh", "ow", "ch"], "win"),
+    ([("x", 1), ("y", 700)], ["y", "x"], "y"),
+]
+
+
+@pytest.mark.parametrize("dims,order,axis", EXTREME_AXIS_CASES)
+@pytest.mark.parametrize("maximum", [False, True])
+def test_extreme_axis_matches_plan_reductions(dev, oracle, dims, order, axis, maximum):
+    rng = np.random.default_rng(len(dims) * 7 + int(maximum))
+    n = int(np.prod([e for _, e in dims]))
+    a = np.round(rng.standard_normal(n) * 4).astype(np.float32) / 4  # physical storage, many ties
+    a[::11] = np.inf
+    a[::13] = -np.inf
+    a[::17] = np.nan
+    strides = oracle.layout_for(dims, order)
+    out_dims, fwd, rev = oracle.min_plans(dims, strides, axis)
+    olen = int(np.prod([e for _, e in out_dims]))
+    ref, ref_mask, _ = oracle.grouped_minimum(a, fwd, rev, maximum)
+    ext = np.array([e for _, e in dims], np.int64)
+    st = np.array(strides, np.int64)
+    ax = [name for name, _ in dims].index(axis)
+    geo = (I32(len(dims)), ext.ctypes.data_as(VP), st.ctypes.data_as(VP), I32(ax))
+    da, out, mask = up(dev, a), dev.empty(olen), dev.empty(n)
+    dev.call("axis_extreme_axis", da.vp, *geo, I32(1 if maximum else 0), out.vp, mask.vp)
+    got, got_mask = dev.read(out, olen), dev.read(mask, n)
+    assert np.array_equal(np.isnan(got), np.isnan(ref)) and np.array_equal(got[~np.isnan(ref)], ref[~np.isnan(ref)])
+    assert np.array_equal(got_mask, ref_mask)
+    # backward: the gather plan's grouped sum, then mask_gradient
+    g = rng.standard_normal(olen).astype(np.float32)
+    g[::5] = -0.0
+    dg, back = up(dev, g), dev.empty(n)
+    dev.call("axis_extreme_axis_backward", dg.vp, mask.vp, *geo, back.vp)
+    expect = oracle.mask_gradient(oracle.grouped(g, None, rev, 1.0), ref_mask)
+    assert np.array_equal(dev.read(back, n).view(np.uint32), expect.view(np.uint32))
+
+
+def test_extreme_axis_past_the_plan_cap(dev, oracle):
+    # a [batch, 32, 32, 64, window 9] unfolded pool input: 18.9M members, past the plan cap
+    dims = [("n", 32), ("oh", 32), ("ow", 32), ("ch", 64), ("win", 9)]
+    strides = oracle.contiguous(dims)
+    n = int(np.prod([e for _, e in dims]))
+    assert n > 16777216
+    rng = np.random.default_rng(5)
+    a = rng.standard_normal(n).astype(np.float32)
+    ext = np.array([e for _, e in dims], np.int64)
+    st = np.array(strides, np.int64)
+    geo = (I32(len(dims)), ext.ctypes.data_as(VP), st.ctypes.data_as(VP), I32(4))
+    da, out, mask = up(dev, a), dev.empty(n // 9), dev.empty(n)
+    dev.call("axis_extreme_axis", da.vp, *geo, I32(0), out.vp, mask.vp)
+    windows = a.reshape(-1, 9)
+    assert np.array_equal(dev.read(out, n // 9), windows.min(axis=1))
+    m = dev.read(mask, n).reshape(-1, 9)
+    assert np.array_equal(np.argmax(m, axis=1), np.argmin(windows, axis=1)) and np.all(m.sum(axis=1) == 1)
+
+
 def test_reduce_axes_past_the_plan_cap(dev, oracle):
     """A mean over two non-adjacent axes of 2^24 + 2^20 elements: past the reference's 16,777,216
     contribution cap, still in the reverse plan's order (plan built uncapped on the host)."""
