@@ -26,6 +26,9 @@ struct axis_device_s {
     size_t in_use = 0;
     size_t cached = 0;
     int multiprocessors = 256;
+    // Device::cuda_bf16 (backend.rs:274-283): matrix products take bf16-rounded operands and
+    // accumulate in fp32; everything else stays fp32.
+    bool bf16_matmul = false;
     // launch timing (axis_timing_*): event pairs and work per family
     bool timing = false;
     struct Timed {

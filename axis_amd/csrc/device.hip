@@ -175,6 +175,19 @@ int axis_device_create(int ordinal, axis_device *out) {
     return AXIS_OK;
 }
 
+int axis_device_create_bf16(int ordinal, axis_device *out) {
+    if (int st = axis_device_create(ordinal, out)) return st;
+    (*out)->bf16_matmul = true;
+    return AXIS_OK;
+}
+
+int axis_device_bf16_matmul(axis_device device, int *enabled) {
+    AXIS_ENTER(device);
+    AXIS_REQUIRE(enabled, "null output");
+    *enabled = device->bf16_matmul ? 1 : 0;
+    return AXIS_OK;
+}
+
 int axis_device_destroy(axis_device device) {
     AXIS_ENTER(device);
     AXIS_HIP(hipStreamSynchronize(device->stream));

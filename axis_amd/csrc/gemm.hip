@@ -31,6 +31,7 @@
 #include <type_traits>
 
 #include "common.hpp"
+#include "bf16.hpp"
 #include "conv_small.hpp"
 #include "fastdiv.hpp"
 #include "pool_rule.hpp"
@@ -103,6 +104,7 @@ struct GemmParams {
     // Output rows ordered (pos, c) with perm_c channels and perm_taps taps are written as rows
     // c * perm_taps + pos (the reference's weight layout); 0 = rows as computed.
     int32_t perm_c, perm_taps;
+    bool bf16;                 // operands rounded to bf16 as they are staged (Device::cuda_bf16)
 };
 
 template <int VEC>
@@ -155,7 +157,12 @@ struct Staging {
     static constexpr int kPer = RCONTIG ? BK / VEC : BT / VEC;  // vectors per contiguous line
     float reg[kElems];
 
-    __device__ __forceinline__ void store(float *__restrict__ lds, int tid) const {
+    // bf16: round every staged operand to bf16 first (products of bf16 values are exact in fp32).
+    __device__ __forceinline__ void store(float *__restrict__ lds, int tid, bool bf16 = false) {
+        if (bf16) {
+#pragma unroll
+            for (int e = 0; e < kElems; ++e) reg[e] = bf16_round(reg[e]);
+        }
 #pragma unroll
         for (int e = 0; e < kVecs; ++e) {
             const int idx = tid + e * NT;
@@ -581,8 +588,8 @@ __global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
     if (r_begin < r_end) {
         lx.load(p.conv, r_begin, r_end, tid);
         ly.load(p.conv, r_begin, r_end, tid);
-        lx.store(xs, tid);
-        ly.store(ys, tid);
+        lx.store(xs, tid, p.bf16);
+        ly.store(ys, tid, p.bf16);
     }
     __syncthreads();
 
@@ -635,8 +642,8 @@ __global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
         }
         __syncthreads();
         if (more) {
-            lx.store(xs, tid);
-            ly.store(ys, tid);
+            lx.store(xs, tid, p.bf16);
+            ly.store(ys, tid, p.bf16);
             __syncthreads();
         }
     }
@@ -989,6 +996,7 @@ int sum_splits(axis_device device, const float *partial, float *out, int64_t len
 
 template <bool XR, bool YR, int XMODE, int EPI>
 int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out) {
+    p.bf16 = device->bf16_matmul;
     const int64_t cus = device->multiprocessors;
     const Choice ch = choose(p.m, p.n, p.k, batch, cus, EPI == 1);
     const int BK = ch.bk;
@@ -1352,7 +1360,7 @@ int axis_conv2d_forward(axis_device device, const float *input, const int64_t in
     ConvShape s{};
     if (int st = conv_shape(batch, height, width, channels, out_channels, kernel, stride, padding, &s))
         return st;
-    if (axis::small_conv_applies(small_shape(s))) {
+    if (!device->bf16_matmul && axis::small_conv_applies(small_shape(s))) {
         int64_t ld[4];
         if (int st = input_strides(input_strides_, batch, height, width, channels, ld)) return st;
         return axis::small_conv_forward(device, small_shape(s), input, ld, weight, bias, out, nullptr, nullptr);
@@ -1391,7 +1399,7 @@ int axis_conv2d_relu_pool_forward(axis_device device, const float *input,
                  "pool window must be positive with fewer than 255 positions");
     AXIS_REQUIRE(s.out_h % pool[0] == 0 && s.out_w % pool[1] == 0,
                  "fused pooling needs windows that tile the convolution output exactly");
-    if (pool[0] == 2 && pool[1] == 2 && axis::small_conv_applies(small_shape(s)))
+    if (pool[0] == 2 && pool[1] == 2 && !device->bf16_matmul && axis::small_conv_applies(small_shape(s)))
         return axis::small_conv_forward(device, small_shape(s), input, ld_check, weight, bias, nullptr, pooled,
                                         argmax);
     AXIS_REQUIRE(128 % (pool[0] * s.out_w) == 0,
@@ -1517,7 +1525,7 @@ int axis_conv2d_relu_pool_backward_weight(axis_device device, const float *input
     AXIS_REQUIRE(pool[0] >= 1 && pool[1] >= 1 && pool[0] * pool[1] < 255 && s.out_h % pool[0] == 0 &&
                      s.out_w % pool[1] == 0,
                  "fused pooling needs windows that tile the convolution output exactly");
-    if (pool[0] == 2 && pool[1] == 2 && axis::small_conv_applies(small_shape(s)))
+    if (pool[0] == 2 && pool[1] == 2 && !device->bf16_matmul && axis::small_conv_applies(small_shape(s)))
         return axis::small_conv_pool_backward_weight(device, small_shape(s), input, ld, gradient, pooled, argmax,
                                                      d_weight, d_bias);
     // Any other shape: the pre-activation gradient through axis_relu_pool_backward, then the

@@ -122,6 +122,8 @@ class Device {
     std::shared_ptr<DeviceImpl> impl;
 
     static Device hip(int ordinal);
+    static Device hip_bf16(int ordinal);
+    bool bf16_matmul() const;
     bool same(const Device &o) const { return impl == o.impl; }
     axis_device h() const { return impl->handle; }
 

@@ -78,6 +78,8 @@ PYBIND11_MODULE(_axis, m) {
 
     py::class_<Device>(m, "Device")
         .def_static("hip", &Device::hip, py::arg("ordinal") = 0)
+        .def_static("hip_bf16", &Device::hip_bf16, py::arg("ordinal") = 0)
+        .def("bf16_matmul", &Device::bf16_matmul)
         .def("synchronize", &Device::synchronize)
         .def("same", &Device::same)
         .def("memory_stats", [](const Device &d) {

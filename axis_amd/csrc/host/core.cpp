@@ -155,6 +155,21 @@ Device Device::hip(int ordinal) {
     return d;
 }
 
+// Device::cuda_bf16 (backend.rs:274-283): bf16 operands, fp32 accumulation in matrix products.
+Device Device::hip_bf16(int ordinal) {
+    Device d;
+    d.impl = std::make_shared<DeviceImpl>();
+    d.impl->ordinal = ordinal;
+    check(axis_device_create_bf16(ordinal, &d.impl->handle), "Device::hip_bf16");
+    return d;
+}
+
+bool Device::bf16_matmul() const {
+    int enabled = 0;
+    check(axis_device_bf16_matmul(h(), &enabled), "Device::bf16_matmul");
+    return enabled != 0;
+}
+
 Buffer Device::alloc_bytes(int64_t bytes) const {
     auto b = std::make_shared<BufferImpl>();
     b->device = impl;

@@ -107,9 +107,10 @@ class Buffer:
 class Device:
     """One GPU, one stream, one caching allocator (axis_device)."""
 
-    def __init__(self, ordinal: int = 0):
+    def __init__(self, ordinal: int = 0, bf16_matmul: bool = False):
         h = ctypes.c_void_p()
-        check(load().axis_device_create(ordinal, ctypes.byref(h)), "axis_device_create")
+        create = "axis_device_create_bf16" if bf16_matmul else "axis_device_create"
+        check(getattr(load(), create)(ordinal, ctypes.byref(h)), create)
         self.handle = h
 
     def call(self, name: str, *args):

@@ -45,6 +45,13 @@ const char *axis_version(void);
 
 /* Device::cuda (backend.rs:268): bind GPU `ordinal`, create its stream and allocator. */
 int axis_device_create(int ordinal, axis_device *out);
+/* Device::cuda_bf16 (backend.rs:274-283): the same device with bf16 matrix products -- every
+ * matmul, matmul_left/right_backward and convolution product of this handle rounds its operands to
+ * bf16 (nearest, ties to even) and accumulates in fp32 (the operand conversion of matmul_bf16,
+ * :2209-2312); parameters, activations outside the products, optimizer state and reductions stay
+ * fp32.  axis_device_bf16_matmul reports the mode. */
+int axis_device_create_bf16(int ordinal, axis_device *out);
+int axis_device_bf16_matmul(axis_device device, int *enabled);
 int axis_device_destroy(axis_device device);
 /* Device::synchronize (backend.rs:352): wait for every launch on the stream. */
 int axis_device_synchronize(axis_device device);

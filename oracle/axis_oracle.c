@@ -86,6 +86,22 @@ float axo_powi(float base, int32_t exponent) {
 
 /* ---------------------------------------------------------------- contractions */
 
+/* runtime/backend.rs:2209-2312 (matmul_bf16 and its backward kernels): convert_tile of each fp32
+ * operand tile to bf16 before the mma -- round to nearest, ties to even, on the bit pattern; NaN
+ * stays a (quiet) NaN.  The result is returned widened back to fp32. */
+void axo_bf16_round(const float *a, int64_t len, float *out) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < len; ++i) {
+        uint32_t bits;
+        memcpy(&bits, &a[i], 4);
+        if ((bits & 0x7fffffffu) > 0x7f800000u)
+            bits = (bits | 0x00400000u) & 0xffff0000u;
+        else
+            bits = (bits + 0x7fffu + ((bits >> 16) & 1u)) & 0xffff0000u;
+        memcpy(&out[i], &bits, 4);
+    }
+}
+
 /* runtime/backend.rs:2190-2207: out[b] = a[b] . b[b], a [batch,m,k], b [batch,k,n].
  * fp64 accumulation (cuTile's mma order is not observable). */
 void axo_matmul(const float *a, const float *b, int64_t batch, int64_t m, int64_t k, int64_t n,

@@ -53,6 +53,7 @@ void axo_normal_host_values(uint64_t seed, int64_t count, float mean, float std,
 float axo_powi(float base, int32_t exponent);
 
 /* Contractions: runtime/backend.rs:934-1021 (kernels :2190-2290) */
+void axo_bf16_round(const float *a, int64_t len, float *out);
 void axo_matmul(const float *a, const float *b, int64_t batch, int64_t m, int64_t k, int64_t n, float *out);
 void axo_matmul_left_backward(const float *gradient, const float *rhs, int64_t batch, int64_t m,
                               int64_t k, int64_t n, float *out);

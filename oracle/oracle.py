@@ -139,6 +139,15 @@ def one_hot_labels(seed: int, rows: int, classes: int) -> tuple[np.ndarray, np.n
 
 # ------------------------------------------------------------------ contractions
 
+def bf16_round(a):
+    """fp32 -> bf16 (nearest, ties to even) -> fp32: the operand conversion of the reference's bf16
+    matrix products (backend.rs:2209-2312)."""
+    a = _f32(a)
+    out = np.empty_like(a)
+    lib().axo_bf16_round(_f(a), ctypes.c_int64(a.size), _f(out))
+    return out
+
+
 def matmul(a, b, batch, m, k, n):
     a, b = _f32(a), _f32(b)
     out = np.empty(batch * m * n, np.float32)
@@ -729,13 +738,15 @@ def mlp_inputs(batch=128, sizes=(784, 256, 256, 10), x_seed=1, label_seed=2, wei
     return x, y.reshape(-1), params
 
 
-def mlp_forward_backward(x, y, params, batch, sizes):
-    """ReLU MLP forward, mean categorical cross-entropy, and the tape's reverse sweep."""
+def mlp_forward_backward(x, y, params, batch, sizes, bf16=False):
+    """ReLU MLP forward, mean categorical cross-entropy, and the tape's reverse sweep.  bf16: the
+    matrix products take bf16-rounded operands (Device::cuda_bf16, backend.rs:274-283)."""
+    r = bf16_round if bf16 else (lambda v: v)
     acts, pre = [x], []
     h = x
     layers = len(sizes) - 1
     for j in range(layers):
-        z = linear_forward(h, params[f"w{j}"], params[f"b{j}"], batch, sizes[j], sizes[j + 1])
+        z = linear_forward(r(h), r(params[f"w{j}"]), params[f"b{j}"], batch, sizes[j], sizes[j + 1])
         pre.append(z)
         h = relu(z) if j < layers - 1 else z
         acts.append(h)
@@ -747,16 +758,16 @@ def mlp_forward_backward(x, y, params, batch, sizes):
         if j < layers - 1:
             g = relu_backward(g, pre[j])
         grads[f"b{j}"] = bias_gradient(g, batch, sizes[j + 1])
-        grads[f"w{j}"] = matmul_right_backward(acts[j], g, 1, batch, sizes[j], sizes[j + 1])
+        grads[f"w{j}"] = matmul_right_backward(r(acts[j]), r(g), 1, batch, sizes[j], sizes[j + 1])
         if j > 0:
-            g = matmul_left_backward(g, params[f"w{j}"], 1, batch, sizes[j], sizes[j + 1])
+            g = matmul_left_backward(r(g), r(params[f"w{j}"]), 1, batch, sizes[j], sizes[j + 1])
     return loss, grads
 
 
-def mlp_step(batch=128, sizes=(784, 256, 256, 10), lr=1e-3):
+def mlp_step(batch=128, sizes=(784, 256, 256, 10), lr=1e-3, bf16=False):
     """one forward + backward + Adam step; returns loss, grads, new params."""
     x, y, params = mlp_inputs(batch, sizes)
-    loss, grads = mlp_forward_backward(x, y, params, batch, sizes)
+    loss, grads = mlp_forward_backward(x, y, params, batch, sizes, bf16)
     new = AdamOracle(lr).step(params, grads)
     return {"loss": loss, "grads": grads, "params": new, "initial": params, "x": x, "y": y}
 

@@ -376,6 +376,36 @@ def test_mlp_config1_step_matches_oracle(ax, device, oracle):
             check_first_adam_step(oracle, key, v, g, ref["initial"][key], ref["grads"][key], ref["params"][key])
 
 
+def test_mlp_config1_step_bf16_device(ax, oracle):
+    """Config 1 on a Device.hip_bf16 handle against the oracle's step with bf16-rounded product
+    operands (Device::cuda_bf16: parameters, activations and optimizer state stay fp32)."""
+    device = ax.Device.hip_bf16(0)
+    assert device.bf16_matmul()
+    sizes, batch = (784, 256, 256, 10), 128
+    ref = oracle.mlp_step(batch, sizes, bf16=True)
+    model, bt, feats = build_mlp(ax, device, batch, sizes)
+    names = {}
+    for j in range(len(sizes) - 1):
+        names[f"{2 * j}.weight"] = ref["initial"][f"w{j}"]
+        names[f"{2 * j}.bias"] = ref["initial"][f"b{j}"]
+    _set_all(model, names)
+    x = ax.Tensor.from_slice(ref["x"], [bt.of(batch), feats[0].of(784)], device)
+    y = ax.Tensor.from_slice(ref["y"], [bt.of(batch), feats[-1].of(10)], device)
+    loss = model.forward(x).categorical_cross_entropy_with_logits(y, feats[-1]).mean([bt])
+    loss.backward()
+    assert abs(loss.item() - ref["loss"]) <= 1e-5 * max(1, abs(ref["loss"]))
+    fp32 = oracle.mlp_step(batch, sizes)
+    assert abs(ref["loss"] - fp32["loss"]) > 1e-6  # bf16 operands change the loss
+    grads = {name: model.parameter(name).grad().to_vec() for name in names}
+    ax.Adam(1e-3).step(model)
+    for j in range(len(sizes) - 1):
+        for kind, key in (("weight", f"w{j}"), ("bias", f"b{j}")):
+            g = grads[f"{2 * j}.{kind}"]
+            assert rel_max(g, ref["grads"][key]) < 1e-4, (key, rel_max(g, ref["grads"][key]))
+            v = model.parameter(f"{2 * j}.{kind}").tensor().to_vec()
+            check_first_adam_step(oracle, key, v, g, ref["initial"][key], ref["grads"][key], ref["params"][key])
+
+
 def build_cnn(ax, device, batch, size, classes, ch):
     bt, c0, h, w = ax.Axis("batch"), ax.Axis("channel"), ax.Axis("height"), ax.Axis("width")
     cs = [c0] + [ax.Axis(f"c{j + 1}") for j in range(3)]

@@ -570,6 +570,76 @@ def test_reduce_axes_rejects_non_dense_layouts(dev):
                  red.ctypes.data_as(VP), F32(1.0))
 
 
+# ---------------------------------------------------------------- bf16 matrix products
+
+@pytest.fixture(scope="module")
+def dev_bf16():
+    return hip.Device(0, bf16_matmul=True)
+
+
+@pytest.mark.parametrize("m,k,n", [(96, 160, 130), (257, 512, 256), (64, 2048, 40)])
+def test_bf16_matmul_family(dev, dev_bf16, oracle, m, k, n):
+    # Device::cuda_bf16: each product rounds its operands to bf16 and accumulates in fp32
+    rng = np.random.default_rng(m + k + n)
+    a = rng.standard_normal(m * k).astype(np.float32)
+    b = rng.standard_normal(k * n).astype(np.float32)
+    g = rng.standard_normal(m * n).astype(np.float32)
+    ra, rb, rg = oracle.bf16_round(a), oracle.bf16_round(b), oracle.bf16_round(g)
+    flag = ctypes.c_int()
+    hip.check(hip.load().axis_device_bf16_matmul(dev_bf16.handle, ctypes.byref(flag)), "bf16 flag")
+    assert flag.value == 1
+    da, db, dg = up(dev_bf16, a), up(dev_bf16, b), up(dev_bf16, g)
+    geo = (I64(1), I64(m), I64(k), I64(n))
+    out = dev_bf16.empty(m * n)
+    dev_bf16.call("axis_matmul", da.vp, db.vp, out.vp, *geo)
+    got = dev_bf16.read(out, m * n)
+    ref = oracle.matmul(ra, rb, 1, m, k, n)
+    assert rel_err(got, ref) < 1e-5
+    assert rel_err(got, oracle.matmul(a, b, 1, m, k, n)) > 1e-4  # the rounding is really there
+    dx, dw = dev_bf16.empty(m * k), dev_bf16.empty(k * n)
+    dev_bf16.call("axis_matmul_left_backward", dg.vp, db.vp, dx.vp, *geo)
+    assert rel_err(dev_bf16.read(dx, m * k), oracle.matmul_left_backward(rg, rb, 1, m, k, n)) < 1e-5
+    dev_bf16.call("axis_matmul_right_backward", da.vp, dg.vp, dw.vp, *geo)
+    assert rel_err(dev_bf16.read(dw, k * n), oracle.matmul_right_backward(ra, rg, 1, m, k, n)) < 1e-5
+    # an fp32 handle is unaffected
+    out32 = dev.empty(m * n)
+    d32a, d32b = up(dev, a), up(dev, b)
+    dev.call("axis_matmul", d32a.vp, d32b.vp, out32.vp, *geo)
+    assert rel_err(dev.read(out32, m * n), oracle.matmul(a, b, 1, m, k, n)) < 1e-5
+
+
+@pytest.mark.parametrize("layout,b,c,h,w,n", [("nchw", 2, 3, 16, 16, 64), ("nhwc", 2, 64, 8, 8, 128)])
+def test_bf16_convolution_entries(dev_bf16, oracle, layout, b, c, h, w, n):
+    # bf16 mode: the convolution's product (unfold -> matmul_bf16) takes rounded input and weight;
+    # the bias is added in fp32 after it, as the separate add of the reference's lowering.
+    k = 3
+    rng = np.random.default_rng(c + n)
+    x = rng.uniform(-1, 1, b * c * h * w).astype(np.float32)
+    weight = (rng.standard_normal(c * k * k * n) * 0.2).astype(np.float32)
+    bias = (rng.standard_normal(n) * 0.1).astype(np.float32)
+    if layout == "nchw":
+        dims = [("batch", b), ("c", c), ("height", h), ("width", w)]
+        strides = (I64 * 4)(c * h * w, h * w, w, 1)
+    else:
+        dims = [("batch", b), ("height", h), ("width", w), ("c", c)]
+        strides = None
+    z, _ = _oracle_conv(oracle, oracle.bf16_round(x), oracle.bf16_round(weight), bias, dims, b, c, n, k, 1, 1, h, w)
+    geo = [(I32 * 2)(k, k), (I32 * 2)(1, 1), (I32 * 2)(1, 1)]
+    dx, dw, db = up(dev_bf16, x), up(dev_bf16, weight), up(dev_bf16, bias)
+    out = dev_bf16.empty(b * h * w * n)
+    dev_bf16.call("axis_conv2d_forward", dx.vp, strides, dw.vp, db.vp, out.vp, I64(b), I32(h), I32(w), I32(c),
+                  I32(n), *geo)
+    assert rel_err(dev_bf16.read(out, b * h * w * n), z) < 1e-5
+    # fused ReLU + 2x2 pool: pooled values of the same bf16 products
+    pooled_len = b * (h // 2) * (w // 2) * n
+    pooled, arg = dev_bf16.empty(pooled_len), dev_bf16.empty(pooled_len, np.uint8)
+    dev_bf16.call("axis_conv2d_relu_pool_forward", dx.vp, strides, dw.vp, db.vp, pooled.vp, arg.vp, I64(b), I32(h),
+                  I32(w), I32(c), I32(n), *geo, (I32 * 2)(2, 2))
+    ref, _ = _first_max(_windows(np.maximum(z, 0), b, h, w, n, 2, 2))
+    scale = np.abs(z).max()
+    assert np.abs(dev_bf16.read(pooled, pooled_len) - ref.reshape(-1)).max() <= 1e-5 * scale
+
+
 # ---------------------------------------------------------------- implicit-GEMM convolution
 
 # Outputs of 16x16, 8x8, 32x32 (stride 2, and padding 0) and 64x64 pixels take the weight

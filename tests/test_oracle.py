@@ -53,6 +53,26 @@ def test_powi_matches_repeated_squaring(oracle):
 
 # ---------------------------------------------------------------- contractions
 
+def test_bf16_round_matches_torch(oracle):
+    # The operand conversion of the reference's bf16 products (backend.rs:2209-2312) against an
+    # independent implementation (torch's float32 -> bfloat16, round to nearest even), including
+    # exact ties, overflow to infinity, subnormals, signed zeros, infinities and NaN.
+    import torch
+    rng = np.random.default_rng(12)
+    values = np.concatenate([
+        rng.standard_normal(100000).astype(np.float32) * np.float32(10) ** rng.integers(-30, 30, 100000).astype(np.float32),
+        np.array([0x3F808000, 0x3F818000, 0xBF808000, 0x7F7FFFFF, 0x7F7F8000, 0x00018000, 0x00008000,
+                  0x80000000, 0x00000000, 0x7F800000, 0xFF800000], np.uint32).view(np.float32),
+    ]).astype(np.float32)
+    got = oracle.bf16_round(values)
+    ref = torch.from_numpy(values).to(torch.bfloat16).to(torch.float32).numpy()
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    # ties go to the even bf16 neighbour
+    assert got[-11:-9].view(np.uint32).tolist() == [0x3F800000, 0x3F820000]
+    nan = oracle.bf16_round(np.array([np.nan, -np.nan], np.float32))
+    assert np.all(np.isnan(nan)) and np.all((nan.view(np.uint32) & 0xFFFF) == 0)
+
+
 def test_matmul_family_matches_float64(oracle):
     rng = np.random.default_rng(0)
     b, m, k, n = 2, 7, 5, 9
