@@ -34,6 +34,7 @@
 #include "bf16.hpp"
 #include "conv_small.hpp"
 #include "fastdiv.hpp"
+#include "gemm_bf16.hpp"
 #include "pool_rule.hpp"
 
 namespace {
@@ -994,8 +995,67 @@ int sum_splits(axis_device device, const float *partial, float *out, int64_t len
     return axis::launch_status("split_sum_kernel");
 }
 
+// Dense product on a bf16 device: both operands staged as bf16 rows, then bf16 matrix cores
+// (gemm_bf16.hip).  The staging passes sit inside the timed launch.
+int run_gemm_bf16(axis_device device, const GemmParams &p, int64_t batch, float *out) {
+    constexpr int64_t D = axis::kBf16Depth;
+    const int64_t kp = (p.k + D - 1) / D * D;
+    const int64_t xb = p.x_batch ? batch : 1, yb = p.y_batch ? batch : 1;
+    axis::Scratch sx, sy, partial;
+    if (int st = sx.get(device, sizeof(uint16_t) * (size_t)(xb * p.m * kp))) return st;
+    if (int st = sy.get(device, sizeof(uint16_t) * (size_t)(yb * p.n * kp))) return st;
+    const double k_work = (double)(p.k_work > 0 ? p.k_work : p.k);
+    axis::TimedLaunch timed(device, "gemm", 2.0 * (double)batch * (double)p.m * (double)p.n * k_work);
+    if (int st = axis::stage_bf16(device, {p.x, p.x_batch, p.x_si, p.x_sr}, xb, p.m, p.k, kp, sx.as<uint16_t>()))
+        return st;
+    if (int st = axis::stage_bf16(device, {p.y, p.y_batch, p.y_sj, p.y_sr}, yb, p.n, p.k, kp, sy.as<uint16_t>()))
+        return st;
+    const int tile = axis::bf16_gemm_tile(p.m, p.n, batch, device->multiprocessors);
+    const int64_t tiles = ((p.m + tile - 1) / tile) * ((p.n + tile - 1) / tile) * batch;
+    const int64_t slots = device->multiprocessors * 2;
+    const int64_t out_len = batch * p.m * p.n;
+    // split as the fp32 path does: fill one round of resident blocks, reductions of 8 stages or more
+    int64_t splits = 1;
+    if (tiles < slots && kp >= 8 * D) {
+        splits = std::min<int64_t>({slots / tiles, kp / (D * 4), (int64_t(16) << 20) / out_len});
+        splits = std::max<int64_t>(splits, 1);
+    }
+    int64_t chunk = (kp + splits - 1) / splits;
+    chunk = (chunk + D - 1) / D * D;
+    splits = (kp + chunk - 1) / chunk;
+    axis::Bf16Gemm g{};
+    g.x = sx.as<uint16_t>();
+    g.y = sy.as<uint16_t>();
+    g.x_batch = p.x_batch ? p.m * kp : 0;
+    g.y_batch = p.y_batch ? p.n * kp : 0;
+    g.bias = p.bias;
+    g.d = p.d;
+    g.alpha = p.alpha;
+    g.beta = p.beta;
+    g.m = p.m;
+    g.n = p.n;
+    g.kp = kp;
+    g.c_batch = p.m * p.n;
+    g.k_chunk = chunk;
+    g.splits = (int32_t)splits;
+    if (splits > 1) {
+        if (int st = partial.get(device, sizeof(float) * (size_t)(out_len * splits))) return st;
+        g.c = partial.as<float>();
+        g.c_split = out_len;
+    } else {
+        g.c = out;
+        g.c_split = 0;
+    }
+    if (int st = axis::bf16_gemm(device, g, batch, tile)) return st;
+    if (splits > 1)
+        return sum_splits(device, partial.as<float>(), out, out_len, splits, p.bias, p.n, p.d, p.alpha, p.beta, 0, 0);
+    return AXIS_OK;
+}
+
 template <bool XR, bool YR, int XMODE, int EPI>
 int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out) {
+    if constexpr (XMODE == 0 && EPI == 0)
+        if (device->bf16_matmul && !p.ytaps.on && !p.perm_c) return run_gemm_bf16(device, p, batch, out);
     p.bf16 = device->bf16_matmul;
     const int64_t cus = device->multiprocessors;
     const Choice ch = choose(p.m, p.n, p.k, batch, cus, EPI == 1);

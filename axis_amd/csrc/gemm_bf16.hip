@@ -1,0 +1,356 @@
+// bf16 matrix-core product of the dense matmul family on a bf16 device (interface and the
+// reference kernels it stands for: gemm_bf16.hpp).
+//
+// Staging: each operand becomes bf16 rows [b][t][kp], reduction index contiguous, so every
+// MFMA operand (eight consecutive reduction elements of one row) is one 16-byte LDS read and
+// every global read of the product kernel a 16-byte row chunk.  Operands already contiguous
+// along the reduction are rounded in place order; those contiguous along t go through a 64 x 64
+// LDS transpose so both the fp32 reads and the bf16 writes stay coalesced.
+//
+// Product: 256 threads (2 x 2 waves) per BM x BN tile, 64-deep LDS stages of both operands in
+// two LDS buffers, each stage loaded into registers two stages ahead of its use and fed to
+// v_mfma_f32_16x16x32_bf16.
+#include <algorithm>
+#include <type_traits>
+
+#include "common.hpp"
+#include "bf16.hpp"
+#include "gemm_bf16.hpp"
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t bf16_bits(float x) { return __builtin_bit_cast(uint32_t, bf16_round(x)) >> 16; }
+
+// One thread per 8-element chunk of a staged row; reads along r (coalesced when s_r == 1).
+// VEC: s_r == 1 with 16-byte aligned rows, so a chunk inside k is two 16-byte reads.
+template <bool VEC>
+__global__ void stage_rows_kernel(axis::Bf16Source s, int64_t rows, int64_t k, int64_t kp, int64_t total,
+                                  uint16_t *dst) {
+    const int64_t chunks = kp / 8;
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t c8 = idx % chunks;
+        const int64_t row = idx / chunks;  // b * rows + t
+        const int64_t b = row / rows, t = row - b * rows;
+        const float *src = s.base + b * s.s_b + t * s.s_t;
+        uint32_t h[8];
+        if (VEC && c8 * 8 + 8 <= k) {
+            const floatx4 lo = *reinterpret_cast<const floatx4 *>(src + c8 * 8);
+            const floatx4 hi = *reinterpret_cast<const floatx4 *>(src + c8 * 8 + 4);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                h[j] = bf16_bits(lo[j]);
+                h[j + 4] = bf16_bits(hi[j]);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int64_t r = c8 * 8 + j;
+                h[j] = r < k ? bf16_bits(src[r * s.s_r]) : 0u;
+            }
+        }
+        const u32x4 v = {h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+        *reinterpret_cast<u32x4 *>(dst + row * kp + c8 * 8) = v;
+    }
+}
+
+// Operands contiguous along t (s_t == 1): block (tt, rt, b) moves the 64 x 64 tile at
+// t0 = 64 tt, r0 = 64 rt through LDS; reads run along t, writes along r.
+__global__ void __launch_bounds__(256) stage_transpose_kernel(axis::Bf16Source s, int64_t rows, int64_t k,
+                                                              int64_t kp, uint16_t *dst) {
+    constexpr int PITCH = 66;  // bf16 per LDS row: 2-byte stores of 64 consecutive rows hit distinct banks
+    __shared__ uint16_t tile[64 * PITCH];
+    const int tid = threadIdx.x;
+    const int64_t t0 = (int64_t)blockIdx.x * 64, r0 = (int64_t)blockIdx.y * 64, b = blockIdx.z;
+    const float *src = s.base + b * s.s_b;
+    const int tl = tid & 63;
+    const int64_t t = t0 + tl;
+#pragma unroll 4
+    for (int e = 0; e < 16; ++e) {
+        const int rl = e * 4 + (tid >> 6);
+        const int64_t r = r0 + rl;
+        tile[tl * PITCH + rl] = (uint16_t)(t < rows && r < k ? bf16_bits(src[t * s.s_t + r * s.s_r]) : 0u);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const int idx = tid + e * 256;
+        const int row = idx >> 3, ch = idx & 7;
+        if (t0 + row >= rows) continue;
+        const uint32_t *q = reinterpret_cast<const uint32_t *>(tile + row * PITCH + ch * 8);
+        const u32x4 v = {q[0], q[1], q[2], q[3]};
+        *reinterpret_cast<u32x4 *>(dst + (b * rows + t0 + row) * kp + r0 + ch * 8) = v;
+    }
+}
+
+// Buffer loads: an offset at or past the resource's record count reads as zero (rows past the
+// end of the operand).
+constexpr uint32_t kOutside = 0x80000000u;
+
+__device__ __forceinline__ const uint16_t *uniform_ptr(const uint16_t *p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return reinterpret_cast<const uint16_t *>(((uint64_t)hi << 32) | lo);
+}
+
+// records = 0 makes every load of the resource read zero without touching memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const uint16_t *base, int records = 0x7fffffff) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, records, 0x00020000);
+}
+
+// LDS layout of one operand's stage: row t (64 reduction elements, 128 bytes, unpadded) at
+// t * kPitch, its 16-byte chunk c at chunk position c ^ (t % 8).  An MFMA operand read (16
+// consecutive rows, one chunk) and a stage store (whole rows) then meet no bank conflict
+// (SQ_LDS_BANK_CONFLICT reads 0, against 2.7 cycles per LDS instruction for a 144-byte padded
+// pitch).  The swizzle depends on t % 16 only, so the rows 16 i apart that one lane reads share it.
+constexpr int kPitch = axis::kBf16Depth;
+__device__ __forceinline__ constexpr int chunk_swizzle(int t) { return t & 7; }
+__device__ __forceinline__ constexpr int chunk_at(int t, int c) { return t * kPitch + ((c ^ chunk_swizzle(t)) << 3); }
+
+struct KernelArgs {
+    axis::Bf16Gemm g;
+    int32_t tiles_m, tiles_n;
+    uint32_t xcd_span;  // blocks per XCD when the launch is remapped (blocks % 8 == 0), else 0
+};
+
+// + bias[col], then beta * d + alpha * v, each product and the sum rounded separately.
+__device__ __forceinline__ float finish(const float *bias, const float *d, float alpha, float beta, float v,
+                                        int64_t idx, int64_t col) {
+#pragma clang fp contract(off)
+    if (bias) v = v + bias[col];
+    if (d) {
+        const float t1 = beta * d[idx];
+        const float t2 = alpha * v;
+        v = t1 + t2;
+    }
+    return v;
+}
+
+// Rows [t0, t0 + BT) of a staged operand, one 64-deep stage: CH 16-byte chunks per thread,
+// chunk idx = tid + 256 e at row idx / 8, reduction offset 8 * (idx % 8).  The registers a stage
+// lands in belong to the caller, so two stages can be in flight.
+template <int BT>
+struct StageLoader {
+    static constexpr int CH = BT * axis::kBf16Depth / 8 / 256;
+    uint32_t off[CH];  // byte offset from the stage's row-0 origin, or kOutside
+    const uint16_t *base;
+
+    __device__ __forceinline__ void init(const uint16_t *b, int64_t t0, int64_t rows, int64_t kp, int tid) {
+        base = uniform_ptr(b + t0 * kp);
+#pragma unroll
+        for (int e = 0; e < CH; ++e) {
+            const int idx = tid + e * 256;
+            const int row = idx >> 3;
+            off[e] = t0 + row < rows ? (uint32_t)((row * kp + (idx & 7) * 8) * 2) : kOutside;
+        }
+    }
+    // live == false (a stage past the end) issues the same loads against an empty resource, so
+    // every path has the same loads in flight and the waits before the LDS writes stay exact.
+    __device__ __forceinline__ void load(int64_t r0, u32x4 *reg, bool live = true) const {
+        const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(uniform_ptr(base + (live ? r0 : 0)), live ? 0x7fffffff : 0);
+#pragma unroll
+        for (int e = 0; e < CH; ++e)
+            reg[e] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off[e], 0, 0));
+    }
+    static __device__ __forceinline__ void store(uint16_t *lds, int tid, const u32x4 *reg) {
+#pragma unroll
+        for (int e = 0; e < CH; ++e) {
+            const int idx = tid + e * 256;
+            *reinterpret_cast<u32x4 *>(lds + chunk_at(idx >> 3, idx & 7)) = reg[e];
+        }
+    }
+};
+
+// Logical tile -> (row panel, column panel): groups of 8 row panels, column-major inside a group,
+// so consecutive tiles (one XCD's resident blocks) cover a compact patch and share panels in L2.
+__device__ __forceinline__ void grouped_tile(uint32_t tile, uint32_t tiles_m, uint32_t tiles_n, uint32_t &ti,
+                                             uint32_t &tj) {
+    const uint32_t per_group = 8u * tiles_n;
+    const uint32_t group = tile / per_group;
+    const uint32_t first = group * 8u;
+    const uint32_t height = tiles_m - first < 8u ? tiles_m - first : 8u;
+    const uint32_t in = tile - group * per_group;
+    ti = first + in % height;
+    tj = in / height;
+}
+
+template <int BM, int BN>
+__global__ void __launch_bounds__(256, 2) bf16_gemm_kernel(KernelArgs a) {
+    constexpr int BK = axis::kBf16Depth;
+    constexpr int LDK = kPitch;
+    constexpr int WM = 2, WN = 2, TM = BM / WM, TN = BN / WN, FM = TM / 16, FN = TN / 16;
+    constexpr int kBuf = (BM + BN) * LDK;  // one stage of both operands
+    __shared__ __attribute__((aligned(16))) uint16_t lds[2 * kBuf];
+    const axis::Bf16Gemm &g = a.g;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave % WM, wn = wave / WM;
+    const int quad = lane >> 4, l16 = lane & 15;
+
+    // XCD-aware order: block L takes logical tile (L % 8) * (blocks / 8) + L / 8, so each XCD's
+    // L2 serves a contiguous range of tiles.
+    const uint32_t tiles = (uint32_t)a.tiles_m * (uint32_t)a.tiles_n;
+    const uint32_t L = blockIdx.x;
+    const uint32_t logical = a.xcd_span ? (L % 8u) * a.xcd_span + L / 8u : L;
+    const uint32_t tile = logical % tiles;
+    const uint32_t slice = logical / tiles;
+    uint32_t ti, tj;
+    grouped_tile(tile, (uint32_t)a.tiles_m, (uint32_t)a.tiles_n, ti, tj);
+    const int64_t i0 = (int64_t)ti * BM;
+    const int64_t j0 = (int64_t)tj * BN;
+    const int split = (int)(slice % (uint32_t)g.splits);
+    const int64_t batch = slice / (uint32_t)g.splits;
+    const int64_t r_begin = (int64_t)split * g.k_chunk;
+    const int64_t r_end = r_begin + g.k_chunk < g.kp ? r_begin + g.k_chunk : g.kp;
+    const int stages = (int)((r_end - r_begin) / BK);  // the host splits in whole stages
+
+    floatx4 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    using LX = StageLoader<BM>;
+    using LY = StageLoader<BN>;
+    LX lx;
+    LY ly;
+    lx.init(g.x + batch * g.x_batch, i0, g.m, g.kp, tid);
+    ly.init(g.y + batch * g.y_batch, j0, g.n, g.kp, tid);
+    // Two register sets: stage s lands in set s % 2, two stages ahead of its use.
+    u32x4 rx[2][LX::CH], ry[2][LY::CH];
+    lx.load(r_begin, rx[0], stages > 0);
+    ly.load(r_begin, ry[0], stages > 0);
+    lx.load(r_begin + BK, rx[1], stages > 1);
+    ly.load(r_begin + BK, ry[1], stages > 1);
+    if (stages > 0) {
+        LX::store(lds, tid, rx[0]);
+        LY::store(lds + BM * LDK, tid, ry[0]);
+    }
+    __syncthreads();
+
+    // v_mfma_f32_16x16x32_bf16: lane l supplies row l % 16 of A and column l % 16 of B at
+    // reduction elements 8 * (l / 16) .. + 7; result register v is row 4 * (l / 16) + v,
+    // column l % 16.  Block i of a wave covers its rows 16 i .. 16 i + 15, block j its columns.
+    // operand offsets of the lane's chunk for the two 32-deep halves of a stage (chunks quad, 4 + quad)
+    const int xa[2] = {chunk_at(wm * TM + l16, quad), chunk_at(wm * TM + l16, 4 + quad)};
+    const int yb[2] = {BM * LDK + chunk_at(wn * TN + l16, quad), BM * LDK + chunk_at(wn * TN + l16, 4 + quad)};
+    auto compute = [&](const uint16_t *buf) {
+        bf16x8 av[2][FM], bv[2][FN];
+        auto read_operands = [&](int kk, bf16x8 *avk, bf16x8 *bvk) {
+            const int h = kk / 32;
+#pragma unroll
+            for (int i = 0; i < FM; ++i) avk[i] = *reinterpret_cast<const bf16x8 *>(buf + xa[h] + 16 * i * LDK);
+#pragma unroll
+            for (int j = 0; j < FN; ++j) bvk[j] = *reinterpret_cast<const bf16x8 *>(buf + yb[h] + 16 * j * LDK);
+        };
+        read_operands(0, av[0], bv[0]);
+#pragma unroll
+        for (int kk = 0; kk < BK; kk += 32) {
+            const int cur = (kk / 32) & 1;
+            if (kk + 32 < BK) read_operands(kk + 32, av[cur ^ 1], bv[cur ^ 1]);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[cur][i], bv[cur][j], acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    // Stage s: loads of stage s + 2 go into the register set stage s came from, stage s is
+    // computed from LDS buffer s % 2, stage s + 1 moves from registers into the other buffer
+    // (whose stage s - 1 every wave finished before the last barrier), then one barrier.
+    auto step = [&](int s, auto parity) {
+        constexpr int P = decltype(parity)::value;
+        const int64_t r0 = r_begin + (int64_t)s * BK;
+        lx.load(r0 + 2 * BK, rx[P], s + 2 < stages);
+        ly.load(r0 + 2 * BK, ry[P], s + 2 < stages);
+        compute(lds + P * kBuf);
+        if (s + 1 < stages) {
+            LX::store(lds + (P ^ 1) * kBuf, tid, rx[P ^ 1]);
+            LY::store(lds + (P ^ 1) * kBuf + BM * LDK, tid, ry[P ^ 1]);
+        }
+        __syncthreads();
+    };
+    for (int s = 0; s < stages; s += 2) {
+        step(s, std::integral_constant<int, 0>{});
+        if (s + 1 < stages) step(s + 1, std::integral_constant<int, 1>{});
+    }
+
+    // acc[i][j][v]: tile row wm*TM + 16 i + 4 quad + v, column wn*TN + 16 j + l16.  Bias and
+    // axpby apply to whole sums only; a split reduction's slices are finished by its sum.
+    float *c = g.c + batch * g.c_batch + (int64_t)split * g.c_split;
+    const bool whole = g.splits == 1;
+    const float *bias = whole ? g.bias : nullptr;
+    const float *d = whole ? g.d : nullptr;
+    const int64_t out_base = batch * g.m * g.n;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+        const int64_t col = j0 + wn * TN + 16 * j + l16;
+        if (col >= g.n) continue;
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int64_t row = i0 + wm * TM + 16 * i + 4 * quad + v;
+                if (row < g.m)
+                    c[row * g.n + col] =
+                        finish(bias, d, g.alpha, g.beta, acc[i][j][v], out_base + row * g.n + col, col);
+            }
+    }
+}
+
+}  // namespace
+
+namespace axis {
+
+int stage_bf16(axis_device device, const Bf16Source &src, int64_t batch, int64_t rows, int64_t k, int64_t kp,
+               uint16_t *dst) {
+    if (kp % kBf16Depth != 0 || kp < k) return fail(AXIS_ERROR_INVALID, "bf16 staging depth must cover k in whole stages");
+    if (src.s_t == 1 && src.s_r != 1) {
+        dim3 grid((unsigned)((rows + 63) / 64), (unsigned)(kp / 64), (unsigned)batch);
+        if (rows > (int64_t)64 * INT32_MAX || batch > 65535 || kp / 64 > 65535)
+            return fail(AXIS_ERROR_INVALID, "bf16 staging grid too large");
+        stage_transpose_kernel<<<grid, 256, 0, device->stream>>>(src, rows, k, kp, dst);
+        return launch_status("stage_transpose_kernel");
+    }
+    const int64_t total = batch * rows * (kp / 8);
+    const bool vec = src.s_r == 1 && aligned16(src.base) && src.s_t % 4 == 0 && src.s_b % 4 == 0;
+    if (vec)
+        stage_rows_kernel<true><<<blocks_for(total, 256, 1 << 16), 256, 0, device->stream>>>(src, rows, k, kp, total, dst);
+    else
+        stage_rows_kernel<false><<<blocks_for(total, 256, 1 << 16), 256, 0, device->stream>>>(src, rows, k, kp, total, dst);
+    return launch_status("stage_rows_kernel");
+}
+
+int bf16_gemm_tile(int64_t m, int64_t n, int64_t batch, int64_t cus) {
+    const int64_t large = ((m + 127) / 128) * ((n + 127) / 128) * batch;
+    return large * 2 < cus ? 64 : 128;
+}
+
+int bf16_gemm(axis_device device, const Bf16Gemm &g, int64_t batch, int tile) {
+    KernelArgs a{};
+    a.g = g;
+    a.tiles_m = (int32_t)((g.m + tile - 1) / tile);
+    a.tiles_n = (int32_t)((g.n + tile - 1) / tile);
+    const int64_t blocks = (int64_t)a.tiles_m * a.tiles_n * batch * g.splits;
+    if (blocks >= INT32_MAX) return fail(AXIS_ERROR_INVALID, "matmul too large for one launch");
+    // 32-bit byte offsets inside one tile's rows: (tile rows + 1) * kp * 2 bytes
+    if ((int64_t)(tile + 1) * g.kp * 2 >= (int64_t(1) << 31)) return fail(AXIS_ERROR_INVALID, "bf16 matmul reduction too long");
+    a.xcd_span = blocks % 8 == 0 ? (uint32_t)(blocks / 8) : 0u;
+    dim3 grid((unsigned)blocks);
+    if (tile == 128)
+        bf16_gemm_kernel<128, 128><<<grid, 256, 0, device->stream>>>(a);
+    else
+        bf16_gemm_kernel<64, 64><<<grid, 256, 0, device->stream>>>(a);
+    return launch_status("bf16_gemm_kernel");
+}
+
+}  // namespace axis

@@ -30,6 +30,7 @@ sys.path.insert(0, ROOT)
 
 BASELINE_METRIC = "images/sec (3-block CNN, bs256, fp32 fwd+bwd+Adam); % of fp32 MFMA peak"
 FP32_MFMA_PEAK_TFLOPS = 157.3
+BF16_MFMA_PEAK_TFLOPS = 2500.0  # dense
 HBM_PEAK_GBS = 8000.0
 
 BATCH, SIZE, CLASSES, CHANNELS = 256, 64, 1000, (3, 64, 128, 256)
@@ -127,11 +128,14 @@ def _timing(lib, handle, family):
 
 def bench_matmul(args):
     """dX = dY W^T and dW = X^T dY for X, W, dY [4096, 4096] and for the
-    skinny case X [8192, 784], W [784, 1024], all N(0, 1) from seeds 21, 22, 23."""
+    skinny case X [8192, 784], W [784, 1024], all N(0, 1) from seeds 21, 22, 23.  With --bf16 the
+    device rounds product operands to bf16 (Device::cuda_bf16) and the products run on bf16 matrix
+    cores; the timed launches then include the operand staging."""
     import axis_amd
     from axis_amd import hip
     ax = axis_amd.host()
-    dev = hip.Device(0)
+    dev = hip.Device(0, bf16_matmul=args.bf16)
+    peak = BF16_MFMA_PEAK_TFLOPS if args.bf16 else FP32_MFMA_PEAK_TFLOPS
     lib = hip.load()
     results = {}
     for name, (m, k, n) in {"square_4096": (4096, 4096, 4096), "skinny_8192x784x1024": (8192, 784, 1024)}.items():
@@ -155,16 +159,18 @@ def bench_matmul(args):
             launches, ms, work = _timing(lib, dev.handle, "gemm")
             tflops = work / (ms * 1e-3) / 1e12
             row[op] = {"ms": round(ms / launches, 4), "tflops": round(tflops, 2),
-                       "frac": round(tflops / FP32_MFMA_PEAK_TFLOPS, 4)}
+                       "frac": round(tflops / peak, 4)}
         results[name] = row
     total = [v for r in results.values() for v in r.values()]
     avg = sum(v["tflops"] for v in total) / len(total)
-    print(json.dumps({"metric": "fp32 matmul backward TFLOP/s (dgrad + wgrad)", "value": round(avg, 2),
+    kind = "bf16" if args.bf16 else "fp32"
+    print(json.dumps({"metric": f"{kind} matmul backward TFLOP/s (dgrad + wgrad)", "value": round(avg, 2),
                       "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-                      "higher_is_better": True, "dtype": "fp32", "data": "synthetic N(0,1), seeds 21-23",
-                      "config": {"workload": "BASELINE config 2: isolated matmul backward"},
-                      "roofline": {"bound": "mfma", "achieved": round(avg, 2), "peak": FP32_MFMA_PEAK_TFLOPS,
-                                   "unit": "TFLOP/s", "frac": round(avg / FP32_MFMA_PEAK_TFLOPS, 4)},
+                      "higher_is_better": True, "dtype": kind, "data": "synthetic N(0,1), seeds 21-23",
+                      "config": {"workload": "BASELINE config 2: isolated matmul backward"
+                                             + (" on a bf16 device" if args.bf16 else "")},
+                      "roofline": {"bound": "mfma", "achieved": round(avg, 2), "peak": peak,
+                                   "unit": "TFLOP/s", "frac": round(avg / peak, 4)},
                       "results": results}))
 
 
@@ -321,6 +327,8 @@ def main():
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="one device-to-device copy of this size before the timed steps (a known-size "
                          "dispatch that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
+    ap.add_argument("--bf16", action="store_true",
+                    help="matmul workload: products on a bf16 device (operands rounded to bf16)")
     ap.add_argument("--workload", choices=["cnn", "matmul", "adam", "muon"], default="cnn",
                     help="cnn: the headline metric (BASELINE config 4); the others are configs 2, 3, 5")
     args = ap.parse_args()

@@ -608,6 +608,50 @@ def test_bf16_matmul_family(dev, dev_bf16, oracle, m, k, n):
     assert rel_err(dev.read(out32, m * n), oracle.matmul(a, b, 1, m, k, n)) < 1e-5
 
 
+@pytest.mark.parametrize("batch,m,k,n", [(3, 130, 70, 33), (2, 64, 1000, 200), (1, 1, 9, 1)])
+def test_bf16_batched_products_and_axpby(dev_bf16, oracle, batch, m, k, n):
+    # batched bf16 products (staged operands per batch, reduction tail padded) and the axpby
+    # epilogue: beta * d + alpha * product, each operation rounded on its own
+    rng = np.random.default_rng(batch * 1000 + m + k + n)
+    a = rng.standard_normal(batch * m * k).astype(np.float32)
+    b = rng.standard_normal(batch * k * n).astype(np.float32)
+    g = rng.standard_normal(batch * m * n).astype(np.float32)
+    ra, rb, rg = oracle.bf16_round(a), oracle.bf16_round(b), oracle.bf16_round(g)
+    da, db, dg = up(dev_bf16, a), up(dev_bf16, b), up(dev_bf16, g)
+    geo = (I64(batch), I64(m), I64(k), I64(n))
+    out = dev_bf16.empty(batch * m * n)
+    dev_bf16.call("axis_matmul", da.vp, db.vp, out.vp, *geo)
+    prod = dev_bf16.read(out, batch * m * n)
+    assert rel_err(prod, oracle.matmul(ra, rb, batch, m, k, n)) < 1e-5
+    dx, dw = dev_bf16.empty(batch * m * k), dev_bf16.empty(batch * k * n)
+    dev_bf16.call("axis_matmul_left_backward", dg.vp, db.vp, dx.vp, *geo)
+    assert rel_err(dev_bf16.read(dx, batch * m * k), oracle.matmul_left_backward(rg, rb, batch, m, k, n)) < 1e-5
+    dev_bf16.call("axis_matmul_right_backward", da.vp, dg.vp, dw.vp, *geo)
+    assert rel_err(dev_bf16.read(dw, batch * k * n), oracle.matmul_right_backward(ra, rg, batch, m, k, n)) < 1e-5
+    alpha, beta = 2.0315, -4.7750
+    fused = dev_bf16.empty(batch * m * n)
+    dev_bf16.call("axis_matmul_axpby", da.vp, db.vp, dg.vp, fused.vp, *geo, F32(alpha), F32(beta))
+    # the epilogue applied to this handle's own product is bit-exact (d itself is not rounded)
+    expect = (np.float32(beta) * g) + (np.float32(alpha) * prod)
+    assert np.array_equal(dev_bf16.read(fused, batch * m * n).view(np.uint32), expect.astype(np.float32).view(np.uint32))
+
+
+def test_bf16_products_carry_inf_and_nan(dev_bf16):
+    # a NaN operand stays NaN after rounding, an infinity stays infinite: rows meeting them turn
+    # NaN / inf exactly as the fp32 product of the rounded operands does
+    m, k, n = 4, 80, 5
+    a = np.ones(m * k, np.float32)
+    a[1 * k + 3] = np.nan
+    a[2 * k + 70] = np.inf
+    b = np.full(k * n, 0.5, np.float32)
+    da, db = up(dev_bf16, a), up(dev_bf16, b)
+    out = dev_bf16.empty(m * n)
+    dev_bf16.call("axis_matmul", da.vp, db.vp, out.vp, I64(1), I64(m), I64(k), I64(n))
+    got = dev_bf16.read(out, m * n).reshape(m, n)
+    assert np.all(np.isnan(got[1])) and np.all(np.isposinf(got[2]))
+    assert np.array_equal(got[0], np.full(n, 40.0, np.float32)) and np.array_equal(got[3], got[0])
+
+
 @pytest.mark.parametrize("layout,b,c,h,w,n", [("nchw", 2, 3, 16, 16, 64), ("nhwc", 2, 64, 8, 8, 128)])
 def test_bf16_convolution_entries(dev_bf16, oracle, layout, b, c, h, w, n):
     # bf16 mode: the convolution's product (unfold -> matmul_bf16) takes rounded input and weight;
