@@ -103,14 +103,18 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const uint16_t *base
     return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, records, 0x00020000);
 }
 
-// LDS layout of one operand's stage: row t (64 reduction elements, 128 bytes, unpadded) at
-// t * kPitch, its 16-byte chunk c at chunk position c ^ (t % 8).  An MFMA operand read (16
-// consecutive rows, one chunk) and a stage store (whole rows) then meet no bank conflict
-// (SQ_LDS_BANK_CONFLICT reads 0, against 2.7 cycles per LDS instruction for a 144-byte padded
-// pitch).  The swizzle depends on t % 16 only, so the rows 16 i apart that one lane reads share it.
-constexpr int kPitch = axis::kBf16Depth;
-__device__ __forceinline__ constexpr int chunk_swizzle(int t) { return t & 7; }
-__device__ __forceinline__ constexpr int chunk_at(int t, int c) { return t * kPitch + ((c ^ chunk_swizzle(t)) << 3); }
+// LDS layout of one operand's stage of depth BK: row t (BK reduction elements, unpadded) at
+// t * BK, its 16-byte chunk c at chunk position c ^ Layout<BK>::swizzle(t).  With these swizzles
+// an MFMA operand read (16 consecutive rows, one chunk) and a stage store (whole rows) meet no
+// bank conflict (SQ_LDS_BANK_CONFLICT reads 0, against 2.7 cycles per LDS instruction for 64-deep
+// rows at a 144-byte padded pitch).  A swizzle depends on t % 16 only, so the rows 16 i apart
+// that one lane reads share it.
+template <int BK>
+struct Layout {
+    static constexpr int chunks = BK / 8;
+    static __device__ __forceinline__ constexpr int swizzle(int t) { return BK == 64 ? t & 7 : (t >> 1) & 3; }
+    static __device__ __forceinline__ constexpr int at(int t, int c) { return t * BK + ((c ^ swizzle(t)) << 3); }
+};
 
 struct KernelArgs {
     axis::Bf16Gemm g;
@@ -131,12 +135,13 @@ __device__ __forceinline__ float finish(const float *bias, const float *d, float
     return v;
 }
 
-// Rows [t0, t0 + BT) of a staged operand, one 64-deep stage: CH 16-byte chunks per thread,
-// chunk idx = tid + 256 e at row idx / 8, reduction offset 8 * (idx % 8).  The registers a stage
+// Rows [t0, t0 + BT) of a staged operand, one BK-deep stage: CH 16-byte chunks per thread,
+// chunk idx = tid + 256 e at row idx / (BK / 8), chunk idx % (BK / 8).  The registers a stage
 // lands in belong to the caller, so two stages can be in flight.
-template <int BT>
+template <int BT, int BK>
 struct StageLoader {
-    static constexpr int CH = BT * axis::kBf16Depth / 8 / 256;
+    using Lay = Layout<BK>;
+    static constexpr int CH = BT * BK / 8 / 256;
     uint32_t off[CH];  // byte offset from the stage's row-0 origin, or kOutside
     const uint16_t *base;
 
@@ -145,8 +150,8 @@ struct StageLoader {
 #pragma unroll
         for (int e = 0; e < CH; ++e) {
             const int idx = tid + e * 256;
-            const int row = idx >> 3;
-            off[e] = t0 + row < rows ? (uint32_t)((row * kp + (idx & 7) * 8) * 2) : kOutside;
+            const int row = idx / Lay::chunks;
+            off[e] = t0 + row < rows ? (uint32_t)((row * kp + (idx % Lay::chunks) * 8) * 2) : kOutside;
         }
     }
     // live == false (a stage past the end) issues the same loads against an empty resource, so
@@ -161,7 +166,7 @@ struct StageLoader {
 #pragma unroll
         for (int e = 0; e < CH; ++e) {
             const int idx = tid + e * 256;
-            *reinterpret_cast<u32x4 *>(lds + chunk_at(idx >> 3, idx & 7)) = reg[e];
+            *reinterpret_cast<u32x4 *>(lds + Lay::at(idx / Lay::chunks, idx % Lay::chunks)) = reg[e];
         }
     }
 };
@@ -179,10 +184,11 @@ __device__ __forceinline__ void grouped_tile(uint32_t tile, uint32_t tiles_m, ui
     tj = in / height;
 }
 
-template <int BM, int BN>
+template <int BM, int BN, int BK>
 __global__ void __launch_bounds__(256, 2) bf16_gemm_kernel(KernelArgs a) {
-    constexpr int BK = axis::kBf16Depth;
-    constexpr int LDK = kPitch;
+    static_assert(axis::kBf16Depth % BK == 0 && BK % 32 == 0, "stages tile the staged depth");
+    using Lay = Layout<BK>;
+    constexpr int LDK = BK;  // bf16 per LDS row
     constexpr int WM = 2, WN = 2, TM = BM / WM, TN = BN / WN, FM = TM / 16, FN = TN / 16;
     constexpr int kBuf = (BM + BN) * LDK;  // one stage of both operands
     __shared__ __attribute__((aligned(16))) uint16_t lds[2 * kBuf];
@@ -217,8 +223,8 @@ __global__ void __launch_bounds__(256, 2) bf16_gemm_kernel(KernelArgs a) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    using LX = StageLoader<BM>;
-    using LY = StageLoader<BN>;
+    using LX = StageLoader<BM, BK>;
+    using LY = StageLoader<BN, BK>;
     LX lx;
     LY ly;
     lx.init(g.x + batch * g.x_batch, i0, g.m, g.kp, tid);
@@ -238,9 +244,14 @@ __global__ void __launch_bounds__(256, 2) bf16_gemm_kernel(KernelArgs a) {
     // v_mfma_f32_16x16x32_bf16: lane l supplies row l % 16 of A and column l % 16 of B at
     // reduction elements 8 * (l / 16) .. + 7; result register v is row 4 * (l / 16) + v,
     // column l % 16.  Block i of a wave covers its rows 16 i .. 16 i + 15, block j its columns.
-    // operand offsets of the lane's chunk for the two 32-deep halves of a stage (chunks quad, 4 + quad)
-    const int xa[2] = {chunk_at(wm * TM + l16, quad), chunk_at(wm * TM + l16, 4 + quad)};
-    const int yb[2] = {BM * LDK + chunk_at(wn * TN + l16, quad), BM * LDK + chunk_at(wn * TN + l16, 4 + quad)};
+    // operand offsets of the lane's chunk for each 32-deep part h of a stage (chunk 4 h + quad)
+    constexpr int KS = BK / 32;
+    int xa[KS], yb[KS];
+#pragma unroll
+    for (int h = 0; h < KS; ++h) {
+        xa[h] = Lay::at(wm * TM + l16, 4 * h + quad);
+        yb[h] = BM * LDK + Lay::at(wn * TN + l16, 4 * h + quad);
+    }
     auto compute = [&](const uint16_t *buf) {
         bf16x8 av[2][FM], bv[2][FN];
         auto read_operands = [&](int kk, bf16x8 *avk, bf16x8 *bvk) {
@@ -330,26 +341,29 @@ int stage_bf16(axis_device device, const Bf16Source &src, int64_t batch, int64_t
     return launch_status("stage_rows_kernel");
 }
 
-int bf16_gemm_tile(int64_t m, int64_t n, int64_t batch, int64_t cus) {
+Bf16Tile bf16_gemm_tile(int64_t m, int64_t n, int64_t batch, int64_t cus) {
+    // (A 256 x 128 tile of 32-deep stages, 128 x 64 per wave, measured no faster: a stage's few
+    // hundred MFMA cycles per wave, not LDS or L2 bytes, bound this kernel.)
     const int64_t large = ((m + 127) / 128) * ((n + 127) / 128) * batch;
-    return large * 2 < cus ? 64 : 128;
+    return large * 2 >= cus ? Bf16Tile{128, 128} : Bf16Tile{64, 64};
 }
 
-int bf16_gemm(axis_device device, const Bf16Gemm &g, int64_t batch, int tile) {
+int bf16_gemm(axis_device device, const Bf16Gemm &g, int64_t batch, Bf16Tile tile) {
     KernelArgs a{};
     a.g = g;
-    a.tiles_m = (int32_t)((g.m + tile - 1) / tile);
-    a.tiles_n = (int32_t)((g.n + tile - 1) / tile);
+    a.tiles_m = (int32_t)((g.m + tile.rows - 1) / tile.rows);
+    a.tiles_n = (int32_t)((g.n + tile.cols - 1) / tile.cols);
     const int64_t blocks = (int64_t)a.tiles_m * a.tiles_n * batch * g.splits;
     if (blocks >= INT32_MAX) return fail(AXIS_ERROR_INVALID, "matmul too large for one launch");
     // 32-bit byte offsets inside one tile's rows: (tile rows + 1) * kp * 2 bytes
-    if ((int64_t)(tile + 1) * g.kp * 2 >= (int64_t(1) << 31)) return fail(AXIS_ERROR_INVALID, "bf16 matmul reduction too long");
+    if ((int64_t)(std::max(tile.rows, tile.cols) + 1) * g.kp * 2 >= (int64_t(1) << 31))
+        return fail(AXIS_ERROR_INVALID, "bf16 matmul reduction too long");
     a.xcd_span = blocks % 8 == 0 ? (uint32_t)(blocks / 8) : 0u;
     dim3 grid((unsigned)blocks);
-    if (tile == 128)
-        bf16_gemm_kernel<128, 128><<<grid, 256, 0, device->stream>>>(a);
+    if (tile.rows == 128)
+        bf16_gemm_kernel<128, 128, 64><<<grid, 256, 0, device->stream>>>(a);
     else
-        bf16_gemm_kernel<64, 64><<<grid, 256, 0, device->stream>>>(a);
+        bf16_gemm_kernel<64, 64, 64><<<grid, 256, 0, device->stream>>>(a);
     return launch_status("bf16_gemm_kernel");
 }
 

@@ -608,8 +608,9 @@ def test_bf16_matmul_family(dev, dev_bf16, oracle, m, k, n):
     assert rel_err(dev.read(out32, m * n), oracle.matmul(a, b, 1, m, k, n)) < 1e-5
 
 
-@pytest.mark.parametrize("batch,m,k,n", [(3, 130, 70, 33), (2, 64, 1000, 200), (1, 1, 9, 1)])
+@pytest.mark.parametrize("batch,m,k,n", [(3, 130, 70, 33), (2, 64, 1000, 200), (1, 1, 9, 1), (1, 4100, 96, 2050)])
 def test_bf16_batched_products_and_axpby(dev_bf16, oracle, batch, m, k, n):
+    # (1, 4100, 96, 2050): enough 256 x 128 output tiles for the largest tile, ragged on both sides
     # batched bf16 products (staged operands per batch, reduction tail padded) and the axpby
     # epilogue: beta * d + alpha * product, each operation rounded on its own
     rng = np.random.default_rng(batch * 1000 + m + k + n)
