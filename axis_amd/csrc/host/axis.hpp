@@ -203,6 +203,9 @@ struct Rule {
     std::shared_ptr<axis_unfold_spec> spec;
     std::vector<int32_t> metadata;  // select_axis metadata; ReduceAxes: reduced flags
     std::vector<int64_t> extents, strides;  // ReduceAxes input geometry
+    // BroadcastAxes: select_axis metadata that moves the reduced gradient (kept axes in the output's
+    // order, contiguous) into the input's own layout; empty when it is already in that layout
+    std::vector<int32_t> place;
     int64_t outer = 0, reduce = 0, inner = 0;
     PoolGeometry pool;
     ConvGeometry conv;

@@ -32,7 +32,7 @@ int32_t to_i32(int64_t v) {
     return (int32_t)v;
 }
 
-// Plan::groups / gather / reverse (runtime/backend.rs:1549-1583) as host vectors.
+// Plan::groups / gather (runtime/backend.rs:1549-1583) as host vectors.
 struct HostPlan {
     std::vector<int32_t> offsets{0}, left, right;
 };
@@ -44,19 +44,6 @@ HostPlan plan_gather(const std::vector<int64_t> &map) {
     for (size_t i = 0; i <= map.size(); ++i) p.offsets[i] = (int32_t)i;
     p.left.reserve(map.size());
     for (int64_t v : map) p.left.push_back(to_i32(v));
-    return p;
-}
-
-HostPlan plan_reverse(const std::vector<int64_t> &map, int64_t len) {
-    check_plan_size((int64_t)map.size());
-    std::vector<int32_t> counts((size_t)len + 1, 0);
-    for (int64_t g : map) ++counts[(size_t)g + 1];
-    HostPlan p;
-    p.offsets.assign((size_t)len + 1, 0);
-    for (int64_t g = 0; g < len; ++g) p.offsets[(size_t)g + 1] = p.offsets[(size_t)g] + counts[(size_t)g + 1];
-    std::vector<int32_t> cursor(p.offsets.begin(), p.offsets.end() - 1);
-    p.left.assign(map.size(), 0);
-    for (size_t pos = 0; pos < map.size(); ++pos) p.left[(size_t)cursor[(size_t)map[pos]]++] = (int32_t)pos;
     return p;
 }
 
@@ -324,10 +311,12 @@ Tensor Tensor::align(const Shape &target) const {
             rb.outer = target.len / width;
             rb.inner = width;
             edges.push_back(Edge{*this, rb});
-        } else if (in_order) {
-            // The reverse plan sums each input element's copies in increasing output position
-            // (tensor.rs:679-698, Plan::reverse); with the input's axes in the output's order and
-            // contiguous, that is the strided reduction over the new axes, without the plan.
+        } else {
+            // The reverse plan (tensor.rs:679-698, Plan::reverse) sums each input element's copies in
+            // increasing output position: that is the strided reduction over the new axes, which
+            // walks every group in increasing memory position of the output gradient and writes the
+            // kept axes in the output's order.  An input whose axes run in another order (its
+            // layout is a dense permutation) then takes one select_axis copy into its own layout.
             Rule rb = rule(Rule::BroadcastAxes);
             for (size_t index = 0; index < target.rank(); ++index) {
                 rb.extents.push_back(target.dims[index].extent);
@@ -336,21 +325,18 @@ Tensor Tensor::align(const Shape &target) const {
                 for (size_t p : positions) own = own || p == index;
                 rb.metadata.push_back(own ? 0 : 1);
             }
-            edges.push_back(Edge{*this, rb});
-        } else {
-            // align_reverse_plan (tensor.rs:679-698)
-            std::vector<int64_t> map((size_t)target.len);
-            for (int64_t i = 0; i < target.len; ++i) {
-                auto c = target.coords(i);
-                int64_t off = 0;
-                for (size_t own = 0; own < positions.size(); ++own)
-                    off += c[positions[own]] * this->layout().strides[own];
-                map[(size_t)i] = off;
+            if (!in_order) {
+                // stride of target axis `index` in the reduced buffer: extents of the kept axes after it
+                for (size_t own = 0; own < positions.size(); ++own) {
+                    int64_t reduced_stride = 1;
+                    for (size_t index = positions[own] + 1; index < target.rank(); ++index)
+                        if (!rb.metadata[index]) reduced_stride *= target.dims[index].extent;
+                    rb.place.push_back(to_i32(shape().dims[own].extent));
+                    rb.place.push_back(to_i32(reduced_stride));
+                    rb.place.push_back(to_i32(this->layout().strides[own]));
+                }
             }
-            Rule g = rule(Rule::Group);
-            g.plan = upload(device(), plan_reverse(map, shape().len));
-            g.factor = 1.0f;
-            edges.push_back(Edge{*this, g});
+            edges.push_back(Edge{*this, rb});
         }
     }
     Tensor out = node(target, layout, value, device(), std::move(edges), false);
@@ -1020,6 +1006,7 @@ void Tensor::backward() const {
                     check(axis_reduce_axes(dev.h(), g->f32(), c->f32(), (int32_t)r.extents.size(), r.extents.data(),
                                            r.strides.data(), r.metadata.data(), 1.0f),
                           "align_backward");
+                    if (!r.place.empty()) c = dev.select_axis(c, r.place, len);
                     break;
                 }
                 case Rule::MinimumAxis: {

@@ -257,6 +257,34 @@ def test_align_backward_without_plan(ax, device, oracle, extents):
               atol=5e-4, rtol=1e-5)
 
 
+@pytest.mark.parametrize("extents", [(3, 700, 5), (6, 9, 4), (17, 2048, 512)])
+def test_align_backward_permuted_operand(ax, device, oracle, extents):
+    """A [c, a] operand (axes in the other order than the output's [a, b, c]) broadcast over b: the
+    reverse plan's grouped sum lands in the operand's own c-major layout -- bit-identical to the
+    plan, and past the plan's 16,777,216 cap for the last shape."""
+    A, B, C = extents
+    a, b, c = ax.Axis("a"), ax.Axis("b"), ax.Axis("c")
+    rng = np.random.default_rng(A + 1)
+    n = A * B * C
+    xv = rng.standard_normal(n).astype(np.float32)
+    wv = rng.standard_normal(n).astype(np.float32)
+    tv = rng.standard_normal(A * C).astype(np.float32)
+    x = ax.Tensor.from_slice(xv, [a.of(A), b.of(B), c.of(C)], device)
+    w = ax.Tensor.from_slice(wv, [a.of(A), b.of(B), c.of(C)], device)
+    t = ax.Tensor.from_slice(tv, [c.of(C), a.of(A)], device).with_grad()
+    y = x.add(t)
+    close("broadcast add", y.to_vec(), (xv.reshape(A, B, C) + tv.reshape(C, A).T.reshape(A, 1, C)).reshape(-1))
+    y.mul(w).sum([a, b, c]).backward()
+    got = t.grad().to_vec()
+    if n <= 16777216:
+        small = [("c", C), ("a", A)]
+        rev = oracle.align_reverse_plan(small, oracle.contiguous(small), [("a", A), ("b", B), ("c", C)])
+        assert np.array_equal(got, oracle.grouped(wv, None, rev, 1.0))
+    else:
+        close("broadcast gradient", got, wv.reshape(A, B, C).astype(np.float64).sum(axis=1).T.reshape(-1),
+              atol=5e-4, rtol=1e-5)
+
+
 def test_normalized_l2_fixture(ax, device):
     # model/optim.rs:1492-1503
     v = ax.Axis("value")
