@@ -232,11 +232,15 @@ def bench_adam(args):
 def bench_muon(args):
     """wide MLP 4096-8192-8192-4096-1000, batch 4096, inputs N(0,1), labels
     over 1000 classes, He-normal weights; forward, backward, Muon (momentum 0.95, Nesterov, five
-    Newton-Schulz steps) on the four weight matrices and AdamW (wd 0) on the biases."""
+    Newton-Schulz steps) on the four weight matrices and AdamW (wd 0) on the biases.  With --bf16
+    the device rounds every product operand to bf16 (Device::cuda_bf16): the dense products and
+    Newton-Schulz steps run on bf16 matrix cores."""
     import axis_amd
     from axis_amd import hip
     ax = axis_amd.host()
-    device = ax.Device.hip(0)
+    device = ax.Device.hip_bf16(0) if args.bf16 else ax.Device.hip(0)
+    peak = BF16_MFMA_PEAK_TFLOPS if args.bf16 else FP32_MFMA_PEAK_TFLOPS
+    kind = "bf16" if args.bf16 else "fp32"
     lib = hip.load()
     sizes, batch = (4096, 8192, 8192, 4096, 1000), 4096
     bt = ax.Axis("batch")
@@ -277,13 +281,14 @@ def bench_muon(args):
     lib.axis_timing_enable(handle, 0)
     launches, ms, work = _timing(lib, handle, "gemm")
     tflops = work / (ms * 1e-3) / 1e12
-    print(json.dumps({"metric": "wide-MLP Muon training step (ms/step); GEMM % of fp32 MFMA peak",
+    print(json.dumps({"metric": f"wide-MLP Muon training step (ms/step); GEMM % of {kind} MFMA peak",
                       "value": round(elapsed * 1e3 / args.steps, 3), "unit": "ms/step", "n_gpus": 1,
-                      "steps": args.steps, "warmup": args.warmup, "higher_is_better": False, "dtype": "fp32",
+                      "steps": args.steps, "warmup": args.warmup, "higher_is_better": False, "dtype": kind,
                       "data": "synthetic N(0,1) inputs, seeds 1/2/10-13",
-                      "config": {"workload": "BASELINE config 5: MLP 4096-8192-8192-4096-1000, bs4096, MuonWithAuxAdamW"},
-                      "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": FP32_MFMA_PEAK_TFLOPS,
-                                   "unit": "TFLOP/s", "frac": round(tflops / FP32_MFMA_PEAK_TFLOPS, 4),
+                      "config": {"workload": "BASELINE config 5: MLP 4096-8192-8192-4096-1000, bs4096, MuonWithAuxAdamW"
+                                             + (" on a bf16 device" if args.bf16 else "")},
+                      "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": peak,
+                                   "unit": "TFLOP/s", "frac": round(tflops / peak, 4),
                                    "gemm_ms_per_step": round(ms / args.steps, 3),
                                    "gemm_tflop_per_step": round(work / args.steps / 1e12, 3)},
                       "loss": float(loss.item())}))
@@ -328,7 +333,7 @@ def main():
                     help="one device-to-device copy of this size before the timed steps (a known-size "
                          "dispatch that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     ap.add_argument("--bf16", action="store_true",
-                    help="matmul workload: products on a bf16 device (operands rounded to bf16)")
+                    help="matmul / muon workloads: products on a bf16 device (operands rounded to bf16)")
     ap.add_argument("--workload", choices=["cnn", "matmul", "adam", "muon"], default="cnn",
                     help="cnn: the headline metric (BASELINE config 4); the others are configs 2, 3, 5")
     args = ap.parse_args()

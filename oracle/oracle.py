@@ -645,19 +645,22 @@ def normalized_l2(x, epsilon):
     return multiply_scalar(x, inv)
 
 
-def zeroth_power(d, rows, cols):
+def zeroth_power(d, rows, cols, bf16=False):
     """optim.rs:728-752 on a row-major [rows, cols] matrix: X = d/||d||; five times
-    A = X X^T (small side), B = b*A + c*A*A, X = a*X + B*X (transposed when cols < rows)."""
+    A = X X^T (small side), B = b*A + c*A*A, X = a*X + B*X (transposed when cols < rows).
+    bf16: every product takes bf16-rounded operands (Device::cuda_bf16, backend.rs:274-283); the
+    scale-and-add terms stay fp32."""
+    r = bf16_round if bf16 else (lambda v: v)
     x = normalized_l2(d, 1e-7).reshape(rows, cols)
     transposed = rows > cols
     if transposed:
         x = np.ascontiguousarray(x.T)
     s, l = x.shape
     for _ in range(5):
-        gram = matmul(x, np.ascontiguousarray(x.T), 1, s, l, s).reshape(s, s)
-        gram2 = matmul(gram, gram, 1, s, s, s).reshape(s, s)
+        gram = matmul(r(x), r(np.ascontiguousarray(x.T)), 1, s, l, s).reshape(s, s)
+        gram2 = matmul(r(gram), r(gram), 1, s, s, s).reshape(s, s)
         b = binary(scale(gram, float(NS_B)), scale(gram2, float(NS_C)), 0).reshape(s, s)
-        bx = matmul(b, x, 1, s, s, l).reshape(s, l)
+        bx = matmul(r(b), r(x), 1, s, s, l).reshape(s, l)
         x = binary(scale(x, float(NS_A)), bx, 0).reshape(s, l)
     if transposed:
         x = np.ascontiguousarray(x.T)
@@ -668,8 +671,8 @@ class MuonOracle:
     """Muon::prepare/commit (optim.rs:610-678): EMA momentum, Nesterov direction, zeroth power,
     scaled decoupled update.  `fan` maps a parameter to (fan_in, fan_out)."""
 
-    def __init__(self, lr, momentum=0.95, nesterov=True, wd=0.0):
-        self.lr, self.mu, self.nesterov, self.wd = lr, momentum, nesterov, wd
+    def __init__(self, lr, momentum=0.95, nesterov=True, wd=0.0, bf16=False):
+        self.lr, self.mu, self.nesterov, self.wd, self.bf16 = lr, momentum, nesterov, wd, bf16
         self.states = {}
         self.step_count = 0
 
@@ -683,7 +686,7 @@ class MuonOracle:
             m = gw if prev is None else binary(scale(prev, self.mu), gw, 0)
             d = binary(scale(g, float(w)), scale(m, self.mu), 0) if self.nesterov else m
             rows, cols = shapes[name]
-            x = zeroth_power(d, rows, cols)
+            x = zeroth_power(d, rows, cols, self.bf16)
             fan_in, fan_out = fans[name]
             scaling = np.sqrt(max(np.float32(fan_out) / np.float32(fan_in), np.float32(1.0)),
                               dtype=np.float32)

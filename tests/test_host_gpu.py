@@ -434,6 +434,52 @@ def test_mlp_config1_step_bf16_device(ax, oracle):
             check_first_adam_step(oracle, key, v, g, ref["initial"][key], ref["grads"][key], ref["params"][key])
 
 
+@pytest.mark.parametrize("rows,cols", [(64, 96), (160, 48)])
+def test_muon_steps_bf16_device(ax, oracle, rows, cols):
+    """Two Muon steps (optim.rs:610-678) on a Device.hip_bf16 handle: every Newton-Schulz product
+    runs on the bf16 matrix-core path with bf16-rounded operands; the scale-and-add terms, momentum
+    and the update stay fp32.  Five bf16 iterations amplify single operand rounding flips (the
+    quintic keeps singular values oscillating in a band): the oracle's own result moves by 0.1-2%
+    when its input changes by one ulp, so two accumulation orders agree only to that level.  Hence:
+    the momentum exactly; the update exactly as the oracle's formula applied to this device's own
+    zeroth power of the same direction; that zeroth power nearer the oracle's bf16 restatement
+    than the fp32 products are.  test_bf16_newton_schulz_iterations pins each iteration to 2e-4."""
+    device = ax.Device.hip_bf16(0)
+    r, c = ax.Axis("row"), ax.Axis("column")
+    n = rows * cols
+    rng = np.random.default_rng(rows * cols)
+    initial = rng.standard_normal(n).astype(np.float32) * np.float32(0.05)
+    grads = [rng.standard_normal(n).astype(np.float32) for _ in range(2)]
+    param = ax.Parameter(ax.Tensor.from_slice(initial, [r.of(rows), c.of(cols)], device))
+    model = ax.ParameterList([("weight", param)])
+    lr, mu, wd = 0.04, 0.8, 0.03
+    opt = ax.Muon([ax.MuonMatrix.fan_in_fan_out(param)], lr, mu, True, wd)
+    ref = oracle.MuonOracle(lr, mu, True, wd, bf16=True)
+    w = float(np.float32(1.0) - np.float32(mu))
+    scaling = float(np.sqrt(max(np.float32(cols) / np.float32(rows), np.float32(1.0)), dtype=np.float32))
+    for g in grads:
+        param.zero_grad()
+        # a gradient of about g: d/dp mean(p * g * n); the oracle takes the gradient the tape produced
+        gt = ax.Tensor.from_slice(g * np.float32(n), [r.of(rows), c.of(cols)], device)
+        param.tensor().mul(gt).mean([r, c]).backward()
+        g_now = param.grad().to_vec()
+        before = param.tensor().to_vec()
+        opt.step(model)
+        got = param.tensor().to_vec()
+        ref.step({"w": before}, {"w": g_now}, {"w": (rows, cols)}, {"w": (rows, cols)})
+        m = ref.states["w"]
+        assert np.array_equal(np.asarray(opt.momentum_state(param), np.float32), m)
+        d = oracle.binary(oracle.scale(g_now, w), oracle.scale(m, mu), 0)
+        ns = ax.zeroth_power(ax.Tensor.from_slice(d, [r.of(rows), c.of(cols)], device)).to_vec()
+        decayed = oracle.scale(before, float(np.float32(1.0) - np.float32(lr) * np.float32(wd)))
+        expect = oracle.binary(decayed, oracle.scale(ns, float(np.float32(lr) * np.float32(scaling))), 1)
+        assert np.array_equal(got, expect)
+        ns_bf, ns_32 = oracle.zeroth_power(d, rows, cols, True), oracle.zeroth_power(d, rows, cols, False)
+        err = np.linalg.norm(ns - ns_bf) / np.linalg.norm(ns_bf)
+        gap = np.linalg.norm(ns_32 - ns_bf) / np.linalg.norm(ns_bf)
+        assert err < gap, (err, gap)
+
+
 def build_cnn(ax, device, batch, size, classes, ch):
     bt, c0, h, w = ax.Axis("batch"), ax.Axis("channel"), ax.Axis("height"), ax.Axis("width")
     cs = [c0] + [ax.Axis(f"c{j + 1}") for j in range(3)]

@@ -637,6 +637,39 @@ def test_bf16_batched_products_and_axpby(dev_bf16, oracle, batch, m, k, n):
     assert np.array_equal(dev_bf16.read(fused, batch * m * n).view(np.uint32), expect.astype(np.float32).view(np.uint32))
 
 
+@pytest.mark.parametrize("s,l", [(64, 96), (48, 160)])
+def test_bf16_newton_schulz_iterations(dev_bf16, oracle, s, l):
+    """The Newton-Schulz iteration of Muon's fused path (optim.rs:728-752; gram through the NT
+    product, both scale-and-adds in axpby epilogues) on a bf16 handle, one iteration at a time
+    from the GPU's own state: each matches the oracle's bf16 iteration (operands of every product
+    rounded, fp32 terms) to 2e-5 of its norm (measured: at most 3e-6), while one fp32 iteration from
+    the same state lies about 1e-4 away -- four times the error at least."""
+    rng = np.random.default_rng(s * l)
+    x = oracle.normalized_l2(rng.standard_normal(s * l).astype(np.float32), 1e-7)
+    R = oracle.bf16_round
+    A, B, C = float(oracle.NS_A), float(oracle.NS_B), float(oracle.NS_C)
+
+    def step(xh, r):
+        xm = xh.reshape(s, l)
+        gram = oracle.matmul(r(xm), r(np.ascontiguousarray(xm.T)), 1, s, l, s)
+        b = oracle.binary(oracle.scale(gram, B), oracle.scale(oracle.matmul(r(gram), r(gram), 1, s, s, s), C), 0)
+        return oracle.binary(oracle.scale(xh, A), oracle.matmul(r(b), r(xh), 1, s, s, l), 0)
+
+    X = up(dev_bf16, x)
+    for _ in range(5):
+        xh = dev_bf16.read(X, s * l)
+        gram, b, nx = dev_bf16.empty(s * s), dev_bf16.empty(s * s), dev_bf16.empty(s * l)
+        dev_bf16.call("axis_matmul_left_backward", X.vp, X.vp, gram.vp, I64(1), I64(s), I64(s), I64(l))
+        dev_bf16.call("axis_matmul_axpby", gram.vp, gram.vp, gram.vp, b.vp, I64(1), I64(s), I64(s), I64(s), F32(C), F32(B))
+        dev_bf16.call("axis_matmul_axpby", b.vp, X.vp, X.vp, nx.vp, I64(1), I64(s), I64(s), I64(l), F32(1.0), F32(A))
+        X = nx
+        got = dev_bf16.read(X, s * l)
+        want, want32 = step(xh, R), step(xh, lambda v: v)
+        err = np.linalg.norm(got - want) / np.linalg.norm(want)
+        gap = np.linalg.norm(want32 - want) / np.linalg.norm(want)
+        assert err < 2e-5 and gap > 4 * max(err, 1e-5), (err, gap)
+
+
 def test_bf16_products_carry_inf_and_nan(dev_bf16):
     # a NaN operand stays NaN after rounding, an infinity stays infinite: rows meeting them turn
     # NaN / inf exactly as the fp32 product of the rounded operands does
