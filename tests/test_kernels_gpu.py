@@ -670,6 +670,32 @@ def test_bf16_newton_schulz_iterations(dev_bf16, oracle, s, l):
         assert err < 2e-5 and gap > 4 * max(err, 1e-5), (err, gap)
 
 
+@pytest.mark.parametrize("m,k,n", [(4096, 4096, 4096), (8192, 784, 1024)])
+def test_bf16_backward_at_config2_sizes(dev_bf16, oracle, m, k, n):
+    """BASELINE config 2's shapes on a bf16 handle (the bench's workload): 16 sampled rows of dX and
+    16 sampled columns of dW against float64 products of the bf16-rounded operands."""
+    rng = np.random.default_rng(k)
+    x = rng.standard_normal(m * k).astype(np.float32)
+    w = rng.standard_normal(k * n).astype(np.float32)
+    dy = rng.standard_normal(m * n).astype(np.float32)
+    X, W, DY = up(dev_bf16, x), up(dev_bf16, w), up(dev_bf16, dy)
+    dx, dw = dev_bf16.empty(m * k), dev_bf16.empty(k * n)
+    geo = (I64(1), I64(m), I64(k), I64(n))
+    dev_bf16.call("axis_matmul_left_backward", DY.vp, W.vp, dx.vp, *geo)
+    dev_bf16.call("axis_matmul_right_backward", X.vp, DY.vp, dw.vp, *geo)
+    R = oracle.bf16_round
+    rows = np.sort(rng.choice(m, 16, replace=False))
+    cols = np.sort(rng.choice(n, 16, replace=False))
+    rx, rw, rdy = R(x).reshape(m, k), R(w).reshape(k, n), R(dy).reshape(m, n)
+    want_dx = rdy[rows].astype(np.float64) @ rw.astype(np.float64).T
+    want_dw = rx.astype(np.float64).T @ rdy[:, cols].astype(np.float64)
+    got_dx = dev_bf16.read(dx, m * k).reshape(m, k)[rows]
+    got_dw = dev_bf16.read(dw, k * n).reshape(k, n)[:, cols]
+    for got, want in ((got_dx, want_dx), (got_dw, want_dw)):
+        # fp32 accumulation of exact bf16 products over n (dX) or m (dW) terms
+        assert rel_err(got, want) < 1e-5
+
+
 def test_bf16_products_carry_inf_and_nan(dev_bf16):
     # a NaN operand stays NaN after rounding, an infinity stays infinite: rows meeting them turn
     # NaN / inf exactly as the fp32 product of the rounded operands does
