@@ -8,8 +8,8 @@
 // LDS transpose so both the fp32 reads and the bf16 writes stay coalesced.
 //
 // Product: 256 threads (2 x 2 waves) per BM x BN tile, 64-deep LDS stages of both operands in
-// two LDS buffers, each stage loaded into registers two stages ahead of its use and fed to
-// v_mfma_f32_16x16x32_bf16.
+// two LDS buffers; the next stage streams straight into the idle buffer (buffer_load ... lds)
+// while the current one feeds v_mfma_f32_16x16x32_bf16, then one wait and one barrier per stage.
 #include <algorithm>
 #include <type_traits>
 
@@ -98,16 +98,15 @@ __device__ __forceinline__ const uint16_t *uniform_ptr(const uint16_t *p) {
     return reinterpret_cast<const uint16_t *>(((uint64_t)hi << 32) | lo);
 }
 
-// records = 0 makes every load of the resource read zero without touching memory.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const uint16_t *base, int records = 0x7fffffff) {
-    return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, records, 0x00020000);
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const uint16_t *base) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, 0x7fffffff, 0x00020000);
 }
 
 // LDS layout of one operand's stage of depth BK: row t (BK reduction elements, unpadded) at
 // t * BK, its 16-byte chunk c at chunk position c ^ Layout<BK>::swizzle(t).  With these swizzles
-// an MFMA operand read (16 consecutive rows, one chunk) and a stage store (whole rows) meet no
-// bank conflict (SQ_LDS_BANK_CONFLICT reads 0, against 2.7 cycles per LDS instruction for 64-deep
-// rows at a 144-byte padded pitch).  A swizzle depends on t % 16 only, so the rows 16 i apart
+// an MFMA operand read (16 consecutive rows, one chunk) meets no bank conflict
+// (SQ_LDS_BANK_CONFLICT reads 0, against 2.7 cycles per LDS instruction for 64-deep rows at a
+// 144-byte padded pitch).  A swizzle depends on t % 16 only, so the rows 16 i apart
 // that one lane reads share it.
 template <int BK>
 struct Layout {
@@ -135,38 +134,38 @@ __device__ __forceinline__ float finish(const float *bias, const float *d, float
     return v;
 }
 
-// Rows [t0, t0 + BT) of a staged operand, one BK-deep stage: CH 16-byte chunks per thread,
-// chunk idx = tid + 256 e at row idx / (BK / 8), chunk idx % (BK / 8).  The registers a stage
-// lands in belong to the caller, so two stages can be in flight.
-template <int BT, int BK>
-struct StageLoader {
-    using Lay = Layout<BK>;
-    static constexpr int CH = BT * BK / 8 / 256;
-    uint32_t off[CH];  // byte offset from the stage's row-0 origin, or kOutside
+// Rows [t0, t0 + BT) of a staged operand, one 64-deep stage, loaded straight into LDS: one
+// buffer_load ... lds moves 16 bytes per lane to the wave's M0 base + 16 * lane (checked on the
+// device), with no registers or LDS store instructions in between.  Instruction q of a stage fills
+// rows 8q..8q+7 (1 KB); lane i writes row 8q + i/8 at chunk position i % 8, so it loads that row's
+// chunk (i % 8) ^ ((i / 8) & 7), the swizzled layout above.  Rows past the operand's end read
+// out of range; they only reach output rows or columns that are never stored.
+template <int BT>
+struct DirectLoader {
+    static_assert(axis::kBf16Depth == 64, "eight 16-byte chunks per staged row");
+    static constexpr int CH = BT * 64 / 8 / 256;  // instructions per wave and stage
+    uint32_t off[CH];
     const uint16_t *base;
-
+    int wave;
     __device__ __forceinline__ void init(const uint16_t *b, int64_t t0, int64_t rows, int64_t kp, int tid) {
         base = uniform_ptr(b + t0 * kp);
+        wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const int i = tid & 63;
 #pragma unroll
         for (int e = 0; e < CH; ++e) {
-            const int idx = tid + e * 256;
-            const int row = idx / Lay::chunks;
-            off[e] = t0 + row < rows ? (uint32_t)((row * kp + (idx % Lay::chunks) * 8) * 2) : kOutside;
+            const int q = e * 4 + wave;
+            const int row = 8 * q + (i >> 3);
+            const int c = (i & 7) ^ ((i >> 3) & 7);
+            off[e] = t0 + row < rows ? (uint32_t)((row * kp + c * 8) * 2) : kOutside;
         }
     }
-    // live == false (a stage past the end) issues the same loads against an empty resource, so
-    // every path has the same loads in flight and the waits before the LDS writes stay exact.
-    __device__ __forceinline__ void load(int64_t r0, u32x4 *reg, bool live = true) const {
-        const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(uniform_ptr(base + (live ? r0 : 0)), live ? 0x7fffffff : 0);
-#pragma unroll
-        for (int e = 0; e < CH; ++e)
-            reg[e] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off[e], 0, 0));
-    }
-    static __device__ __forceinline__ void store(uint16_t *lds, int tid, const u32x4 *reg) {
+    __device__ __forceinline__ void load(int64_t r0, uint16_t *stage) const {
+        const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(uniform_ptr(base + r0));
 #pragma unroll
         for (int e = 0; e < CH; ++e) {
-            const int idx = tid + e * 256;
-            *reinterpret_cast<u32x4 *>(lds + Lay::at(idx / Lay::chunks, idx % Lay::chunks)) = reg[e];
+            const int q = e * 4 + wave;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rsrc, (__attribute__((address_space(3))) void *)(stage + q * 512), 16, off[e], 0, 0, 0);
         }
     }
 };
@@ -223,22 +222,17 @@ __global__ void __launch_bounds__(256, 2) bf16_gemm_kernel(KernelArgs a) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    using LX = StageLoader<BM, BK>;
-    using LY = StageLoader<BN, BK>;
+    using LX = DirectLoader<BM>;
+    using LY = DirectLoader<BN>;
     LX lx;
     LY ly;
     lx.init(g.x + batch * g.x_batch, i0, g.m, g.kp, tid);
     ly.init(g.y + batch * g.y_batch, j0, g.n, g.kp, tid);
-    // Two register sets: stage s lands in set s % 2, two stages ahead of its use.
-    u32x4 rx[2][LX::CH], ry[2][LY::CH];
-    lx.load(r_begin, rx[0], stages > 0);
-    ly.load(r_begin, ry[0], stages > 0);
-    lx.load(r_begin + BK, rx[1], stages > 1);
-    ly.load(r_begin + BK, ry[1], stages > 1);
     if (stages > 0) {
-        LX::store(lds, tid, rx[0]);
-        LY::store(lds + BM * LDK, tid, ry[0]);
+        lx.load(r_begin, lds);
+        ly.load(r_begin, lds + BM * LDK);
     }
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
     // v_mfma_f32_16x16x32_bf16: lane l supplies row l % 16 of A and column l % 16 of B at
@@ -275,19 +269,18 @@ __global__ void __launch_bounds__(256, 2) bf16_gemm_kernel(KernelArgs a) {
             __builtin_amdgcn_sched_barrier(0);
         }
     };
-    // Stage s: loads of stage s + 2 go into the register set stage s came from, stage s is
-    // computed from LDS buffer s % 2, stage s + 1 moves from registers into the other buffer
-    // (whose stage s - 1 every wave finished before the last barrier), then one barrier.
+    // Stage s: stage s + 1 streams into the other buffer (whose stage s - 1 every wave finished
+    // before the last barrier) while stage s is computed; then its loads are waited for and one
+    // barrier makes it visible to every wave.
     auto step = [&](int s, auto parity) {
         constexpr int P = decltype(parity)::value;
         const int64_t r0 = r_begin + (int64_t)s * BK;
-        lx.load(r0 + 2 * BK, rx[P], s + 2 < stages);
-        ly.load(r0 + 2 * BK, ry[P], s + 2 < stages);
-        compute(lds + P * kBuf);
         if (s + 1 < stages) {
-            LX::store(lds + (P ^ 1) * kBuf, tid, rx[P ^ 1]);
-            LY::store(lds + (P ^ 1) * kBuf + BM * LDK, tid, ry[P ^ 1]);
+            lx.load(r0 + BK, lds + (P ^ 1) * kBuf);
+            ly.load(r0 + BK, lds + (P ^ 1) * kBuf + BM * LDK);
         }
+        compute(lds + P * kBuf);
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
     };
     for (int s = 0; s < stages; s += 2) {
