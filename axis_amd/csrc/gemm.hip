@@ -1010,7 +1010,7 @@ int run_gemm_bf16(axis_device device, const GemmParams &p, int64_t batch, float 
         return st;
     if (int st = axis::stage_bf16(device, {p.y, p.y_batch, p.y_sj, p.y_sr}, yb, p.n, p.k, kp, sy.as<uint16_t>()))
         return st;
-    const axis::Bf16Tile tile = axis::bf16_gemm_tile(p.m, p.n, batch, device->multiprocessors);
+    const axis::Bf16Tile tile = axis::bf16_gemm_tile(p.m, p.n, batch, kp, device->multiprocessors);
     const int64_t tiles = ((p.m + tile.rows - 1) / tile.rows) * ((p.n + tile.cols - 1) / tile.cols) * batch;
     const int64_t slots = device->multiprocessors * 2;
     const int64_t out_len = batch * p.m * p.n;

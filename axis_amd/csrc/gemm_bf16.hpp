@@ -43,9 +43,10 @@ struct Bf16Tile {
     int rows, cols;  // output rows (of X) and columns (of Y) per block
 };
 
-// Output tile for a device with `cus` compute units: 128 x 128 unless the output has too few of
-// them to fill the chip, then 64 x 64.
-Bf16Tile bf16_gemm_tile(int64_t m, int64_t n, int64_t batch, int64_t cus);
+// Output tile for a device with `cus` compute units and a reduction padded to kp: 128 x 128
+// unless the output has too few of them to fill the chip and the reduction is too short to be
+// split into slices (under 8 stages), then 64 x 64.
+Bf16Tile bf16_gemm_tile(int64_t m, int64_t n, int64_t batch, int64_t kp, int64_t cus);
 
 // C[b][i][j] = sum_r X[b][i][r] Y[b][j][r] with `tile` from bf16_gemm_tile; slice s of a split
 // reduction covers r in [s * k_chunk, (s + 1) * k_chunk) and lands at c + s * c_split.
