@@ -794,14 +794,37 @@ def cnn_inputs(batch=256, size=64, classes=1000, channels=CNN_CHANNELS, x_seed=1
     return x, y.reshape(-1), params
 
 
-def cnn_forward_backward(x, y, params, batch=256, size=64, classes=1000, channels=CNN_CHANNELS):
+def _decision_masks(argmax, pooled, batch, hh, ww, cout):
+    """The pool's winner mask in the unfolded window layout [channel, batch, oh, ow, pool] and a
+    ReLU sign array in the activation layout [batch, h, w, channel] from one forward's decisions:
+    `argmax` [batch, oh, ow, channel] window-local winners (ky*2 + kx) and `pooled` its pooled
+    values (the winner's ReLU is positive exactly when the pooled value is)."""
+    am = np.asarray(argmax, np.uint8).reshape(batch, hh // 2, ww // 2, cout)
+    pos = np.asarray(pooled, np.float32).reshape(am.shape) > 0
+    mask = (am.transpose(3, 0, 1, 2)[..., None] == np.arange(4, dtype=np.uint8)).astype(np.float32)
+    sign = np.zeros((batch, hh // 2, 2, ww // 2, 2, cout), np.float32)
+    for p in range(4):
+        sign[:, :, p // 2, :, p % 2, :] = (am == p) & pos
+    return mask.reshape(-1), sign.reshape(-1)
+
+
+def cnn_forward_backward(x, y, params, batch=256, size=64, classes=1000, channels=CNN_CHANNELS,
+                         decisions=None, return_decisions=False):
     """convolution.rs:211-235 (Conv2d) + ReLU + convolution.rs:1334-1370 (MaxPool2d as
     -min(-unfold(x, -inf))) per block, mean over [H, W], Linear, mean categorical
-    cross-entropy; then the reverse sweep of tensor.rs:5591-5718 rule by rule."""
+    cross-entropy; then the reverse sweep of tensor.rs:5591-5718 rule by rule.
+
+    `decisions` (optional, one ``(argmax, pooled)`` pair per block, laid out [batch, oh, ow,
+    channel]) replaces the backward's discrete choices -- each pool window's winner and the ReLU
+    sign at it -- with those of another fp32 forward of the same step.  Two fp32 forwards that
+    accumulate in different orders can break a near-tie (two window values, or a pre-activation
+    and zero, within rounding) differently, which moves a whole gradient term; replaying one set
+    of decisions leaves the arithmetic as the only difference.  `return_decisions` also returns
+    this forward's own decisions in that form (argmax 255 where a window has no finite value)."""
     dims = [("batch", batch), ("channel", channels[0]), ("height", size), ("width", size)]
     strides = contiguous(dims)
     h = x
-    saved = []
+    saved, made = [], []
     for j in range(3):
         cin, cout = channels[j], channels[j + 1]
         conv = unfold_spec(dims, strides, "channel" if j == 0 else f"c{j}", ["height", "width"],
@@ -825,7 +848,14 @@ def cnn_forward_backward(x, y, params, batch=256, size=64, classes=1000, channel
         out_dims, forward, reverse = min_plans(pool.shape, pool.strides, "pool", cap=False)
         mn, mask, _ = grouped_minimum(qn, forward, reverse)
         h = scale(mn, -1.0)
-        saved.append(dict(conv=conv, patches=patches, zb=zb, m=m, pool=pool, mask=mask,
+        relu_sign = zb
+        if return_decisions:
+            won = mask.reshape(cout, batch, hh // 2, ww // 2, 4)
+            own = np.where(won.any(-1), won.argmax(-1), 255).astype(np.uint8).transpose(1, 2, 3, 0)
+            made.append((np.ascontiguousarray(own), h.copy()))
+        if decisions is not None:
+            mask, relu_sign = _decision_masks(decisions[j][0], decisions[j][1], batch, hh, ww, cout)
+        saved.append(dict(conv=conv, patches=patches, zb=relu_sign, m=m, pool=pool, mask=mask,
                           reverse=reverse, in_len=shape_len(dims), a_len=len(a)))
         dims, strides = out_dims, contiguous(out_dims)
     # global average pool: mean over [height, width] of [batch, 8, 8, 256]
@@ -856,6 +886,8 @@ def cnn_forward_backward(x, y, params, batch=256, size=64, classes=1000, channel
         if j > 0:
             dp = matmul_left_backward(g, params[f"conv{j}.weight"], 1, s["m"], cin * 9, cout)
             g = unfold2d_backward(dp, s["conv"], s["in_len"])
+    if return_decisions:
+        return loss, grads, made
     return loss, grads
 
 

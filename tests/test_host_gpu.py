@@ -378,6 +378,12 @@ def check_first_adam_step(oracle, name, v, g, p0, g_ref, p_ref, lr=1e-3):
     assert sure.any(), name
     assert rel_max(v[sure], p_ref[sure]) < 1e-5, name
     assert np.abs(v - p_ref).max() <= 2.0 * lr * 1.0001, name
+    # Returned for the record: the fraction of parameters held only to the 2 lr bound, and the
+    # fraction that actually miss 1e-5 of the tensor's range (all of them with gradients too small
+    # for the first step's lr * g / (|g| + eps) to be fixed by the gradient's accuracy).
+    miss = np.abs(np.asarray(v, np.float64) - p_ref) > 1e-5 * np.abs(np.asarray(p_ref, np.float64)).max()
+    assert not (miss & sure).any(), name
+    return float(1.0 - sure.mean()), float(miss.mean())
 
 
 def test_mlp_config1_step_matches_oracle(ax, device, oracle):
@@ -529,37 +535,6 @@ def test_cnn_small_batch_step_matches_oracle(ax, device, oracle):
         v = model.parameter(ours).tensor().to_vec()
         check_first_adam_step(oracle, theirs, v, g, ref["initial"][theirs], ref["grads"][theirs],
                               ref["params"][theirs])
-
-
-def test_cnn_full_config_invariants(ax, device, oracle):
-    # BASELINE config 4 at its real shape: bs256, 64x64x3.  Size-independent properties: the
-    # loss of the He-initialised model is near ln(1000); every gradient is finite; each bias
-    # gradient equals the column sums of its layer's pre-bias gradient (checked via the final
-    # linear: d bias = sum_rows (p - y) / batch must sum to 0 over classes); and the Adam step
-    # moves every parameter by at most lr * (1 + eps-scale).
-    batch, size, classes, ch = 256, 64, 1000, (3, 64, 128, 256)
-    x_host, y_host, params = oracle.cnn_inputs(batch, size, classes, ch)
-    model, features, head, bt, c0, h, w, cls = build_cnn(ax, device, batch, size, classes, ch)
-    mapping = {f"0.{3 * j}.weight": f"conv{j}.weight" for j in range(3)}
-    mapping.update({f"0.{3 * j}.bias": f"conv{j}.bias" for j in range(3)})
-    mapping["1.weight"], mapping["1.bias"] = "linear.weight", "linear.bias"
-    for ours, theirs in mapping.items():
-        model.parameter(ours).set_values(params[theirs])
-    x = ax.Tensor.from_slice(x_host, [bt.of(batch), c0.of(3), h.of(size), w.of(size)], device)
-    y = ax.Tensor.from_slice(y_host, [bt.of(batch), cls.of(classes)], device)
-    loss = head.forward(features.forward(x).mean([h, w])).categorical_cross_entropy_with_logits(y, cls).mean([bt])
-    loss.backward()
-    assert np.isfinite(loss.item()) and abs(loss.item() - math.log(1000)) < 3.0
-    grads = {ours: model.parameter(ours).grad().to_vec() for ours in mapping}
-    trainer = ax.Trainer(ax.Adam(1e-3))
-    trainer.step(model, lambda m: head.forward(features.forward(x).mean([h, w]))
-                 .categorical_cross_entropy_with_logits(y, cls).mean([bt]))
-    for ours in mapping:
-        g = grads[ours]
-        assert np.all(np.isfinite(g)) and np.abs(g).max() > 0, ours
-        delta = np.abs(model.parameter(ours).tensor().to_vec() - params[mapping[ours]])
-        assert delta.max() <= 1e-3 * 1.0001, ours
-    assert abs(float(grads["1.bias"].astype(np.float64).sum())) < 1e-5
 
 
 # ---------------------------------------------------------------- convolution block lowerings

@@ -393,3 +393,174 @@ def test_cnn_small_matches_torch_float64_autograd(oracle):
         assert np.abs(grads[f"conv{j}.bias"] - gb).max() <= 1e-4 * np.abs(gb).max() + 1e-7
     gl = tp["linear.weight"].grad.numpy().reshape(-1)
     assert np.abs(grads["linear.weight"] - gl).max() <= 1e-4 * np.abs(gl).max()
+
+
+# ---------------------------------------------------------------- pins for the remaining oracle functions
+
+def test_softmax_backward_matches_torch_autograd(oracle):
+    # backend.rs:2529-2543 against torch's float64 softmax vector-Jacobian product (an independent
+    # implementation): rows of logits with spread and with a dominant entry
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(21)
+    rows, width = 37, 129
+    z = torch.tensor(rng.standard_normal((rows, width)) * 3.0, dtype=torch.float64, requires_grad=True)
+    with torch.no_grad():
+        z[5, 7] += 40.0
+    p = torch.softmax(z, dim=1)
+    g = rng.standard_normal((rows, width))
+    (vjp,) = torch.autograd.grad(p, z, torch.from_numpy(g))
+    got = oracle.softmax_backward(g.astype(np.float32), p.detach().numpy().astype(np.float32), rows, width)
+    ref = vjp.numpy()
+    err = np.abs(got.reshape(rows, width) - ref)
+    assert np.all(err <= 1e-6 + 1e-5 * np.abs(ref)), float(err.max())
+    # a dropped "- sum(g p)" term or a sign error would not pass
+    wrong = p.detach().numpy() * g
+    assert np.abs(wrong - ref).max() > 1e-2
+
+
+def _brute_extreme(values, groups, maximum):
+    out, winners = [], []
+    for members in groups:
+        best, win = None, -1
+        for i in members:
+            v = values[i]
+            if not np.isfinite(v):
+                continue
+            if best is None or (v > best if maximum else v < best):
+                best, win = v, i
+        out.append(np.nan if best is None else best)
+        winners.append(win)
+    return np.array(out, np.float32), np.array(winners, np.int32)
+
+
+def test_grouped_maximum_first_strictly_greater_finite(oracle):
+    # backend.rs:3059-3099: first strictly greater finite value in plan order, NaN and -1 for a group
+    # with none; brute force over shuffled member orders with ties, NaN and infinities, and the
+    # identity max(x) = -min(-x) with the minimum pinned by the max-pool fixtures
+    rng = np.random.default_rng(8)
+    n, count = 600, 97
+    values = rng.integers(-4, 5, n).astype(np.float32)
+    values[rng.choice(n, 40, replace=False)] = np.nan
+    values[rng.choice(n, 20, replace=False)] = np.inf
+    values[rng.choice(n, 20, replace=False)] = -np.inf
+    owner = rng.integers(0, count, n)
+    owner[:8] = count - 1  # a group whose members are all non-finite
+    values[:8] = [np.nan, np.inf, -np.inf, np.nan, np.inf, np.nan, -np.inf, np.nan]
+    values[np.isin(owner, [count - 1]) & (np.arange(n) >= 8)] = np.nan
+    groups = [list(rng.permutation(np.flatnonzero(owner == gi))) for gi in range(count)]
+    forward = oracle.plan_groups([[(int(i), 0) for i in members] for members in groups], cap=False)
+    reverse = oracle.plan_gather(owner)
+    out, mask, winners = oracle.grouped_minimum(values, forward, reverse, maximum=True)
+    want, want_w = _brute_extreme(values, groups, True)
+    assert np.array_equal(out, want, equal_nan=True)
+    assert np.array_equal(winners, want_w)
+    assert np.isnan(out[count - 1]) and winners[count - 1] == -1
+    expect_mask = np.zeros(n, np.float32)
+    expect_mask[want_w[want_w >= 0]] = 1.0
+    assert np.array_equal(mask, expect_mask)
+    mn, _, mn_w = oracle.grouped_minimum(-values, forward, reverse)
+    assert np.array_equal(out, -mn, equal_nan=True) and np.array_equal(winners, mn_w)
+
+
+def _select_metadata(extents, order, selected):
+    """Dense input laid out in `order` (axis indices, outermost first); output row-major over the
+    kept dims in dim order; (extent, input_stride, output_stride or -1) per dim."""
+    strides = [0] * len(extents)
+    s = 1
+    for d in reversed(order):
+        strides[d] = s
+        s *= extents[d]
+    kept = [d for d in range(len(extents)) if d != selected]
+    out_strides, s = {}, 1
+    for d in reversed(kept):
+        out_strides[d] = s
+        s *= extents[d]
+    md = []
+    for d, e in enumerate(extents):
+        md += [e, strides[d], -1 if d == selected else out_strides[d]]
+    return md, strides
+
+
+@pytest.mark.parametrize("extents,order,selected,coordinate", [
+    ((3, 4, 5), (0, 1, 2), 1, 2), ((3, 4, 5), (2, 0, 1), 0, 1), ((2, 3, 4, 5), (3, 1, 0, 2), 2, 3),
+    ((6, 1, 7), (1, 2, 0), 2, 6)])
+def test_select_axis_pair_against_numpy_and_adjoint(oracle, extents, order, selected, coordinate):
+    # backend.rs:2057-2148: the forward copy against numpy's indexing of the same strided view; the
+    # backward as its adjoint, <select(x), y> = <x, select_backward(y)> in float64, and zero off the
+    # selected coordinate
+    rng = np.random.default_rng(sum(extents) + selected)
+    md, strides = _select_metadata(extents, order, selected)
+    n = int(np.prod(extents))
+    x = rng.standard_normal(n).astype(np.float32)
+    view = np.lib.stride_tricks.as_strided(x, shape=extents, strides=[s * 4 for s in strides])
+    out_len = n // extents[selected]
+    got = oracle.select_axis(x, md, len(extents), coordinate, out_len)
+    assert np.array_equal(got, np.take(view, coordinate, axis=selected).reshape(-1))
+    y = rng.standard_normal(out_len).astype(np.float32)
+    back = oracle.select_axis_backward(y, md, len(extents), coordinate, n)
+    lhs = float(np.dot(got.astype(np.float64), y.astype(np.float64)))
+    rhs = float(np.dot(x.astype(np.float64), back.astype(np.float64)))
+    assert abs(lhs - rhs) <= 1e-12 * max(1.0, abs(lhs))
+    bview = np.lib.stride_tricks.as_strided(back, shape=extents, strides=[s * 4 for s in strides])
+    assert np.array_equal(np.take(bview, coordinate, axis=selected).reshape(-1), y)
+    assert np.count_nonzero(back) == np.count_nonzero(y)
+
+
+def _ns_bf16_float64(d, rows, cols, oracle):
+    """Newton-Schulz with bf16 product operands in float64 arithmetic, every stored intermediate
+    rounded to fp32 as the device's fp32 tensors hold them (optim.rs:728-752; convert_tile +
+    mma of backend.rs:2209-2312).  The bf16 rounding itself is torch's."""
+    import torch
+
+    def f32(v):
+        return np.asarray(v, np.float64).astype(np.float32).astype(np.float64)
+
+    def r(v):
+        return torch.from_numpy(np.asarray(v, np.float32)).to(torch.bfloat16).to(torch.float64).numpy()
+
+    a, b, c = 3.4445, -4.7750, 2.0315
+    x = oracle.normalized_l2(d, 1e-7).astype(np.float64).reshape(rows, cols)
+    if rows > cols:
+        x = x.T.copy()
+    for _ in range(5):
+        gram = f32(r(x) @ r(x).T)
+        gram2 = f32(r(gram) @ r(gram))
+        bm = f32(f32(np.float32(b) * gram.astype(np.float32)) + f32(np.float32(c) * gram2.astype(np.float32)))
+        bx = f32(r(bm) @ r(x))
+        x = f32(f32(np.float32(a) * x.astype(np.float32)) + bx)
+    return (x.T if rows > cols else x).reshape(-1)
+
+
+@pytest.mark.parametrize("rows,cols", [(24, 40), (40, 24)])
+def test_bf16_zeroth_power_matches_float64_restatement(oracle, rows, cols):
+    # the bf16 Newton-Schulz (zeroth_power(..., bf16=True)) against an independent float64
+    # restatement; the fp32 zeroth power of the same input lies far from both, so a product whose
+    # operands were not rounded would not pass
+    rng = np.random.default_rng(rows * cols)
+    d = rng.standard_normal(rows * cols).astype(np.float32)
+    got = oracle.zeroth_power(d, rows, cols, bf16=True).astype(np.float64)
+    want = _ns_bf16_float64(d, rows, cols, oracle)
+    err = np.linalg.norm(got - want) / np.linalg.norm(want)
+    gap = np.linalg.norm(oracle.zeroth_power(d, rows, cols, bf16=False) - want) / np.linalg.norm(want)
+    assert err < 1e-5 and gap > 1e-3, (err, gap)
+
+
+def test_cnn_decision_replay_is_exact_and_used(oracle):
+    # a forward's own pool winners and ReLU signs, replayed, give bit-identical gradients (so the
+    # window and activation layouts of the replay are the forward's); moving one winner changes them
+    batch, size, classes, ch = 2, 16, 10, (3, 8, 16, 32)
+    x, y, params = oracle.cnn_inputs(batch, size, classes, ch)
+    loss, grads, made = oracle.cnn_forward_backward(x, y, params, batch, size, classes, ch,
+                                                    return_decisions=True)
+    assert [d[0].shape for d in made] == [(2, 8, 8, 8), (2, 4, 4, 16), (2, 2, 2, 32)]
+    assert all(np.all(d[0] < 4) for d in made)
+    loss2, grads2 = oracle.cnn_forward_backward(x, y, params, batch, size, classes, ch, decisions=made)
+    assert loss2 == loss
+    for name in grads:
+        assert np.array_equal(grads[name], grads2[name]), name
+    moved = [(a.copy(), p.copy()) for a, p in made]
+    pos = np.argwhere(moved[2][1] > 0)[0]
+    moved[2][0][tuple(pos)] = (moved[2][0][tuple(pos)] + 1) % 4
+    _, grads3 = oracle.cnn_forward_backward(x, y, params, batch, size, classes, ch, decisions=moved)
+    assert not np.array_equal(grads3["conv2.weight"], grads["conv2.weight"])
+    assert np.array_equal(grads3["linear.weight"], grads["linear.weight"])
