@@ -37,6 +37,8 @@ struct axis_device_s {
     };
     std::map<std::string, std::vector<Timed>> timed;
     std::vector<hipEvent_t> spare_events;
+    // This GPU's copy of the allocation-free product's scratch array (gemm.hip), bound at create.
+    float *static_scratch = nullptr;
 };
 
 struct axis_plan_s {
@@ -60,6 +62,7 @@ int enter(axis_device device);  // validates the handle and makes its GPU curren
 int launch_status(const char *kernel);
 int alloc(axis_device device, size_t bytes, void **out);
 void release(axis_device device, void *ptr);
+int bind_static_scratch(axis_device device);  // gemm.hip
 
 // RAII scratch block from the device's caching allocator (returned on scope exit; stream order
 // makes the reuse safe).

@@ -118,7 +118,7 @@ hipEvent_t take_event(axis_device device) {
 }  // namespace
 
 TimedLaunch::TimedLaunch(axis_device d, const char *f, double w) : device(d), family(f), work(w) {
-    if (!device->timing) return;
+    if (!device || !device->timing) return;
     start = take_event(device);
     if (start) (void)hipEventRecord(start, device->stream);
 }
@@ -170,6 +170,11 @@ int axis_device_create(int ordinal, axis_device *out) {
     if (e != hipSuccess) {
         delete device;
         return axis::hip_fail(e, "hipStreamCreateWithFlags");
+    }
+    if (int st = axis::bind_static_scratch(device)) {
+        (void)hipStreamDestroy(device->stream);
+        delete device;
+        return st;
     }
     *out = device;
     return AXIS_OK;

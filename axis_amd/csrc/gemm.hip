@@ -1,4 +1,4 @@
-// fp32 GEMM family on CDNA4 matrix cores (v_mfma_f32_32x32x2_f32) for the reference's
+// fp32 GEMM family on CDNA4 matrix cores (v_mfma_f32_16x16x4_f32) for the reference's
 // matmul / matmul_left_backward / matmul_right_backward (runtime/backend.rs:934-1021,
 // kernels :2190-2290), and implicit-GEMM convolution entries that compute the reference's
 // unfold -> contract (forward), contract-backward -> unfold_backward (dgrad) and
@@ -28,7 +28,9 @@
 // no atomics).
 #include <algorithm>
 #include <cfloat>
+#include <mutex>
 #include <type_traits>
+#include <unordered_map>
 
 #include "common.hpp"
 #include "bf16.hpp"
@@ -41,6 +43,21 @@ namespace {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+// Split partial sums of the allocation-free weight gradient (axis_matmul_right_backward_noalloc).
+// One copy per GPU, alive until the process ends.  Host code never passes this name to a kernel:
+// it is a host-side stand-in, and kernels take the device address hipGetSymbolAddress returns
+// (axis_device_s::static_scratch).  Under the split rule of run_gemm one launch needs at most
+// slots * tile area + its range sums (768 * 128 * 128 + 3% floats on 256 CUs, about 53 MB).
+constexpr int64_t kStaticScratchFloats = int64_t(16) << 20;  // 64 MiB
+static __device__ __align__(256) float scratch[kStaticScratchFloats];
+
+// Device memory a caller hands to run_gemm in place of allocations (split partials, then the
+// range sums of more than 32 slices).
+struct Workspace {
+    float *ptr;
+    int64_t floats;
+};
 
 // Geometry of a gathered convolution operand (tensor [batch, height, width, channels]).
 struct ConvGeom {
@@ -976,7 +993,7 @@ Choice choose(int64_t m, int64_t n, int64_t k, int64_t batch, int64_t cus, bool 
 // of 32 consecutive slices first, then the range sums -- a fixed association for a given count.
 int sum_splits(axis_device device, const float *partial, float *out, int64_t len, int64_t splits,
                const float *bias, int64_t n, const float *d, float alpha, float beta, int32_t perm_c,
-               int32_t perm_taps) {
+               int32_t perm_taps, float *mid_space = nullptr) {
     const unsigned blocks = axis::blocks_for(len, 64, INT32_MAX);
     if (splits <= 32) {
         split_sum_kernel<<<blocks, 256, 0, device->stream>>>(partial, out, len, (int32_t)splits, len, bias, n, d,
@@ -986,11 +1003,15 @@ int sum_splits(axis_device device, const float *partial, float *out, int64_t len
     const int32_t span = 32;
     const int64_t ranges = (splits + span - 1) / span;
     axis::Scratch mid;
-    if (int st = mid.get(device, sizeof(float) * (size_t)(ranges * len))) return st;
+    float *sums = mid_space;
+    if (!sums) {
+        if (int st = mid.get(device, sizeof(float) * (size_t)(ranges * len))) return st;
+        sums = mid.as<float>();
+    }
     dim3 grid(axis::blocks_for(len, 256, INT32_MAX), (unsigned)ranges);
-    split_range_kernel<<<grid, 256, 0, device->stream>>>(partial, mid.as<float>(), len, (int32_t)splits, span);
+    split_range_kernel<<<grid, 256, 0, device->stream>>>(partial, sums, len, (int32_t)splits, span);
     if (int st = axis::launch_status("split_range_kernel")) return st;
-    split_sum_kernel<<<blocks, 256, 0, device->stream>>>(mid.as<float>(), out, len, (int32_t)ranges, len, bias, n,
+    split_sum_kernel<<<blocks, 256, 0, device->stream>>>(sums, out, len, (int32_t)ranges, len, bias, n,
                                                          d, alpha, beta, perm_c, perm_taps);
     return axis::launch_status("split_sum_kernel");
 }
@@ -1052,10 +1073,15 @@ int run_gemm_bf16(axis_device device, const GemmParams &p, int64_t batch, float 
     return AXIS_OK;
 }
 
+// ws: when non-null, the partial sums live there (nothing is allocated, nothing is timed) and a
+// launch whose partials would not fit is rejected before anything runs.
 template <bool XR, bool YR, int XMODE, int EPI>
-int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out) {
+int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out, const Workspace *ws = nullptr) {
     if constexpr (XMODE == 0 && EPI == 0)
-        if (device->bf16_matmul && !p.ytaps.on && !p.perm_c) return run_gemm_bf16(device, p, batch, out);
+        if (device->bf16_matmul && !p.ytaps.on && !p.perm_c) {
+            if (ws) return axis::fail(AXIS_ERROR_INVALID, "the allocation-free product is fp32 only");
+            return run_gemm_bf16(device, p, batch, out);
+        }
     p.bf16 = device->bf16_matmul;
     const int64_t cus = device->multiprocessors;
     const Choice ch = choose(p.m, p.n, p.k, batch, cus, EPI == 1);
@@ -1099,17 +1125,38 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out) {
                        : vec_ok(p.y, p.n, p.y_sr) && p.y_batch % 4 == 0;
 
     axis::Scratch partial, ordered;
+    // spare: the range sums of more than 32 slices, or an unsplit permuted product before its move
+    float *partials = nullptr, *spare = nullptr;
+    if (ws) {
+        const int64_t ranges = splits > 32 ? (splits + 31) / 32 : 0;
+        const int64_t need = (splits > 1 ? splits + ranges : 0) * out_len + (splits == 1 && p.perm_c ? out_len : 0);
+        if (need > ws->floats)
+            return axis::fail(AXIS_ERROR_INVALID, "product needs " + std::to_string(need * 4) +
+                                                      " bytes of partial sums; the static scratch holds " +
+                                                      std::to_string(ws->floats * 4));
+        partials = ws->ptr;
+        spare = ws->ptr + splits * out_len;
+    }
     if (splits > 1) {
-        int status = partial.get(device, sizeof(float) * (size_t)(out_len * splits));
-        if (status) return status;
-        p.c = partial.as<float>();
+        if (!partials) {
+            int status = partial.get(device, sizeof(float) * (size_t)(out_len * splits));
+            if (status) return status;
+            partials = partial.as<float>();
+        }
+        p.c = partials;
         p.c_split = out_len;
         p.c_batch = p.m * p.n;
     } else {
         // an unsplit product with permuted rows is written in its own order, then moved
-        if (p.perm_c)
-            if (int status = ordered.get(device, sizeof(float) * (size_t)out_len)) return status;
-        p.c = p.perm_c ? ordered.as<float>() : out;
+        if (p.perm_c) {
+            if (partials) {
+                spare = partials;
+            } else {
+                if (int status = ordered.get(device, sizeof(float) * (size_t)out_len)) return status;
+                spare = ordered.as<float>();
+            }
+        }
+        p.c = p.perm_c ? spare : out;
         p.c_split = 0;
         p.c_batch = p.m * p.n;
     }
@@ -1117,7 +1164,7 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out) {
     if (blocks >= INT32_MAX) return axis::fail(AXIS_ERROR_INVALID, "matmul too large for one launch");
     p.xcd_span = blocks % 8 == 0 ? (uint32_t)(blocks / 8) : 0u;
     const double k_work = (double)(p.k_work > 0 ? p.k_work : p.k);
-    axis::TimedLaunch timed(device, "gemm", 2.0 * (double)batch * (double)p.m * (double)p.n * k_work);
+    axis::TimedLaunch timed(ws ? nullptr : device, "gemm", 2.0 * (double)batch * (double)p.m * (double)p.n * k_work);
     dim3 grid(static_cast<unsigned>(blocks));
     if constexpr (EPI == 1) {
         if (ch.shape == Shape::Large)
@@ -1135,12 +1182,12 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out) {
     int status = axis::launch_status("gemm_kernel");
     if (status) return status;
     if (splits > 1)
-        status = sum_splits(device, partial.as<float>(), out, out_len, splits, p.bias, p.n, p.d, p.alpha, p.beta,
-                            p.perm_c, p.perm_taps);
+        status = sum_splits(device, partials, out, out_len, splits, p.bias, p.n, p.d, p.alpha, p.beta,
+                            p.perm_c, p.perm_taps, spare);
     else if (p.perm_c) {
         // mode 2 of the weight permutation with the taps as one axis
         conv_weight_permute_kernel<<<axis::blocks_for(out_len, 256, 4096), 256, 0, device->stream>>>(
-            ordered.as<float>(), out, p.perm_c, p.perm_c, (int32_t)p.n, p.perm_taps, 1, 2);
+            spare, out, p.perm_c, p.perm_c, (int32_t)p.n, p.perm_taps, 1, 2);
         status = axis::launch_status("conv_weight_permute_kernel");
     }
     return status;
@@ -1326,6 +1373,27 @@ struct GatherInput {
 
 }  // namespace
 
+namespace axis {
+
+// The device address of this GPU's copy of `scratch`, looked up once per GPU with that GPU
+// current (axis_device_create makes it current before calling this).
+int bind_static_scratch(axis_device device) {
+    static std::mutex guard;
+    static std::unordered_map<int, float *> bound;
+    std::lock_guard<std::mutex> lock(guard);
+    auto it = bound.find(device->ordinal);
+    if (it == bound.end()) {
+        void *address = nullptr;
+        hipError_t e = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+        it = bound.emplace(device->ordinal, static_cast<float *>(address)).first;
+    }
+    device->static_scratch = it->second;
+    return AXIS_OK;
+}
+
+}  // namespace axis
+
 extern "C" {
 
 int axis_matmul(axis_device device, const float *a, const float *b, float *out, int64_t batch,
@@ -1409,6 +1477,28 @@ int axis_matmul_right_backward(axis_device device, const float *lhs, const float
     p.x_batch = m * k;
     p.y_batch = m * n;
     return run_gemm<false, false, 0, 0>(device, p, batch, out);
+}
+
+int axis_matmul_right_backward_noalloc(axis_device device, const float *lhs, const float *gradient,
+                                       float *out, int64_t batch, int64_t m, int64_t k, int64_t n) {
+    AXIS_ENTER(device);
+    if (int s = check_dims(lhs, gradient, out, batch, m, k, n)) return s;
+    AXIS_REQUIRE(!device->bf16_matmul, "the allocation-free product is fp32 only (a bf16 handle stages operands)");
+    AXIS_REQUIRE(device->static_scratch, "static scratch is not bound on this device");
+    GemmParams p{};
+    p.x = lhs;
+    p.y = gradient;
+    p.m = k;
+    p.n = n;
+    p.k = m;
+    p.x_si = 1;
+    p.x_sr = k;
+    p.y_sr = n;
+    p.y_sj = 1;
+    p.x_batch = m * k;
+    p.y_batch = m * n;
+    const Workspace ws{device->static_scratch, kStaticScratchFloats};
+    return run_gemm<false, false, 0, 0>(device, p, batch, out, &ws);
 }
 
 int axis_conv2d_forward(axis_device device, const float *input, const int64_t input_strides_[4],

@@ -105,6 +105,17 @@ int axis_matmul_left_backward(axis_device device, const float *gradient, const f
  * lhs [batch,m,k], gradient [batch,m,n], out [batch,k,n].  Deterministic split over m. */
 int axis_matmul_right_backward(axis_device device, const float *lhs, const float *gradient,
                                float *out, int64_t batch, int64_t m, int64_t k, int64_t n);
+/* No counterpart in the reference.  For callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): the same product as
+ * axis_matmul_right_backward, bit for bit, with its split partial sums in a file-scope 64 MiB
+ * device array (one per GPU, held until the process ends) instead of the caching allocator; it
+ * calls no allocator.  Nothing in the array needs to start at zero.  A product whose partial
+ * sums exceed 64 MiB is rejected before any launch (on MI355X's 256 CUs the split rule never
+ * needs more than about 53 MB); bf16 handles are rejected.  Calls on one GPU share the array:
+ * calls from different handles (streams) on the same GPU that overlap in time race, while calls
+ * on one handle are ordered by its stream. */
+int axis_matmul_right_backward_noalloc(axis_device device, const float *lhs, const float *gradient,
+                                       float *out, int64_t batch, int64_t m, int64_t k, int64_t n);
 
 /* ------------------------------------------------------------------ unfold / fold (im2col) */
 
