@@ -1080,7 +1080,10 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out, const 
     if constexpr (XMODE == 0 && EPI == 0)
         if (device->bf16_matmul && !p.ytaps.on && !p.perm_c) {
             if (ws) return axis::fail(AXIS_ERROR_INVALID, "the allocation-free product is fp32 only");
-            return run_gemm_bf16(device, p, batch, out);
+            const int64_t kp = (p.k + axis::kBf16Depth - 1) / axis::kBf16Depth * axis::kBf16Depth;
+            if (axis::bf16_gemm_fits(p.m, p.n, batch, kp, device->multiprocessors))
+                return run_gemm_bf16(device, p, batch, out);
+            // otherwise the fp32 matrix cores below, rounding the operands to bf16 as they are staged
         }
     p.bf16 = device->bf16_matmul;
     const int64_t cus = device->multiprocessors;

@@ -60,30 +60,36 @@ __global__ void stage_rows_kernel(axis::Bf16Source s, int64_t rows, int64_t k, i
 
 // Operands contiguous along t (s_t == 1): block (tt, rt, b) moves the 64 x 64 tile at
 // t0 = 64 tt, r0 = 64 rt through LDS; reads run along t, writes along r.
-__global__ void __launch_bounds__(256) stage_transpose_kernel(axis::Bf16Source s, int64_t rows, int64_t k,
-                                                              int64_t kp, uint16_t *dst) {
+__global__ void __launch_bounds__(256) stage_transpose_kernel(axis::Bf16Source s, int64_t batch, int64_t rows,
+                                                              int64_t k, int64_t kp, uint16_t *dst) {
     constexpr int PITCH = 66;  // bf16 per LDS row: 2-byte stores of 64 consecutive rows hit distinct banks
     __shared__ uint16_t tile[64 * PITCH];
     const int tid = threadIdx.x;
-    const int64_t t0 = (int64_t)blockIdx.x * 64, r0 = (int64_t)blockIdx.y * 64, b = blockIdx.z;
-    const float *src = s.base + b * s.s_b;
+    const int64_t t0 = (int64_t)blockIdx.x * 64;
     const int tl = tid & 63;
     const int64_t t = t0 + tl;
+    // Reduction tiles and batches past the grid's y / z extents are walked by the same block.
+    for (int64_t b = blockIdx.z; b < batch; b += gridDim.z) {
+        const float *src = s.base + b * s.s_b;
+        for (int64_t r0 = (int64_t)blockIdx.y * 64; r0 < kp; r0 += (int64_t)gridDim.y * 64) {
 #pragma unroll 4
-    for (int e = 0; e < 16; ++e) {
-        const int rl = e * 4 + (tid >> 6);
-        const int64_t r = r0 + rl;
-        tile[tl * PITCH + rl] = (uint16_t)(t < rows && r < k ? bf16_bits(src[t * s.s_t + r * s.s_r]) : 0u);
-    }
-    __syncthreads();
+            for (int e = 0; e < 16; ++e) {
+                const int rl = e * 4 + (tid >> 6);
+                const int64_t r = r0 + rl;
+                tile[tl * PITCH + rl] = (uint16_t)(t < rows && r < k ? bf16_bits(src[t * s.s_t + r * s.s_r]) : 0u);
+            }
+            __syncthreads();
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-        const int idx = tid + e * 256;
-        const int row = idx >> 3, ch = idx & 7;
-        if (t0 + row >= rows) continue;
-        const uint32_t *q = reinterpret_cast<const uint32_t *>(tile + row * PITCH + ch * 8);
-        const u32x4 v = {q[0], q[1], q[2], q[3]};
-        *reinterpret_cast<u32x4 *>(dst + (b * rows + t0 + row) * kp + r0 + ch * 8) = v;
+            for (int e = 0; e < 2; ++e) {
+                const int idx = tid + e * 256;
+                const int row = idx >> 3, ch = idx & 7;
+                if (t0 + row >= rows) continue;
+                const uint32_t *q = reinterpret_cast<const uint32_t *>(tile + row * PITCH + ch * 8);
+                const u32x4 v = {q[0], q[1], q[2], q[3]};
+                *reinterpret_cast<u32x4 *>(dst + (b * rows + t0 + row) * kp + r0 + ch * 8) = v;
+            }
+            __syncthreads();  // the tile is rewritten by the next reduction tile
+        }
     }
 }
 
@@ -319,10 +325,10 @@ int stage_bf16(axis_device device, const Bf16Source &src, int64_t batch, int64_t
                uint16_t *dst) {
     if (kp % kBf16Depth != 0 || kp < k) return fail(AXIS_ERROR_INVALID, "bf16 staging depth must cover k in whole stages");
     if (src.s_t == 1 && src.s_r != 1) {
-        dim3 grid((unsigned)((rows + 63) / 64), (unsigned)(kp / 64), (unsigned)batch);
-        if (rows > (int64_t)64 * INT32_MAX || batch > 65535 || kp / 64 > 65535)
-            return fail(AXIS_ERROR_INVALID, "bf16 staging grid too large");
-        stage_transpose_kernel<<<grid, 256, 0, device->stream>>>(src, rows, k, kp, dst);
+        if (rows > (int64_t)64 * INT32_MAX) return fail(AXIS_ERROR_INVALID, "bf16 staging grid too large");
+        dim3 grid((unsigned)((rows + 63) / 64), (unsigned)std::min<int64_t>(kp / 64, 65535),
+                  (unsigned)std::min<int64_t>(batch, 65535));
+        stage_transpose_kernel<<<grid, 256, 0, device->stream>>>(src, batch, rows, k, kp, dst);
         return launch_status("stage_transpose_kernel");
     }
     const int64_t total = batch * rows * (kp / 8);
@@ -340,6 +346,13 @@ Bf16Tile bf16_gemm_tile(int64_t m, int64_t n, int64_t batch, int64_t kp, int64_t
     // skinny 784 x 1024 x 8192 weight gradient runs 15% faster that way than on 64 x 64 tiles.
     const int64_t large = ((m + 127) / 128) * ((n + 127) / 128) * batch;
     return large * 2 >= cus || kp >= 8 * kBf16Depth ? Bf16Tile{128, 128} : Bf16Tile{64, 64};
+}
+
+bool bf16_gemm_fits(int64_t m, int64_t n, int64_t batch, int64_t kp, int64_t cus) {
+    const Bf16Tile tile = bf16_gemm_tile(m, n, batch, kp, cus);
+    const int64_t tiles = ((m + tile.rows - 1) / tile.rows) * ((n + tile.cols - 1) / tile.cols) * batch;
+    return (int64_t)(std::max(tile.rows, tile.cols) + 1) * kp * 2 < (int64_t(1) << 31) &&
+           std::max<int64_t>(tiles, cus * 2) < INT32_MAX;
 }
 
 int bf16_gemm(axis_device device, const Bf16Gemm &g, int64_t batch, Bf16Tile tile) {

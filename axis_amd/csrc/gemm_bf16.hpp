@@ -48,6 +48,12 @@ struct Bf16Tile {
 // split into slices (under 8 stages), then 64 x 64.
 Bf16Tile bf16_gemm_tile(int64_t m, int64_t n, int64_t batch, int64_t kp, int64_t cus);
 
+// Whether bf16_gemm takes this product: its loads address one tile's staged rows with 32-bit
+// byte offsets, so (tile rows + 1) * kp * 2 must stay below 2^31 (reductions up to about 8.3M).
+// Callers decide before staging anything; a product that does not fit runs on the fp32 matrix
+// cores with its operands rounded to bf16 as they are staged in LDS (the same values).
+bool bf16_gemm_fits(int64_t m, int64_t n, int64_t batch, int64_t kp, int64_t cus);
+
 // C[b][i][j] = sum_r X[b][i][r] Y[b][j][r] with `tile` from bf16_gemm_tile; slice s of a split
 // reduction covers r in [s * k_chunk, (s + 1) * k_chunk) and lands at c + s * c_split.
 int bf16_gemm(axis_device device, const Bf16Gemm &g, int64_t batch, Bf16Tile tile);

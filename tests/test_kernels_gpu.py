@@ -610,7 +610,7 @@ def test_bf16_matmul_family(dev, dev_bf16, oracle, m, k, n):
 
 @pytest.mark.parametrize("batch,m,k,n", [(3, 130, 70, 33), (2, 64, 1000, 200), (1, 1, 9, 1), (1, 4100, 96, 2050)])
 def test_bf16_batched_products_and_axpby(dev_bf16, oracle, batch, m, k, n):
-    # (1, 4100, 96, 2050): enough 256 x 128 output tiles for the largest tile, ragged on both sides
+    # (1, 4100, 96, 2050): enough 128 x 128 output tiles to fill the chip, ragged on both sides
     # batched bf16 products (staged operands per batch, reduction tail padded) and the axpby
     # epilogue: beta * d + alpha * product, each operation rounded on its own
     rng = np.random.default_rng(batch * 1000 + m + k + n)
@@ -694,6 +694,24 @@ def test_bf16_backward_at_config2_sizes(dev_bf16, oracle, m, k, n):
     for got, want in ((got_dx, want_dx), (got_dw, want_dw)):
         # fp32 accumulation of exact bf16 products over n (dX) or m (dW) terms
         assert rel_err(got, want) < 1e-5
+
+
+@pytest.mark.parametrize("m", [4_194_368, 8_400_000])
+def test_bf16_weight_gradient_over_long_reductions(dev_bf16, m):
+    """matmul_right_backward on a bf16 handle reducing over more than 4,194,304 rows (its operands
+    are staged through the LDS transpose, more than 65,535 reduction tiles) and over more than the
+    bf16 kernel's 32-bit offsets reach (about 8.3M: the fp32 matrix cores take the same rounded
+    operands).  Operands in {-1, 0, 1} are exact in bf16 and every partial sum is an integer below
+    2^24, so the result is exact in any summation order."""
+    k = n = 16
+    rng = np.random.default_rng(m)
+    x = rng.integers(-1, 2, m * k).astype(np.float32)
+    g = rng.integers(-1, 2, m * n).astype(np.float32)
+    X, G = up(dev_bf16, x), up(dev_bf16, g)
+    out = dev_bf16.empty(k * n)
+    dev_bf16.call("axis_matmul_right_backward", X.vp, G.vp, out.vp, I64(1), I64(m), I64(k), I64(n))
+    want = x.reshape(m, k).astype(np.float64).T @ g.reshape(m, n).astype(np.float64)
+    assert np.array_equal(dev_bf16.read(out, k * n), want.reshape(-1).astype(np.float32))
 
 
 def test_bf16_products_carry_inf_and_nan(dev_bf16):
