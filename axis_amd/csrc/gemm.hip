@@ -69,6 +69,12 @@ struct ConvGeom {
     int32_t kh, kw, sy, sx, py, px;
     FastDiv c_div, kw_div, ow_div, oh_div;
     bool tap_steps;                   // channels % 32 == 0: a 32-deep K step stays in one tap
+    // With tap steps, the buffer rows loader walks the reduction in 32-channel blocks, every tap
+    // of a block before the next block: r = (cb * taps + pos) * 32 + ci.  A tile then re-reads
+    // the same 32 channels of its neighbourhood on consecutive steps, which stay in L2, instead
+    // of the whole tensor slab between one tap and the next.
+    bool block_major;
+    FastDiv taps_div;                 // kh * kw
     // Rows mode, 2x2 pooling epilogue: tile row t holds position t % 4 (ky major) of the tile's
     // window t / 4, windows numbered row-major over the tile's window rows (pw per row).  A tile
     // starts on an even output row and holds whole window rows.
@@ -92,6 +98,9 @@ struct TapSteps {
     bool on;
     FastDiv r_div;   // R
     int64_t qa, pb, pc;
+    // The rows loader's block-major order: step r0 = (cb * taps + pos) * 32 covers q0 = 32 cb.
+    bool block_major;
+    FastDiv taps_div;
 };
 
 struct GemmParams {
@@ -260,8 +269,17 @@ struct DenseLoader : Staging<BT, BK, NT, RCONTIG, VEC> {
     __device__ __forceinline__ void load(const ConvGeom &, int64_t r0, int64_t r_end, int) {
         int64_t step = r0 * s_r;
         if (taps.on) {
-            const uint32_t pos = taps.r_div.div((uint32_t)r0);
-            const int64_t q0 = r0 - (int64_t)pos * taps.r_div.d;
+            uint32_t pos;
+            int64_t q0;
+            if (taps.block_major) {
+                const uint32_t st = (uint32_t)r0 >> 5;
+                const uint32_t cb = taps.taps_div.div(st);
+                pos = st - cb * taps.taps_div.d;
+                q0 = (int64_t)cb * 32;
+            } else {
+                pos = taps.r_div.div((uint32_t)r0);
+                q0 = r0 - (int64_t)pos * taps.r_div.d;
+            }
             step = q0 * taps.qa + (int64_t)pos * taps.pb + taps.pc;
         }
         const int32_t room = (int32_t)(r_end - r0 < BK ? r_end - r0 : BK);  // k left in this step
@@ -366,8 +384,16 @@ struct ConvRowsBufferLoader : Staging<BT, BK, NT, true, VEC> {
             // r_end is a multiple of BK here, so every k of the step is inside the reduction
             // the step's tap and first channel are wave-uniform: scalar arithmetic, plus the
             // thread's fixed channel offset
-            pos = geom.c_div.div((uint32_t)r0);
-            const int32_t c0 = (int32_t)((uint32_t)r0 - pos * (uint32_t)geom.channels);
+            int32_t c0;
+            if (geom.block_major) {
+                const uint32_t st = (uint32_t)r0 >> 5;
+                const uint32_t cb = geom.taps_div.div(st);
+                pos = st - cb * geom.taps_div.d;
+                c0 = (int32_t)cb * 32;
+            } else {
+                pos = geom.c_div.div((uint32_t)r0);
+                c0 = (int32_t)((uint32_t)r0 - pos * (uint32_t)geom.channels);
+            }
             const int32_t ky = (int32_t)geom.kw_div.div(pos);
             const int32_t kx = (int32_t)pos - ky * geom.kw;
             delta = __builtin_amdgcn_readfirstlane((uint32_t)(ky * geom.ld_h + kx * geom.ld_w + c0 * geom.ld_c)) +
@@ -873,24 +899,44 @@ __global__ void __launch_bounds__(256) split_range_kernel(const float *__restric
 //   mode 0: W'[(ky, kx, c), n] = W[(c, ky, kx), n]                 (forward; rows c >= c_in are 0)
 //   mode 1: W''[(ky', kx', n), c] = W[(c, kh-1-ky', kw-1-kx'), n]   (dgrad, flipped; c_pad == c_in)
 //   mode 2: W[(c, ky, kx), n] = W'[(ky, kx, c), n]                 (wgrad result back; c < c_in)
+// block (modes 0 and 1): the reduction rows in the rows loader's block-major order instead,
+// (cb, ky, kx, ci) with c = 32 cb + ci (mode 0), (nb, ky', kx', ni) with n = 32 nb + ni (mode 1).
+__device__ __forceinline__ void block_row(int64_t r, int32_t taps, int32_t &pos, int32_t &c) {
+    const int32_t ci = (int32_t)(r & 31);
+    const int64_t st = r >> 5;
+    const int32_t cb = (int32_t)(st / taps);
+    pos = (int32_t)(st - (int64_t)cb * taps);
+    c = cb * 32 + ci;
+}
+
 __global__ void __launch_bounds__(256) conv_weight_permute_kernel(const float *__restrict__ src,
                                                                   float *__restrict__ dst, int32_t c_in,
                                                                   int32_t c_pad, int32_t n_out, int32_t kh,
-                                                                  int32_t kw, int32_t mode) {
+                                                                  int32_t kw, int32_t mode, int32_t block = 0) {
     const int64_t total = (int64_t)(mode == 0 ? c_pad : c_in) * kh * kw * n_out;
     for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total;
          idx += (int64_t)gridDim.x * 256) {
         if (mode == 0) {
             const int32_t n = (int32_t)(idx % n_out);
             const int64_t r = idx / n_out;
-            const int32_t c = (int32_t)(r % c_pad);
-            const int32_t pos = (int32_t)(r / c_pad);
+            int32_t c, pos;
+            if (block) {
+                block_row(r, kh * kw, pos, c);
+            } else {
+                c = (int32_t)(r % c_pad);
+                pos = (int32_t)(r / c_pad);
+            }
             dst[idx] = c < c_in ? src[((int64_t)c * kh * kw + pos) * n_out + n] : 0.0f;
         } else if (mode == 1) {
             const int32_t c = (int32_t)(idx % c_in);
             const int64_t r = idx / c_in;
-            const int32_t n = (int32_t)(r % n_out);
-            const int32_t pos = (int32_t)(r / n_out);
+            int32_t n, pos;
+            if (block) {
+                block_row(r, kh * kw, pos, n);
+            } else {
+                n = (int32_t)(r % n_out);
+                pos = (int32_t)(r / n_out);
+            }
             const int32_t ky = pos / kw, kx = pos % kw;
             const int32_t flipped = (kh - 1 - ky) * kw + (kw - 1 - kx);
             dst[idx] = src[((int64_t)c * kh * kw + flipped) * n_out + n];
@@ -1298,6 +1344,8 @@ ConvGeom geom(const float *src, const int64_t ld[4], int32_t height, int32_t wid
     g.ow_div = FastDiv((uint32_t)out_w);
     g.oh_div = FastDiv((uint32_t)out_h);
     g.tap_steps = channels % 32 == 0;
+    g.block_major = false;  // set by launches that take the buffer rows loader (use_block_major)
+    g.taps_div = FastDiv((uint32_t)(kh * kw));
     return g;
 }
 
@@ -1311,11 +1359,18 @@ bool buffer_reach(const ConvGeom &g, int64_t batch) {
 }
 
 int permute_weight(axis_device device, const float *src, float *dst, const ConvShape &s, int mode,
-                   int32_t c_pad) {
+                   int32_t c_pad, bool block = false) {
     const int64_t total = (int64_t)(mode == 0 ? c_pad : s.channels) * s.kh * s.kw * s.out_channels;
     conv_weight_permute_kernel<<<axis::blocks_for(total, 256, 4096), 256, 0, device->stream>>>(
-        src, dst, s.channels, c_pad, s.out_channels, s.kh, s.kw, mode);
+        src, dst, s.channels, c_pad, s.out_channels, s.kh, s.kw, mode, block ? 1 : 0);
     return axis::launch_status("conv_weight_permute_kernel");
+}
+
+// Whether a rows-mode launch takes the buffer loader and, with tap steps, its block-major
+// reduction order (the second operand must then be read in the same order).
+bool use_block_major(ConvGeom &g, int64_t batch) {
+    g.block_major = g.tap_steps && buffer_reach(g, batch);
+    return g.block_major;
 }
 
 // The forward's second operand W'[(ky, kx, c), n]: read in place from the reference's
@@ -1324,15 +1379,17 @@ int permute_weight(axis_device device, const float *src, float *dst, const ConvS
 int forward_weight(axis_device device, const float *weight, const ConvShape &s, int32_t c_pad,
                    axis::Scratch &permuted, GemmParams &p) {
     const int64_t taps = (int64_t)s.kh * s.kw;
+    const bool block = p.conv.block_major;
     if (c_pad == s.channels && s.channels % 32 == 0) {
         p.y = weight;
         p.y_sj = 1;
         p.y_sr = taps * s.out_channels;
-        p.ytaps = TapSteps{true, FastDiv((uint32_t)s.channels), taps * s.out_channels, s.out_channels, 0};
+        p.ytaps = TapSteps{true, FastDiv((uint32_t)s.channels), taps * s.out_channels, s.out_channels, 0, block,
+                           FastDiv((uint32_t)taps)};
         return AXIS_OK;
     }
     if (int st = permuted.get(device, sizeof(float) * (size_t)(c_pad * taps * s.out_channels))) return st;
-    if (int st = permute_weight(device, weight, permuted.as<float>(), s, 0, c_pad)) return st;
+    if (int st = permute_weight(device, weight, permuted.as<float>(), s, 0, c_pad, block)) return st;
     p.y = permuted.as<float>();
     p.y_sr = s.out_channels;
     p.y_sj = 1;
@@ -1523,15 +1580,17 @@ int axis_conv2d_forward(axis_device device, const float *input, const int64_t in
     const int64_t patch = (int64_t)in.channels * s.kh * s.kw;
     axis::Scratch permuted;
     GemmParams p{};
+    p.conv = geom(in.src, in.ld, height, width, in.channels, s.out_h, s.out_w, s.kh, s.kw, s.sy, s.sx, s.py, s.px);
+    const bool buffered = buffer_reach(p.conv, batch);
+    use_block_major(p.conv, batch);
     if (int st = forward_weight(device, weight, s, in.channels, permuted, p)) return st;
     p.bias = bias;
     p.m = batch * s.out_h * s.out_w;
     p.n = out_channels;
     p.k = patch;
     p.k_work = (int64_t)channels * s.kh * s.kw;
-    p.conv = geom(in.src, in.ld, height, width, in.channels, s.out_h, s.out_w, s.kh, s.kw, s.sy, s.sx, s.py, s.px);
-    return buffer_reach(p.conv, batch) ? run_gemm<true, false, 4, 0>(device, p, 1, out)
-                                       : run_gemm<true, false, 1, 0>(device, p, 1, out);
+    return buffered ? run_gemm<true, false, 4, 0>(device, p, 1, out)
+                    : run_gemm<true, false, 1, 0>(device, p, 1, out);
 }
 
 int axis_conv2d_relu_pool_forward(axis_device device, const float *input,
@@ -1562,13 +1621,15 @@ int axis_conv2d_relu_pool_forward(axis_device device, const float *input,
     const int64_t patch = (int64_t)in.channels * s.kh * s.kw;
     axis::Scratch permuted;
     GemmParams p{};
+    p.conv = geom(in.src, in.ld, height, width, in.channels, s.out_h, s.out_w, s.kh, s.kw, s.sy, s.sx, s.py, s.px);
+    const bool buffered = buffer_reach(p.conv, batch);
+    use_block_major(p.conv, batch);
     if (int st = forward_weight(device, weight, s, in.channels, permuted, p)) return st;
     p.bias = bias;
     p.m = batch * s.out_h * s.out_w;
     p.n = out_channels;
     p.k = patch;
     p.k_work = (int64_t)channels * s.kh * s.kw;
-    p.conv = geom(in.src, in.ld, height, width, in.channels, s.out_h, s.out_w, s.kh, s.kw, s.sy, s.sx, s.py, s.px);
     p.pooled = pooled;
     p.argmax = argmax;
     p.pool_h = pool[0];
@@ -1578,8 +1639,8 @@ int axis_conv2d_relu_pool_forward(axis_device device, const float *input,
     // 2x2 windows: tile rows window-major, pooled in registers
     p.conv.window_major = pool[0] == 2 && pool[1] == 2;
     p.conv.pw_div = p.pool_cols;
-    return buffer_reach(p.conv, batch) ? run_gemm<true, false, 4, 1>(device, p, 1, nullptr)
-                                       : run_gemm<true, false, 1, 1>(device, p, 1, nullptr);
+    return buffered ? run_gemm<true, false, 4, 1>(device, p, 1, nullptr)
+                    : run_gemm<true, false, 1, 1>(device, p, 1, nullptr);
 }
 
 int axis_conv2d_backward_data(axis_device device, const float *gradient, const float *weight,
@@ -1607,14 +1668,16 @@ int axis_conv2d_backward_data(axis_device device, const float *gradient, const f
     channels_last(s.out_h, s.out_w, out_channels, ld);
     p.conv = geom(gradient, ld, s.out_h, s.out_w, out_channels, height, width, s.kh, s.kw, 1, 1,
                   s.kh - 1 - s.py, s.kw - 1 - s.px);
+    const bool buffered = buffer_reach(p.conv, batch);
+    const bool block = use_block_major(p.conv, batch);
     axis::Scratch flipped;
     if (int st = flipped.get(device, sizeof(float) * (size_t)(taps * channels * out_channels))) return st;
-    if (int st = permute_weight(device, weight, flipped.as<float>(), s, 1, channels)) return st;
+    if (int st = permute_weight(device, weight, flipped.as<float>(), s, 1, channels, block)) return st;
     p.y = flipped.as<float>();
     p.y_sr = channels;
     p.y_sj = 1;
-    return buffer_reach(p.conv, batch) ? run_gemm<true, false, 4, 0>(device, p, 1, d_input)
-                                       : run_gemm<true, false, 1, 0>(device, p, 1, d_input);
+    return buffered ? run_gemm<true, false, 4, 0>(device, p, 1, d_input)
+                    : run_gemm<true, false, 1, 0>(device, p, 1, d_input);
 }
 
 int axis_conv2d_backward_weight(axis_device device, const float *input,
