@@ -1035,6 +1035,50 @@ Choice choose(int64_t m, int64_t n, int64_t k, int64_t batch, int64_t cus, bool 
     return large;
 }
 
+// Dense products whose 128x128 tiles number fewer than two per CU: every (tile shape, slice count)
+// is priced as the time of the busiest CU -- ceil(blocks / CUs) blocks of BM x BN x chunk products at
+// a per-CU rate measured on these kernels (0.46 GFLOP/ms at 3-5 resident blocks; a CU left one
+// resident block at a time runs 16% slower) scaled by the shape's efficiency -- plus the slice sum
+// (partials written and read once at ~5 TB/s and a launch).  The 8192 x 784 x 1024 products of a
+// 784-wide layer: 128x128 tiles leave 64 CUs one block and 192 two (143 us); 64x64 tiles, unsplit
+// for the data gradient and in six slices for the weight gradient, run in 130 us.
+struct DenseSchedule {
+    Choice choice;
+    int64_t splits;
+};
+
+DenseSchedule dense_schedule(int64_t m, int64_t n, int64_t k, int64_t batch, int64_t cus) {
+    const Choice shapes[3] = {{Shape::Large, 128, 128, 32, 3}, {Shape::Tall, 128, 64, 32, 4},
+                              {Shape::Small, 64, 64, 32, 5}};
+    const double eff[3] = {1.0, 0.96, 0.92};
+    const int64_t out_len = batch * m * n;
+    DenseSchedule best{shapes[0], 1};
+    double best_us = 1e300;
+    for (int c = 0; c < 3; ++c) {
+        const Choice &sh = shapes[c];
+        if (sh.shape == Shape::Tall && n > 64) continue;
+        const int64_t tiles = ((m + sh.bm - 1) / sh.bm) * ((n + sh.bn - 1) / sh.bn) * batch;
+        const int64_t most = std::max<int64_t>(1, k / (sh.bk * 4));
+        for (int64_t want = 1; want <= std::min<int64_t>(most, 64); ++want) {
+            int64_t chunk = (k + want - 1) / want;
+            chunk = (chunk + sh.bk - 1) / sh.bk * sh.bk;
+            const int64_t splits = (k + chunk - 1) / chunk;
+            if (splits != want) continue;
+            if (splits > 1 && out_len * splits > (int64_t(16) << 20)) break;
+            const int64_t blocks = tiles * splits;
+            const int64_t per_cu = (blocks + cus - 1) / cus;
+            const double occ = std::min<int64_t>(per_cu, sh.per_cu) >= 2 ? 1.0 : 0.84;
+            double us = (double)per_cu * 2.0 * sh.bm * sh.bn * (double)chunk / (0.46e6 * eff[c] * occ);
+            if (splits > 1) us += (double)(splits + 1) * (double)out_len * 4.0 / 5.0e6 + 3.0;
+            if (us < best_us) {
+                best_us = us;
+                best = {sh, splits};
+            }
+        }
+    }
+    return best;
+}
+
 // Deterministic sum of reduction slices (+ bias): up to 32 slices in one pass; beyond that, ranges
 // of 32 consecutive slices first, then the range sums -- a fixed association for a given count.
 int sum_splits(axis_device device, const float *partial, float *out, int64_t len, int64_t splits,
@@ -1133,7 +1177,16 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out, const 
         }
     p.bf16 = device->bf16_matmul;
     const int64_t cus = device->multiprocessors;
-    const Choice ch = choose(p.m, p.n, p.k, batch, cus, EPI == 1);
+    Choice ch = choose(p.m, p.n, p.k, batch, cus, EPI == 1);
+    int64_t scheduled_splits = 0;
+    if constexpr (XMODE == 0 && EPI == 0) {
+        const int64_t large_tiles = ((p.m + 127) / 128) * ((p.n + 127) / 128) * batch;
+        if (!p.perm_c && large_tiles < 2 * cus && p.k >= 16 * 32) {
+            const DenseSchedule d = dense_schedule(p.m, p.n, p.k, batch, cus);
+            ch = d.choice;
+            scheduled_splits = d.splits;
+        }
+    }
     const int BK = ch.bk;
     p.tiles_m = static_cast<int32_t>((p.m + ch.bm - 1) / ch.bm);
     p.tiles_n = static_cast<int32_t>((p.n + ch.bn - 1) / ch.bn);
@@ -1145,7 +1198,9 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out, const 
     const int64_t slots = cus * ch.per_cu;
     const int64_t out_len = batch * p.m * p.n;
     int64_t splits = 1;
-    if (EPI == 0 && tiles < slots && p.k >= 16 * BK) {
+    if (scheduled_splits > 0) {
+        splits = scheduled_splits;
+    } else if (EPI == 0 && tiles < slots && p.k >= 16 * BK) {
         splits = std::min<int64_t>({slots / tiles, p.k / (BK * 4), (int64_t(16) << 20) / out_len});
         splits = std::max<int64_t>(splits, 1);
     }

@@ -169,6 +169,13 @@ def bench_matmul(args):
         row = {}
         for op, call in (("dgrad", lambda: dev.call("axis_matmul_left_backward", dy.vp, w.vp, dx.vp, I(1), I(m), I(k), I(n))),
                          ("wgrad", lambda: dev.call("axis_matmul_right_backward", x.vp, dy.vp, dw.vp, I(1), I(m), I(k), I(n)))):
+            # each product runs for at least 0.3 s before it is timed: the clock settles per workload
+            # (a skinny product right after the 4096^3 ones otherwise times up to 20% slow)
+            start = time.perf_counter()
+            while time.perf_counter() - start < 0.3:
+                for _ in range(10):
+                    call()
+                dev.synchronize()
             lib.axis_timing_reset(dev.handle)
             lib.axis_timing_enable(dev.handle, 1)
             for _ in range(args.steps):
