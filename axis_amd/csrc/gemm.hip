@@ -221,19 +221,19 @@ __device__ __forceinline__ const float *uniform_ptr(const float *p) {
     return reinterpret_cast<const float *>(((uint64_t)hi << 32) | lo);
 }
 
-// Dense operand: element (t, r) at base[t * s_t + r * s_r], read through buffer loads.  A lane's
-// (t, r) within each of its vectors differs from the vector's first lane by the same small
-// amount for every vector, so each vector has a wave-uniform base (scalar registers, one 64-bit
-// add per K step) and every lane one 32-bit offset.  The host keeps those offsets below 2^29
-// elements (63 * (|s_t| + |s_r|)).
+// Dense operand: element (t, r) at base[t * s_t + r * s_r], read through buffer loads.  One buffer
+// resource per K step, based at the tile's element (t0, step) (wave-uniform: a 64-bit scalar add and
+// the descriptor words), and one 32-bit element offset per lane and vector inside the tile, fixed at
+// init.  The host keeps those offsets below 2^29 elements (127 * s_t + 31 * s_r, strides
+// nonnegative).
 template <int BT, int BK, int NT, bool RCONTIG, int VEC>
 struct DenseLoader : Staging<BT, BK, NT, RCONTIG, VEC> {
     using S = Staging<BT, BK, NT, RCONTIG, VEC>;
-    const float *vbase[S::kVecs];  // element of each vector's first lane at r = 0 (wave-uniform)
+    const float *tile_base;        // element (t0, 0) (wave-uniform)
+    uint32_t off[S::kVecs];        // this lane's element offset from (t0, r0), per vector
     int32_t r_wave[S::kVecs];      // r of each vector's first lane inside the tile (wave-uniform)
     bool t_ok[S::kVecs];
-    uint32_t lane_off;             // this lane's element offset from its vector's first lane
-    int32_t r_lane;
+    int32_t r_lane;                // this lane's r from its vector's first lane
     int64_t s_r;
     TapSteps taps{};               // tap-major steps (convolution weights), if on
 
@@ -255,15 +255,15 @@ struct DenseLoader : Staging<BT, BK, NT, RCONTIG, VEC> {
         const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
         int t_l, r_l;
         split(tid & 63, t_l, r_l);
-        lane_off = (uint32_t)(t_l * st + r_l * sr);
         r_lane = r_l;
+        tile_base = uniform_ptr(b + t0 * st);
 #pragma unroll
         for (int e = 0; e < S::kVecs; ++e) {
             int t_w, r_w;
             split(wave * 64 + e * NT, t_w, r_w);
             r_wave[e] = r_w;
             t_ok[e] = t0 + t_w + t_l < t_end;
-            vbase[e] = uniform_ptr(b + (t0 + t_w) * st + (int64_t)r_w * sr);
+            off[e] = (uint32_t)((t_w + t_l) * st + (r_w + r_l) * sr);
         }
     }
     __device__ __forceinline__ void load(const ConvGeom &, int64_t r0, int64_t r_end, int) {
@@ -282,12 +282,12 @@ struct DenseLoader : Staging<BT, BK, NT, RCONTIG, VEC> {
             }
             step = q0 * taps.qa + (int64_t)pos * taps.pb + taps.pc;
         }
+        const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(uniform_ptr(tile_base + step));
         const int32_t room = (int32_t)(r_end - r0 < BK ? r_end - r0 : BK);  // k left in this step
 #pragma unroll
         for (int e = 0; e < S::kVecs; ++e) {
             const bool valid = t_ok[e] && r_wave[e] + r_lane < room;
-            buffer_into<VEC>(this->reg + e * VEC, make_rsrc(uniform_ptr(vbase[e] + step)),
-                             valid ? lane_off * 4u : kOutside);
+            buffer_into<VEC>(this->reg + e * VEC, rsrc, valid ? off[e] * 4u : kOutside);
         }
     }
 };
@@ -563,8 +563,8 @@ __device__ __forceinline__ float finish_value(const float *bias, const float *d,
 // XMODE: 0 dense X, 1 convolution rows mode, 2 convolution cols mode, 3 cols mode over aligned
 // pixel steps, 4 rows mode through buffer loads.
 // EPI: 0 store C (+ bias), 1 bias + ReLU + max pool of whole windows (rows are output pixels).
-// Blocks per CU the register budget is held to (three large, four tall, five small tiles).
-constexpr int gemm_blocks_per_cu(int bm, int bn) { return bm == 128 && bn == 128 ? 3 : bm == 128 ? 4 : 5; }
+// Blocks per CU the register budget is held to (two large, four tall, five small tiles).
+constexpr int gemm_blocks_per_cu(int bm, int bn) { return bm == 128 && bn == 128 ? 2 : bm == 128 ? 4 : 5; }
 
 template <int BM, int BN, int BK, int WM, int WN, bool XR, bool YR, int VX, int VY, int XMODE, int EPI>
 __global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
@@ -661,34 +661,83 @@ __global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
             bv[0] = v.x, bv[1] = v.y;
         }
     };
-    for (int64_t r0 = r_begin; r0 < r_end; r0 += BK) {
-        const bool more = r0 + BK < r_end;
-        if (more) {
-            lx.load(p.conv, r0 + BK, r_end, tid);
-            ly.load(p.conv, r0 + BK, r_end, tid);
-        }
-        // The operands of the next k-quad are read before this quad's MFMAs issue, and the
-        // scheduling barriers keep that order: each LDS read has a whole MFMA group to land
-        // (left to itself the compiler sinks every read to just before its use).
-        float av[2][FM], bv[2][FN];
-        read_operands(0, av[0], bv[0]);
+    auto mma_quad = [&](const float *av, const float *bv) {
 #pragma unroll
-        for (int kk = 0; kk < BK; kk += 4) {
-            const int cur = (kk / 4) & 1;
-            if (kk + 4 < BK) read_operands(kk + 4, av[cur ^ 1], bv[cur ^ 1]);
+        for (int a = 0; a < FM; ++a)
+#pragma unroll
+            for (int b = 0; b < FN; ++b)
+                acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[a], bv[b], acc[a][b], 0, 0, 0);
+    };
+    // Large tiles (two blocks per CU, registers to spare): each stage's k-quads run from registers
+    // read one quad ahead, and the last two quads are read before the stage barrier and held, so
+    // their MFMAs cover the stores of the next stage into LDS and the first reads of it and no
+    // wave idles at either barrier.  Smaller tiles (four or five blocks per CU) lack the registers
+    // for the held quads: their waves cover each other at the barriers instead.
+    constexpr int kQuads = BK / 4;
+    constexpr bool kHeld = gemm_blocks_per_cu(BM, BN) == 2;
+    static_assert(kQuads >= 3, "the held-quad schedule needs three k-quads per stage");
+    float av[2][FM], bv[2][FN];
+    if constexpr (kHeld) {
+        float hold_a[2][FM], hold_b[2][FN];
+        if (r_begin < r_end) read_operands(0, av[0], bv[0]);
+        for (int64_t r0 = r_begin; r0 < r_end; r0 += BK) {
+            const bool more = r0 + BK < r_end;
+            if (more) {
+                lx.load(p.conv, r0 + BK, r_end, tid);
+                ly.load(p.conv, r0 + BK, r_end, tid);
+            }
+            // The operands of the next k-quad are read before this quad's MFMAs issue, and the
+            // scheduling barriers keep that order: each LDS read has a whole MFMA group to land
+            // (left to itself the compiler sinks every read to just before its use).
+#pragma unroll
+            for (int q = 0; q < kQuads - 2; ++q) {
+                const int cur = q & 1;
+                if (q + 1 < kQuads - 2) {
+                    read_operands(4 * (q + 1), av[cur ^ 1], bv[cur ^ 1]);
+                } else {
+                    read_operands(4 * (kQuads - 2), hold_a[0], hold_b[0]);
+                    read_operands(4 * (kQuads - 1), hold_a[1], hold_b[1]);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                mma_quad(av[cur], bv[cur]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            __syncthreads();  // every wave is done reading this stage
+            if (more) {
+                lx.store(xs, tid, p.bf16);
+                ly.store(ys, tid, p.bf16);
+            }
+            mma_quad(hold_a[0], hold_b[0]);
             __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int a = 0; a < FM; ++a)
-#pragma unroll
-                for (int b = 0; b < FN; ++b)
-                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[cur][a], bv[cur][b], acc[a][b], 0, 0, 0);
+            if (more) {
+                __syncthreads();  // the next stage is in LDS
+                read_operands(0, av[0], bv[0]);
+            }
+            mma_quad(hold_a[1], hold_b[1]);
             __builtin_amdgcn_sched_barrier(0);
         }
-        __syncthreads();
-        if (more) {
-            lx.store(xs, tid, p.bf16);
-            ly.store(ys, tid, p.bf16);
+    } else {
+        for (int64_t r0 = r_begin; r0 < r_end; r0 += BK) {
+            const bool more = r0 + BK < r_end;
+            if (more) {
+                lx.load(p.conv, r0 + BK, r_end, tid);
+                ly.load(p.conv, r0 + BK, r_end, tid);
+            }
+            read_operands(0, av[0], bv[0]);
+#pragma unroll
+            for (int q = 0; q < kQuads; ++q) {
+                const int cur = q & 1;
+                if (q + 1 < kQuads) read_operands(4 * (q + 1), av[cur ^ 1], bv[cur ^ 1]);
+                __builtin_amdgcn_sched_barrier(0);
+                mma_quad(av[cur], bv[cur]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
             __syncthreads();
+            if (more) {
+                lx.store(xs, tid, p.bf16);
+                ly.store(ys, tid, p.bf16);
+                __syncthreads();
+            }
         }
     }
 
@@ -979,22 +1028,21 @@ __global__ void __launch_bounds__(256) repack_channels_last_kernel(const float *
     }
 }
 
-// lds_pad: unused dynamic LDS per block, which caps how many blocks share a CU.
 template <int BM, int BN, int BK, int WM, int WN, bool XR, bool YR, int VX, int VY, int XMODE, int EPI>
-void launch_config(const GemmParams &p, dim3 grid, size_t lds_pad, hipStream_t stream) {
-    gemm_kernel<BM, BN, BK, WM, WN, XR, YR, VX, VY, XMODE, EPI><<<grid, WM * WN * 64, lds_pad, stream>>>(p);
+void launch_config(const GemmParams &p, dim3 grid, hipStream_t stream) {
+    gemm_kernel<BM, BN, BK, WM, WN, XR, YR, VX, VY, XMODE, EPI><<<grid, WM * WN * 64, 0, stream>>>(p);
 }
 
 template <int BM, int BN, int BK, int WM, int WN, bool XR, bool YR, int XMODE, int EPI>
-void launch_vec(const GemmParams &p, dim3 grid, size_t lds_pad, hipStream_t stream, bool vx, bool vy) {
+void launch_vec(const GemmParams &p, dim3 grid, hipStream_t stream, bool vx, bool vy) {
     if (vx && vy)
-        launch_config<BM, BN, BK, WM, WN, XR, YR, 4, 4, XMODE, EPI>(p, grid, lds_pad, stream);
+        launch_config<BM, BN, BK, WM, WN, XR, YR, 4, 4, XMODE, EPI>(p, grid, stream);
     else if (vx)
-        launch_config<BM, BN, BK, WM, WN, XR, YR, 4, 1, XMODE, EPI>(p, grid, lds_pad, stream);
+        launch_config<BM, BN, BK, WM, WN, XR, YR, 4, 1, XMODE, EPI>(p, grid, stream);
     else if (vy)
-        launch_config<BM, BN, BK, WM, WN, XR, YR, 1, 4, XMODE, EPI>(p, grid, lds_pad, stream);
+        launch_config<BM, BN, BK, WM, WN, XR, YR, 1, 4, XMODE, EPI>(p, grid, stream);
     else
-        launch_config<BM, BN, BK, WM, WN, XR, YR, 1, 1, XMODE, EPI>(p, grid, lds_pad, stream);
+        launch_config<BM, BN, BK, WM, WN, XR, YR, 1, 1, XMODE, EPI>(p, grid, stream);
 }
 
 // Vector loads need the contiguous extent, the other stride and the base to be 4-aligned.
@@ -1010,11 +1058,10 @@ enum class Shape { Large, Tall, Small };
 struct Choice {
     Shape shape;
     int bm, bn, bk, per_cu;
-    size_t lds_pad = 0;
 };
 
 Choice choose(int64_t m, int64_t n, int64_t k, int64_t batch, int64_t cus, bool pool_epilogue) {
-    const Choice large{Shape::Large, 128, 128, 32, 3}, tall{Shape::Tall, 128, 64, 32, 4},
+    const Choice large{Shape::Large, 128, 128, 32, 2}, tall{Shape::Tall, 128, 64, 32, 4},
         small{Shape::Small, 64, 64, 32, 5};
     if (m < 128 && !pool_epilogue) return small;
     if (n < 128) return n <= 64 || pool_epilogue ? tall : small;
@@ -1022,23 +1069,13 @@ Choice choose(int64_t m, int64_t n, int64_t k, int64_t batch, int64_t cus, bool 
     // A short reduction over few large tiles (e.g. a classifier layer) would leave most CUs idle
     // and each block only a few K steps: four times as many small tiles finish sooner.
     if (!pool_epilogue && tiles * 2 < cus && k <= 2048) return small;
-    // Large tiles run three to a CU.  When that leaves each CU one lone block in its last round
-    // (of a few), that block runs at one wave per SIMD; holding them to two per CU (padding the
-    // dynamic LDS past a third of the CU's 160 KiB) fills every round instead.
-    const int64_t per_cu = (tiles + cus - 1) / cus;
-    if (tiles % cus == 0 && per_cu % large.per_cu == 1 && per_cu < 4 * large.per_cu) {
-        Choice two = large;
-        two.per_cu = 2;
-        two.lds_pad = 30 * 1024;
-        return two;
-    }
     return large;
 }
 
 // Dense products whose 128x128 tiles number fewer than two per CU: every (tile shape, slice count)
 // is priced as the time of the busiest CU -- ceil(blocks / CUs) blocks of BM x BN x chunk products at
-// a per-CU rate measured on these kernels (0.46 GFLOP/ms at 3-5 resident blocks; a CU left one
-// resident block at a time runs 16% slower) scaled by the shape's efficiency -- plus the slice sum
+// a per-CU rate measured on these kernels (0.46 GFLOP/ms with two or more resident blocks; a CU
+// left one resident block at a time runs 16% slower) scaled by the shape's efficiency -- plus the slice sum
 // (partials written and read once at ~5 TB/s and a launch).  The 8192 x 784 x 1024 products of a
 // 784-wide layer: 128x128 tiles leave 64 CUs one block and 192 two (143 us); 64x64 tiles, unsplit
 // for the data gradient and in six slices for the weight gradient, run in 130 us.
@@ -1048,7 +1085,7 @@ struct DenseSchedule {
 };
 
 DenseSchedule dense_schedule(int64_t m, int64_t n, int64_t k, int64_t batch, int64_t cus) {
-    const Choice shapes[3] = {{Shape::Large, 128, 128, 32, 3}, {Shape::Tall, 128, 64, 32, 4},
+    const Choice shapes[3] = {{Shape::Large, 128, 128, 32, 2}, {Shape::Tall, 128, 64, 32, 4},
                               {Shape::Small, 64, 64, 32, 5}};
     const double eff[3] = {1.0, 0.96, 0.92};
     const int64_t out_len = batch * m * n;
@@ -1212,12 +1249,12 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out, const 
     p.k_chunk = chunk;
     p.splits = static_cast<int32_t>(splits);
 
-    // Dense operands read through 32-bit lane offsets of at most 63 * (|s_t| + |s_r|) elements.
-    auto reach = [](int64_t a, int64_t b) { return 63 * ((a < 0 ? -a : a) + (b < 0 ? -b : b)) < (int64_t(1) << 29); };
+    // Dense operands read through 32-bit offsets inside a tile: at most 127 * s_t + 31 * s_r elements.
+    auto reach = [](int64_t st, int64_t sr) { return st >= 0 && sr >= 0 && 127 * st + 31 * sr < (int64_t(1) << 29); };
     if (XMODE == 0 && !reach(p.x_si, p.x_sr))
-        return axis::fail(AXIS_ERROR_INVALID, "matmul operand row pitch must stay below 8,388,608 elements");
+        return axis::fail(AXIS_ERROR_INVALID, "matmul operand row pitch must stay below 4,227,000 elements");
     if (!reach(p.y_sj, p.y_sr))
-        return axis::fail(AXIS_ERROR_INVALID, "matmul operand row pitch must stay below 8,388,608 elements");
+        return axis::fail(AXIS_ERROR_INVALID, "matmul operand row pitch must stay below 4,227,000 elements");
     bool vx;
     if constexpr (XMODE == 0)
         vx = XR ? vec_ok(p.x, p.k, p.x_si) && p.x_batch % 4 == 0
@@ -1272,16 +1309,16 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out, const 
     dim3 grid(static_cast<unsigned>(blocks));
     if constexpr (EPI == 1) {
         if (ch.shape == Shape::Large)
-            launch_vec<128, 128, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, ch.lds_pad, device->stream, vx, vy);
+            launch_vec<128, 128, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, device->stream, vx, vy);
         else
-            launch_vec<128, 64, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, ch.lds_pad, device->stream, vx, vy);
+            launch_vec<128, 64, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, device->stream, vx, vy);
     } else {
         if (ch.shape == Shape::Large)
-            launch_vec<128, 128, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, ch.lds_pad, device->stream, vx, vy);
+            launch_vec<128, 128, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, device->stream, vx, vy);
         else if (ch.shape == Shape::Tall)
-            launch_vec<128, 64, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, ch.lds_pad, device->stream, vx, vy);
+            launch_vec<128, 64, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, device->stream, vx, vy);
         else
-            launch_vec<64, 64, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, ch.lds_pad, device->stream, vx, vy);
+            launch_vec<64, 64, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, device->stream, vx, vy);
     }
     int status = axis::launch_status("gemm_kernel");
     if (status) return status;
