@@ -185,7 +185,7 @@ struct Staging {
     float reg[kElems];
 
     // bf16: round every staged operand to bf16 first (products of bf16 values are exact in fp32).
-    __device__ __forceinline__ void store(float *__restrict__ lds, int tid, bool bf16 = false) {
+    __device__ __forceinline__ void store(float *__restrict__ lds, int tid, int bf16 = 0) {
         if (bf16) {
 #pragma unroll
             for (int e = 0; e < kElems; ++e) reg[e] = bf16_round(reg[e]);
@@ -230,9 +230,8 @@ template <int BT, int BK, int NT, bool RCONTIG, int VEC>
 struct DenseLoader : Staging<BT, BK, NT, RCONTIG, VEC> {
     using S = Staging<BT, BK, NT, RCONTIG, VEC>;
     const float *tile_base;        // element (t0, 0) (wave-uniform)
-    uint32_t off[S::kVecs];        // this lane's element offset from (t0, r0), per vector
+    uint32_t voff[S::kVecs];       // this lane's byte offset from (t0, r0) per vector; kOutside past the end
     int32_t r_wave[S::kVecs];      // r of each vector's first lane inside the tile (wave-uniform)
-    bool t_ok[S::kVecs];
     int32_t r_lane;                // this lane's r from its vector's first lane
     int64_t s_r;
     TapSteps taps{};               // tap-major steps (convolution weights), if on
@@ -262,11 +261,11 @@ struct DenseLoader : Staging<BT, BK, NT, RCONTIG, VEC> {
             int t_w, r_w;
             split(wave * 64 + e * NT, t_w, r_w);
             r_wave[e] = r_w;
-            t_ok[e] = t0 + t_w + t_l < t_end;
-            off[e] = (uint32_t)((t_w + t_l) * st + (r_w + r_l) * sr);
+            voff[e] = t0 + t_w + t_l < t_end ? (uint32_t)((t_w + t_l) * st + (r_w + r_l) * sr) * 4u : kOutside;
         }
     }
-    __device__ __forceinline__ void load(const ConvGeom &, int64_t r0, int64_t r_end, int) {
+    // room: k of this step inside the reduction (1..BK)
+    __device__ __forceinline__ void load(const ConvGeom &, int64_t r0, int32_t room, int) {
         int64_t step = r0 * s_r;
         if (taps.on) {
             uint32_t pos;
@@ -283,12 +282,12 @@ struct DenseLoader : Staging<BT, BK, NT, RCONTIG, VEC> {
             step = q0 * taps.qa + (int64_t)pos * taps.pb + taps.pc;
         }
         const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(uniform_ptr(tile_base + step));
-        const int32_t room = (int32_t)(r_end - r0 < BK ? r_end - r0 : BK);  // k left in this step
+        // Branch-free: split into whole-step and partial-step paths, the loads' wait counts merge
+        // conservatively and the next loads wait on this step's.  room - r_wave is scalar work;
+        // r-contiguous operands share one compare for every vector.
 #pragma unroll
-        for (int e = 0; e < S::kVecs; ++e) {
-            const bool valid = t_ok[e] && r_wave[e] + r_lane < room;
-            buffer_into<VEC>(this->reg + e * VEC, rsrc, valid ? off[e] * 4u : kOutside);
-        }
+        for (int e = 0; e < S::kVecs; ++e)
+            buffer_into<VEC>(this->reg + e * VEC, rsrc, r_lane < room - r_wave[e] ? voff[e] : kOutside);
     }
 };
 
@@ -322,10 +321,9 @@ struct ConvRowsLoader : Staging<BT, BK, NT, true, VEC> {
             iy0[e] = live ? y0 : -(1 << 30);
         }
     }
-    __device__ __forceinline__ void load(const ConvGeom &geom, int64_t r0, int64_t r_end, int) {
-        const int64_t gr = r0 + rr;
-        const bool r_ok = gr < r_end;
-        const uint32_t g = r_ok ? (uint32_t)gr : 0u;
+    __device__ __forceinline__ void load(const ConvGeom &geom, int64_t r0, int32_t room, int) {
+        const bool r_ok = rr < room;
+        const uint32_t g = r_ok ? (uint32_t)(r0 + rr) : 0u;
         const uint32_t pos = geom.c_div.div(g);
         const int32_t c = (int32_t)(g - pos * (uint32_t)geom.channels);
         const int32_t ky = (int32_t)geom.kw_div.div(pos);
@@ -342,20 +340,20 @@ struct ConvRowsLoader : Staging<BT, BK, NT, true, VEC> {
 
 // Rows mode through buffer loads, for gathered tensors whose offsets fit 31-bit byte offsets and
 // kernels of at most 32 taps.  Each row keeps its window origin's offset and a mask of the taps
-// that fall inside the image (bit ky*kw + kx), so a K step tests one bit per vector.  When the
+// that fall outside the image (bit ky*kw + kx), so a K step tests one bit per vector.  When the
 // channel count is a multiple of BK (geom.tap_steps), a K step covers BK channels of one tap and
 // the step's tap decode is wave-uniform.
 template <int BT, int BK, int NT, int VEC>
 struct ConvRowsBufferLoader : Staging<BT, BK, NT, true, VEC> {
     using S = Staging<BT, BK, NT, true, VEC>;
-    uint32_t origin[S::kVecs];   // b*ld_b + iy0*ld_h + ix0*ld_w (mod 2^32; exact when valid)
-    uint32_t inside[S::kVecs];   // taps of the row's window inside the image (0 for rows past the end)
+    uint32_t origin4[S::kVecs];  // 4 * (b*ld_b + iy0*ld_h + ix0*ld_w) (mod 2^32; exact when valid)
+    uint32_t outside[S::kVecs];  // taps of the row's window outside the image (all, for rows past the end)
     int rr;
-    uint32_t lane_c;             // rr * ld_c: the thread's channel offset inside a tap step
+    uint32_t lane_c4;            // 4 * rr * ld_c: the thread's channel offset inside a tap step, bytes
 
     __device__ __forceinline__ void init(const ConvGeom &geom, int64_t t0, int64_t t_end, int tid) {
         rr = (tid % S::kPer) * VEC;
-        lane_c = (uint32_t)(rr * geom.ld_c);
+        lane_c4 = (uint32_t)(rr * geom.ld_c) * 4u;
 #pragma unroll
         for (int e = 0; e < S::kVecs; ++e) {
             const int64_t gt = tile_pixel(geom, t0, (tid + e * NT) / S::kPer);
@@ -367,23 +365,23 @@ struct ConvRowsBufferLoader : Staging<BT, BK, NT, true, VEC> {
             const int32_t oy = (int32_t)(q - b * (uint32_t)geom.out_h);
             const int32_t y0 = oy * geom.sy - geom.py;
             const int32_t x0 = ox * geom.sx - geom.px;
-            origin[e] = b * (uint32_t)geom.ld_b + (uint32_t)y0 * (uint32_t)geom.ld_h + (uint32_t)x0 * (uint32_t)geom.ld_w;
+            origin4[e] = (b * (uint32_t)geom.ld_b + (uint32_t)y0 * (uint32_t)geom.ld_h + (uint32_t)x0 * (uint32_t)geom.ld_w) * 4u;
             uint32_t cols = 0, taps = 0;
             for (int32_t kx = 0; kx < geom.kw; ++kx)
                 cols |= (uint32_t)((uint32_t)(x0 + kx) < (uint32_t)geom.width) << kx;
             for (int32_t ky = 0; ky < geom.kh; ++ky)
                 taps |= ((uint32_t)(y0 + ky) < (uint32_t)geom.height ? cols : 0u) << (ky * geom.kw);
-            inside[e] = live ? taps : 0u;
+            outside[e] = live ? ~taps : ~0u;
         }
     }
-    __device__ __forceinline__ void load(const ConvGeom &geom, int64_t r0, int64_t r_end, int) {
+    __device__ __forceinline__ void load(const ConvGeom &geom, int64_t r0, int32_t room, int) {
         const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(geom.src);
-        uint32_t pos, delta;
-        bool r_ok;
         if (geom.tap_steps) {
-            // r_end is a multiple of BK here, so every k of the step is inside the reduction
-            // the step's tap and first channel are wave-uniform: scalar arithmetic, plus the
-            // thread's fixed channel offset
+            // The reduction is a multiple of BK here, so every k of the step is inside it; the
+            // step's tap and first channel are wave-uniform (scalar arithmetic).  Per vector: the
+            // offset, and the window's outside bit for this tap moved to bit 31, which puts a
+            // masked lane's offset past the record count (three vector instructions).
+            uint32_t pos;
             int32_t c0;
             if (geom.block_major) {
                 const uint32_t st = (uint32_t)r0 >> 5;
@@ -396,24 +394,26 @@ struct ConvRowsBufferLoader : Staging<BT, BK, NT, true, VEC> {
             }
             const int32_t ky = (int32_t)geom.kw_div.div(pos);
             const int32_t kx = (int32_t)pos - ky * geom.kw;
-            delta = __builtin_amdgcn_readfirstlane((uint32_t)(ky * geom.ld_h + kx * geom.ld_w + c0 * geom.ld_c)) +
-                    lane_c;
-            pos = __builtin_amdgcn_readfirstlane(pos);
-            r_ok = true;
+            const uint32_t delta4 =
+                __builtin_amdgcn_readfirstlane((uint32_t)(ky * geom.ld_h + kx * geom.ld_w + c0 * geom.ld_c) * 4u) +
+                lane_c4;
+            const uint32_t up = 31u - __builtin_amdgcn_readfirstlane(pos);
+#pragma unroll
+            for (int e = 0; e < S::kVecs; ++e)
+                buffer_into<VEC>(this->reg + e * VEC, rsrc, (origin4[e] + delta4) | ((outside[e] << up) & kOutside));
         } else {
-            const int64_t gr = r0 + rr;
-            r_ok = gr < r_end;
-            const uint32_t g = r_ok ? (uint32_t)gr : 0u;
-            pos = geom.c_div.div(g);
+            const bool r_ok = rr < room;
+            const uint32_t g = r_ok ? (uint32_t)(r0 + rr) : 0u;
+            const uint32_t pos = geom.c_div.div(g);
             const int32_t c = (int32_t)(g - pos * (uint32_t)geom.channels);
             const int32_t ky = (int32_t)geom.kw_div.div(pos);
             const int32_t kx = (int32_t)pos - ky * geom.kw;
-            delta = (uint32_t)(ky * geom.ld_h + kx * geom.ld_w + c * geom.ld_c);
-        }
+            const uint32_t delta4 = (uint32_t)(ky * geom.ld_h + kx * geom.ld_w + c * geom.ld_c) * 4u;
 #pragma unroll
-        for (int e = 0; e < S::kVecs; ++e) {
-            const bool valid = r_ok && ((inside[e] >> pos) & 1u) != 0;
-            buffer_into<VEC>(this->reg + e * VEC, rsrc, valid ? (origin[e] + delta) * 4u : kOutside);
+            for (int e = 0; e < S::kVecs; ++e) {
+                const bool valid = r_ok && ((outside[e] >> pos) & 1u) == 0;
+                buffer_into<VEC>(this->reg + e * VEC, rsrc, valid ? origin4[e] + delta4 : kOutside);
+            }
         }
     }
 };
@@ -474,13 +474,12 @@ struct ConvColsLoader : Staging<BT, BK, NT, false, VEC> {
         }
         next_r += BK;
     }
-    __device__ __forceinline__ void load(const ConvGeom &geom, int64_t r0, int64_t r_end, int tid) {
+    __device__ __forceinline__ void load(const ConvGeom &geom, int64_t r0, int32_t room, int tid) {
         if (r0 != next_r) locate(geom, r0, tid);
 #pragma unroll
         for (int e = 0; e < S::kVecs; ++e) {
-            const int64_t gr = r0 + tid / S::kPer + e * kRowStep;
             const int32_t iy = oy[e] * geom.sy + ky - geom.py, ix = ox[e] * geom.sx + kx - geom.px;
-            const bool valid = t_ok && gr < r_end && (uint32_t)iy < (uint32_t)geom.height &&
+            const bool valid = t_ok && tid / S::kPer + e * kRowStep < room && (uint32_t)iy < (uint32_t)geom.height &&
                                (uint32_t)ix < (uint32_t)geom.width;
             load_into<VEC>(this->reg + e * VEC, geom.src + (valid ? off[e] + tap : 0u), valid);
         }
@@ -522,7 +521,7 @@ struct ConvColsStepLoader : Staging<BT, BK, NT, false, VEC> {
                      (uint32_t)c * (uint32_t)geom.ld_c;
         }
     }
-    __device__ __forceinline__ void load(const ConvGeom &geom, int64_t r0, int64_t r_end, int) {
+    __device__ __forceinline__ void load(const ConvGeom &geom, int64_t r0, int32_t room, int) {
         const uint32_t p0 = (uint32_t)r0;
         const uint32_t q = geom.ow_div.div(p0);
         const int32_t ox0 = (int32_t)(p0 - q * (uint32_t)geom.out_w);
@@ -534,10 +533,10 @@ struct ConvColsStepLoader : Staging<BT, BK, NT, false, VEC> {
         const int64_t shift = (int64_t)geom.py * geom.ld_h + (int64_t)geom.px * geom.ld_w;
         const int64_t base = (int64_t)b * geom.ld_b + (int64_t)oys * geom.ld_h + (int64_t)oxs * geom.ld_w - shift;
         const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(geom.src + base);
-        const int64_t room = r_end - r0;  // pixels of this step inside the reduction
+        // rows past the reduction's end only in a partial last step (room: its pixels)
 #pragma unroll
         for (int e = 0; e < S::kVecs; ++e) {
-            const bool valid = t_ok && s0 + e * kRowStep < room &&
+            const bool valid = t_ok && (room >= BK || s0 + e * kRowStep < room) &&
                                (uint32_t)(oys + iy_rel[e]) < (uint32_t)geom.height &&
                                (uint32_t)(oxs + ix_rel[e]) < (uint32_t)geom.width;
             buffer_into<VEC>(this->reg + e * VEC, rsrc, valid ? (rel[e] + (uint32_t)shift) * 4u : kOutside);
@@ -629,11 +628,19 @@ __global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
         lx.init(p.conv, i0, p.m, tid);
     ly.init(p.y + batch * p.y_batch, p.y_sj, p.y_sr, j0, p.n, tid);
     ly.taps = p.ytaps;
-    if (r_begin < r_end) {
-        lx.load(p.conv, r_begin, r_end, tid);
-        ly.load(p.conv, r_begin, r_end, tid);
-        lx.store(xs, tid, p.bf16);
-        ly.store(ys, tid, p.bf16);
+    // K steps of this slice, counted in 32 bits (scalar compares; 64-bit compares of scalars take
+    // vector instructions), and the k of the last one
+    const int32_t steps = r_begin < r_end ? (int32_t)((r_end - r_begin + BK - 1) / BK) : 0;
+    const int32_t tail = (int32_t)(r_end - r_begin - (int64_t)(steps - 1) * BK);
+    auto room_of = [&](int32_t step) { return step == steps - 1 ? tail : BK; };
+    // flags the loop tests, as ints from the scalar unit: kept as bools they cross the loop's
+    // blocks as lane masks and cost two vector instructions per test
+    const int bf16 = __builtin_amdgcn_readfirstlane(p.bf16 ? 1 : 0);
+    if (steps > 0) {
+        lx.load(p.conv, r_begin, room_of(0), tid);
+        ly.load(p.conv, r_begin, room_of(0), tid);
+        lx.store(xs, tid, bf16);
+        ly.store(ys, tid, bf16);
     }
     __syncthreads();
 
@@ -679,12 +686,13 @@ __global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
     float av[2][FM], bv[2][FN];
     if constexpr (kHeld) {
         float hold_a[2][FM], hold_b[2][FN];
-        if (r_begin < r_end) read_operands(0, av[0], bv[0]);
-        for (int64_t r0 = r_begin; r0 < r_end; r0 += BK) {
-            const bool more = r0 + BK < r_end;
+        if (steps > 0) read_operands(0, av[0], bv[0]);
+        for (int32_t step = 0; step < steps; ++step) {
+            const bool more = step + 1 < steps;
             if (more) {
-                lx.load(p.conv, r0 + BK, r_end, tid);
-                ly.load(p.conv, r0 + BK, r_end, tid);
+                const int64_t r_next = r_begin + (int64_t)(step + 1) * BK;
+                lx.load(p.conv, r_next, room_of(step + 1), tid);
+                ly.load(p.conv, r_next, room_of(step + 1), tid);
             }
             // The operands of the next k-quad are read before this quad's MFMAs issue, and the
             // scheduling barriers keep that order: each LDS read has a whole MFMA group to land
@@ -702,26 +710,25 @@ __global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
                 mma_quad(av[cur], bv[cur]);
                 __builtin_amdgcn_sched_barrier(0);
             }
+            // After the last step the stores, the barrier and the reads below handle stale registers
+            // and LDS nothing reads: unconditional, they keep the loop free of flag tests.
             __syncthreads();  // every wave is done reading this stage
-            if (more) {
-                lx.store(xs, tid, p.bf16);
-                ly.store(ys, tid, p.bf16);
-            }
+            lx.store(xs, tid, bf16);
+            ly.store(ys, tid, bf16);
             mma_quad(hold_a[0], hold_b[0]);
             __builtin_amdgcn_sched_barrier(0);
-            if (more) {
-                __syncthreads();  // the next stage is in LDS
-                read_operands(0, av[0], bv[0]);
-            }
+            __syncthreads();  // the next stage is in LDS
+            read_operands(0, av[0], bv[0]);
             mma_quad(hold_a[1], hold_b[1]);
             __builtin_amdgcn_sched_barrier(0);
         }
     } else {
-        for (int64_t r0 = r_begin; r0 < r_end; r0 += BK) {
-            const bool more = r0 + BK < r_end;
+        for (int32_t step = 0; step < steps; ++step) {
+            const bool more = step + 1 < steps;
             if (more) {
-                lx.load(p.conv, r0 + BK, r_end, tid);
-                ly.load(p.conv, r0 + BK, r_end, tid);
+                const int64_t r_next = r_begin + (int64_t)(step + 1) * BK;
+                lx.load(p.conv, r_next, room_of(step + 1), tid);
+                ly.load(p.conv, r_next, room_of(step + 1), tid);
             }
             read_operands(0, av[0], bv[0]);
 #pragma unroll
@@ -734,8 +741,8 @@ __global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
             }
             __syncthreads();
             if (more) {
-                lx.store(xs, tid, p.bf16);
-                ly.store(ys, tid, p.bf16);
+                lx.store(xs, tid, bf16);
+                ly.store(ys, tid, bf16);
                 __syncthreads();
             }
         }
