@@ -120,7 +120,7 @@ struct GemmParams {
     int64_t k_work;            // algorithmic reduction length for timing (k without padding), or 0
     int32_t splits;
     int32_t tiles_m, tiles_n;
-    uint32_t xcd_span;         // blocks per XCD when the launch is remapped (blocks % 8 == 0), else 0
+    uint32_t xcd_span;         // blocks / 8: the first 8 * xcd_span blocks are remapped, the rest keep their order
     ConvGeom conv;
     // Pooling epilogue: output rows are pixels of a [.., out_h, out_w] grid (out_w = pool_ow).
     float *pooled;
@@ -264,7 +264,8 @@ struct DenseLoader : Staging<BT, BK, NT, RCONTIG, VEC> {
             voff[e] = t0 + t_w + t_l < t_end ? (uint32_t)((t_w + t_l) * st + (r_w + r_l) * sr) * 4u : kOutside;
         }
     }
-    // room: k of this step inside the reduction (1..BK)
+    // room: k of this step inside the reduction (1..BK); WHOLE: every step of the launch is whole
+    template <bool WHOLE = false>
     __device__ __forceinline__ void load(const ConvGeom &, int64_t r0, int32_t room, int) {
         int64_t step = r0 * s_r;
         if (taps.on) {
@@ -287,7 +288,7 @@ struct DenseLoader : Staging<BT, BK, NT, RCONTIG, VEC> {
         // r-contiguous operands share one compare for every vector.
 #pragma unroll
         for (int e = 0; e < S::kVecs; ++e)
-            buffer_into<VEC>(this->reg + e * VEC, rsrc, r_lane < room - r_wave[e] ? voff[e] : kOutside);
+            buffer_into<VEC>(this->reg + e * VEC, rsrc, WHOLE || r_lane < room - r_wave[e] ? voff[e] : kOutside);
     }
 };
 
@@ -496,51 +497,69 @@ template <int BT, int BK, int NT, int VEC>
 struct ConvColsStepLoader : Staging<BT, BK, NT, false, VEC> {
     using S = Staging<BT, BK, NT, false, VEC>;
     static constexpr int kRowStep = NT / S::kPer;  // pixels between the thread's rows
-    int32_t iy_rel[S::kVecs], ix_rel[S::kVecs];    // dy*sy + ky - py, dx*sx + kx - px
-    uint32_t rel[S::kVecs];                        // iy_rel*ld_h + ix_rel*ld_w + c*ld_c (mod 2^32)
-    int32_t s0;                                    // in-step pixel of the thread's first row
-    bool t_ok;
+    static_assert(BK == 32, "steps of 32 pixels");
+    uint32_t rel4[S::kVecs];  // bytes: (iy_rel + py)*ld_h + (ix_rel + px)*ld_w + c*ld_c (mod 2^32)
+    // Bit (first | last << 1 | top << 2 | bottom << 3) set when the lane's element is padding (or
+    // its row past the end) in a step whose pixels start the image's first / last 32-column
+    // segment, first / last row group.  A step elsewhere has every element inside (the host
+    // keeps px <= 32 sx and py <= (rows per step) sy), so these four flags decide.
+    uint32_t bad[S::kVecs];
 
     __device__ __forceinline__ void init(const ConvGeom &geom, int64_t t0, int64_t t_end, int tid) {
         const int64_t gt = t0 + (tid % S::kPer) * VEC;
-        t_ok = gt < t_end;
+        const bool t_ok = gt < t_end;
         const uint32_t g = t_ok ? (uint32_t)gt : 0u;
         const uint32_t pos = geom.c_div.div(g);
         const int32_t c = (int32_t)(g - pos * (uint32_t)geom.channels);
         const int32_t ky = (int32_t)geom.kw_div.div(pos);
         const int32_t kx = (int32_t)pos - ky * geom.kw;
-        s0 = tid / S::kPer;
+        const int32_t s0 = tid / S::kPer;
+        const int32_t seg = geom.out_w < 32 ? geom.out_w : 32;       // columns a step spans
+        const int32_t rows = geom.out_w < 32 ? 32 / geom.out_w : 1;  // rows a step spans
+        const int32_t last_x = (geom.out_w - seg) * geom.sx, last_y = (geom.out_h - rows) * geom.sy;
 #pragma unroll
         for (int e = 0; e < S::kVecs; ++e) {
             const uint32_t s = (uint32_t)(s0 + e * kRowStep);
             const int32_t dy = (int32_t)geom.ow_div.div(s);
             const int32_t dx = (int32_t)s - dy * geom.out_w;
-            iy_rel[e] = dy * geom.sy + ky - geom.py;
-            ix_rel[e] = dx * geom.sx + kx - geom.px;
-            rel[e] = (uint32_t)iy_rel[e] * (uint32_t)geom.ld_h + (uint32_t)ix_rel[e] * (uint32_t)geom.ld_w +
-                     (uint32_t)c * (uint32_t)geom.ld_c;
+            const int32_t iy_rel = dy * geom.sy + ky - geom.py, ix_rel = dx * geom.sx + kx - geom.px;
+            rel4[e] = ((uint32_t)(iy_rel + geom.py) * (uint32_t)geom.ld_h + (uint32_t)(ix_rel + geom.px) * (uint32_t)geom.ld_w +
+                       (uint32_t)c * (uint32_t)geom.ld_c) * 4u;
+            uint32_t b = 0;
+            for (uint32_t f = 0; f < 16; ++f) {
+                const bool first = f & 1u, last = f & 2u, top = f & 4u, bottom = f & 8u;
+                const int32_t x = first ? ix_rel : last ? last_x + ix_rel : 0;
+                const int32_t y = top ? iy_rel : bottom ? last_y + iy_rel : 0;
+                const bool in = t_ok && (!(first || last) || (uint32_t)x < (uint32_t)geom.width) &&
+                                (!(top || bottom) || (uint32_t)y < (uint32_t)geom.height);
+                b |= (in ? 0u : 1u) << f;
+            }
+            bad[e] = b;
         }
     }
-    __device__ __forceinline__ void load(const ConvGeom &geom, int64_t r0, int32_t room, int) {
+    // Every step is whole: the reduction (batch * image pixels) and the slices are multiples of 32.
+    __device__ __forceinline__ void load(const ConvGeom &geom, int64_t r0, int32_t, int) {
         const uint32_t p0 = (uint32_t)r0;
         const uint32_t q = geom.ow_div.div(p0);
         const int32_t ox0 = (int32_t)(p0 - q * (uint32_t)geom.out_w);
         const uint32_t b = geom.oh_div.div(q);
         const int32_t oy0 = (int32_t)(q - b * (uint32_t)geom.out_h);
+        const int32_t seg = geom.out_w < 32 ? geom.out_w : 32;
+        const int32_t rows = geom.out_w < 32 ? 32 / geom.out_w : 1;
+        // sign bits rather than comparisons: compared flags reach vector registers as lane masks
+        const uint32_t flags = ((uint32_t)(ox0 - 1) >> 31) | ((uint32_t)(geom.out_w - ox0 - seg - 1) >> 31 << 1) |
+                               ((uint32_t)(oy0 - 1) >> 31 << 2) | ((uint32_t)(geom.out_h - oy0 - rows - 1) >> 31 << 3);
         const int32_t oys = oy0 * geom.sy, oxs = ox0 * geom.sx;
         // Buffer base at the step origin moved back by the padding, so that every valid lane's
         // offset (at least -py rows and -px columns from the origin) is non-negative.
         const int64_t shift = (int64_t)geom.py * geom.ld_h + (int64_t)geom.px * geom.ld_w;
         const int64_t base = (int64_t)b * geom.ld_b + (int64_t)oys * geom.ld_h + (int64_t)oxs * geom.ld_w - shift;
         const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(geom.src + base);
-        // rows past the reduction's end only in a partial last step (room: its pixels)
+        // the padding bit of this step's case moved to bit 31: past the record count (two vector
+        // instructions per vector)
 #pragma unroll
-        for (int e = 0; e < S::kVecs; ++e) {
-            const bool valid = t_ok && (room >= BK || s0 + e * kRowStep < room) &&
-                               (uint32_t)(oys + iy_rel[e]) < (uint32_t)geom.height &&
-                               (uint32_t)(oxs + ix_rel[e]) < (uint32_t)geom.width;
-            buffer_into<VEC>(this->reg + e * VEC, rsrc, valid ? (rel[e] + (uint32_t)shift) * 4u : kOutside);
-        }
+        for (int e = 0; e < S::kVecs; ++e)
+            buffer_into<VEC>(this->reg + e * VEC, rsrc, (((bad[e] >> flags) & 1u) << 31) | rel4[e]);
     }
 };
 
@@ -600,9 +619,10 @@ __global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
     // Workgroups go to the 8 XCDs round-robin in launch order; block L takes logical tile
     // (L % 8) * (blocks / 8) + L / 8 so each XCD (its own L2) works through a contiguous range
     // of tiles: the tiles of one reduction slice, or neighbouring row panels, share its cache.
+    // The last blocks % 8 blocks keep their own order.
     const uint32_t tiles = (uint32_t)p.tiles_m * (uint32_t)p.tiles_n;
     const uint32_t L = blockIdx.x;
-    const uint32_t logical = p.xcd_span ? (L % 8u) * p.xcd_span + L / 8u : L;
+    const uint32_t logical = L < 8u * p.xcd_span ? (L % 8u) * p.xcd_span + L / 8u : L;
     const uint32_t tile = logical % tiles;
     const uint32_t slice = logical / tiles;
     const int64_t i0 = (int64_t)(tile % (uint32_t)p.tiles_m) * BM;
@@ -633,12 +653,14 @@ __global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
     const int32_t steps = r_begin < r_end ? (int32_t)((r_end - r_begin + BK - 1) / BK) : 0;
     const int32_t tail = (int32_t)(r_end - r_begin - (int64_t)(steps - 1) * BK);
     auto room_of = [&](int32_t step) { return step == steps - 1 ? tail : BK; };
+    // cols mode over aligned steps: the reduction (batch * image pixels) is a multiple of BK
+    constexpr bool kWholeSteps = XMODE == 3;
     // flags the loop tests, as ints from the scalar unit: kept as bools they cross the loop's
     // blocks as lane masks and cost two vector instructions per test
     const int bf16 = __builtin_amdgcn_readfirstlane(p.bf16 ? 1 : 0);
     if (steps > 0) {
         lx.load(p.conv, r_begin, room_of(0), tid);
-        ly.load(p.conv, r_begin, room_of(0), tid);
+        ly.template load<kWholeSteps>(p.conv, r_begin, room_of(0), tid);
         lx.store(xs, tid, bf16);
         ly.store(ys, tid, bf16);
     }
@@ -692,7 +714,7 @@ __global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
             if (more) {
                 const int64_t r_next = r_begin + (int64_t)(step + 1) * BK;
                 lx.load(p.conv, r_next, room_of(step + 1), tid);
-                ly.load(p.conv, r_next, room_of(step + 1), tid);
+                ly.template load<kWholeSteps>(p.conv, r_next, room_of(step + 1), tid);
             }
             // The operands of the next k-quad are read before this quad's MFMAs issue, and the
             // scheduling barriers keep that order: each LDS read has a whole MFMA group to land
@@ -728,7 +750,7 @@ __global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
             if (more) {
                 const int64_t r_next = r_begin + (int64_t)(step + 1) * BK;
                 lx.load(p.conv, r_next, room_of(step + 1), tid);
-                ly.load(p.conv, r_next, room_of(step + 1), tid);
+                ly.template load<kWholeSteps>(p.conv, r_next, room_of(step + 1), tid);
             }
             read_operands(0, av[0], bv[0]);
 #pragma unroll
@@ -1310,7 +1332,7 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out, const 
     }
     const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n * batch * splits;
     if (blocks >= INT32_MAX) return axis::fail(AXIS_ERROR_INVALID, "matmul too large for one launch");
-    p.xcd_span = blocks % 8 == 0 ? (uint32_t)(blocks / 8) : 0u;
+    p.xcd_span = (uint32_t)(blocks / 8);
     const double k_work = (double)(p.k_work > 0 ? p.k_work : p.k);
     axis::TimedLaunch timed(ws ? nullptr : device, "gemm", 2.0 * (double)batch * (double)p.m * (double)p.n * k_work);
     dim3 grid(static_cast<unsigned>(blocks));
@@ -1815,7 +1837,10 @@ int axis_conv2d_backward_weight(axis_device device, const float *input,
     // Every tile shape is 32 deep: when 32-pixel steps never straddle an image and cut its rows
     // the same way each time, the cheaper step loader applies.
     const int64_t image = (int64_t)s.out_h * s.out_w;
-    const bool aligned = (32 % s.out_w == 0 || s.out_w % 32 == 0) && image % 32 == 0;
+    // (the step loader also needs the padding inside the first column segment and row group)
+    const int32_t rows_per_step = s.out_w < 32 ? 32 / s.out_w : 1;
+    const bool aligned = (32 % s.out_w == 0 || s.out_w % 32 == 0) && image % 32 == 0 && s.px <= 32 * s.sx &&
+                         s.py <= rows_per_step * s.sy;
     float *dst = direct ? d_weight : ordered.as<float>();
     const int st = aligned ? run_gemm<false, false, 3, 0>(device, p, 1, dst) : run_gemm<false, false, 2, 0>(device, p, 1, dst);
     if (st || direct) return st;

@@ -124,7 +124,7 @@ struct Layout {
 struct KernelArgs {
     axis::Bf16Gemm g;
     int32_t tiles_m, tiles_n;
-    uint32_t xcd_span;  // blocks per XCD when the launch is remapped (blocks % 8 == 0), else 0
+    uint32_t xcd_span;  // blocks / 8: the first 8 * xcd_span blocks are remapped, the rest keep their order
 };
 
 // + bias[col], then beta * d + alpha * v, each product and the sum rounded separately.
@@ -206,10 +206,10 @@ __global__ void __launch_bounds__(256, 2) bf16_gemm_kernel(KernelArgs a) {
     const int quad = lane >> 4, l16 = lane & 15;
 
     // XCD-aware order: block L takes logical tile (L % 8) * (blocks / 8) + L / 8, so each XCD's
-    // L2 serves a contiguous range of tiles.
+    // L2 serves a contiguous range of tiles (the last blocks % 8 blocks keep their own order).
     const uint32_t tiles = (uint32_t)a.tiles_m * (uint32_t)a.tiles_n;
     const uint32_t L = blockIdx.x;
-    const uint32_t logical = a.xcd_span ? (L % 8u) * a.xcd_span + L / 8u : L;
+    const uint32_t logical = L < 8u * a.xcd_span ? (L % 8u) * a.xcd_span + L / 8u : L;
     const uint32_t tile = logical % tiles;
     const uint32_t slice = logical / tiles;
     uint32_t ti, tj;
@@ -365,7 +365,7 @@ int bf16_gemm(axis_device device, const Bf16Gemm &g, int64_t batch, Bf16Tile til
     // 32-bit byte offsets inside one tile's rows: (tile rows + 1) * kp * 2 bytes
     if ((int64_t)(std::max(tile.rows, tile.cols) + 1) * g.kp * 2 >= (int64_t(1) << 31))
         return fail(AXIS_ERROR_INVALID, "bf16 matmul reduction too long");
-    a.xcd_span = blocks % 8 == 0 ? (uint32_t)(blocks / 8) : 0u;
+    a.xcd_span = (uint32_t)(blocks / 8);
     dim3 grid((unsigned)blocks);
     if (tile.rows == 128)
         bf16_gemm_kernel<128, 128, 64><<<grid, 256, 0, device->stream>>>(a);
