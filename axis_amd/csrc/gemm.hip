@@ -581,8 +581,8 @@ __device__ __forceinline__ float finish_value(const float *bias, const float *d,
 // XMODE: 0 dense X, 1 convolution rows mode, 2 convolution cols mode, 3 cols mode over aligned
 // pixel steps, 4 rows mode through buffer loads.
 // EPI: 0 store C (+ bias), 1 bias + ReLU + max pool of whole windows (rows are output pixels).
-// Blocks per CU the register budget is held to (two large, four tall, five small tiles).
-constexpr int gemm_blocks_per_cu(int bm, int bn) { return bm == 128 && bn == 128 ? 2 : bm == 128 ? 4 : 5; }
+// Blocks per CU the register budget is held to (two large, three tall, five small tiles).
+constexpr int gemm_blocks_per_cu(int bm, int bn) { return bm == 128 && bn == 128 ? 2 : bm == 128 ? 3 : 5; }
 
 template <int BM, int BN, int BK, int WM, int WN, bool XR, bool YR, int VX, int VY, int XMODE, int EPI>
 __global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
@@ -697,13 +697,13 @@ __global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
             for (int b = 0; b < FN; ++b)
                 acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[a], bv[b], acc[a][b], 0, 0, 0);
     };
-    // Large tiles (two blocks per CU, registers to spare): each stage's k-quads run from registers
-    // read one quad ahead, and the last two quads are read before the stage barrier and held, so
-    // their MFMAs cover the stores of the next stage into LDS and the first reads of it and no
-    // wave idles at either barrier.  Smaller tiles (four or five blocks per CU) lack the registers
+    // 128-row tiles (two or three blocks per CU, registers to spare): each stage's k-quads run from
+    // registers read one quad ahead, and the last two quads are read before the stage barrier and
+    // held, so their MFMAs cover the stores of the next stage into LDS and the first reads of it
+    // and no wave idles at either barrier.  64x64 tiles (five blocks per CU) lack the registers
     // for the held quads: their waves cover each other at the barriers instead.
     constexpr int kQuads = BK / 4;
-    constexpr bool kHeld = gemm_blocks_per_cu(BM, BN) == 2;
+    constexpr bool kHeld = BM == 128;
     static_assert(kQuads >= 3, "the held-quad schedule needs three k-quads per stage");
     float av[2][FM], bv[2][FN];
     if constexpr (kHeld) {
@@ -1090,7 +1090,7 @@ struct Choice {
 };
 
 Choice choose(int64_t m, int64_t n, int64_t k, int64_t batch, int64_t cus, bool pool_epilogue) {
-    const Choice large{Shape::Large, 128, 128, 32, 2}, tall{Shape::Tall, 128, 64, 32, 4},
+    const Choice large{Shape::Large, 128, 128, 32, 2}, tall{Shape::Tall, 128, 64, 32, 3},
         small{Shape::Small, 64, 64, 32, 5};
     if (m < 128 && !pool_epilogue) return small;
     if (n < 128) return n <= 64 || pool_epilogue ? tall : small;
@@ -1114,7 +1114,7 @@ struct DenseSchedule {
 };
 
 DenseSchedule dense_schedule(int64_t m, int64_t n, int64_t k, int64_t batch, int64_t cus) {
-    const Choice shapes[3] = {{Shape::Large, 128, 128, 32, 2}, {Shape::Tall, 128, 64, 32, 4},
+    const Choice shapes[3] = {{Shape::Large, 128, 128, 32, 2}, {Shape::Tall, 128, 64, 32, 3},
                               {Shape::Small, 64, 64, 32, 5}};
     const double eff[3] = {1.0, 0.96, 0.92};
     const int64_t out_len = batch * m * n;
