@@ -581,8 +581,8 @@ __device__ __forceinline__ float finish_value(const float *bias, const float *d,
 // XMODE: 0 dense X, 1 convolution rows mode, 2 convolution cols mode, 3 cols mode over aligned
 // pixel steps, 4 rows mode through buffer loads.
 // EPI: 0 store C (+ bias), 1 bias + ReLU + max pool of whole windows (rows are output pixels).
-// Blocks per CU the register budget is held to (two large, three tall, five small tiles).
-constexpr int gemm_blocks_per_cu(int bm, int bn) { return bm == 128 && bn == 128 ? 2 : bm == 128 ? 3 : 5; }
+// Blocks per CU the register budget is held to (two large, three tall, four small tiles).
+constexpr int gemm_blocks_per_cu(int bm, int bn) { return bm == 128 && bn == 128 ? 2 : bm == 128 ? 3 : 4; }
 
 template <int BM, int BN, int BK, int WM, int WN, bool XR, bool YR, int VX, int VY, int XMODE, int EPI>
 __global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
@@ -697,77 +697,49 @@ __global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
             for (int b = 0; b < FN; ++b)
                 acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[a], bv[b], acc[a][b], 0, 0, 0);
     };
-    // 128-row tiles (two or three blocks per CU, registers to spare): each stage's k-quads run from
-    // registers read one quad ahead, and the last two quads are read before the stage barrier and
-    // held, so their MFMAs cover the stores of the next stage into LDS and the first reads of it
-    // and no wave idles at either barrier.  64x64 tiles (five blocks per CU) lack the registers
-    // for the held quads: their waves cover each other at the barriers instead.
+    // Each stage's k-quads run from registers read one quad ahead, and the last two quads are read
+    // before the stage barrier and held, so their MFMAs cover the stores of the next stage into
+    // LDS and the first reads of it and no wave idles at either barrier (the register budget:
+    // two 128x128, three 128x64 or four 64x64 blocks per CU).
     constexpr int kQuads = BK / 4;
-    constexpr bool kHeld = BM == 128;
     static_assert(kQuads >= 3, "the held-quad schedule needs three k-quads per stage");
     float av[2][FM], bv[2][FN];
-    if constexpr (kHeld) {
-        float hold_a[2][FM], hold_b[2][FN];
-        if (steps > 0) read_operands(0, av[0], bv[0]);
-        for (int32_t step = 0; step < steps; ++step) {
-            const bool more = step + 1 < steps;
-            if (more) {
-                const int64_t r_next = r_begin + (int64_t)(step + 1) * BK;
-                lx.load(p.conv, r_next, room_of(step + 1), tid);
-                ly.template load<kWholeSteps>(p.conv, r_next, room_of(step + 1), tid);
-            }
-            // The operands of the next k-quad are read before this quad's MFMAs issue, and the
-            // scheduling barriers keep that order: each LDS read has a whole MFMA group to land
-            // (left to itself the compiler sinks every read to just before its use).
+    float hold_a[2][FM], hold_b[2][FN];
+    if (steps > 0) read_operands(0, av[0], bv[0]);
+    for (int32_t step = 0; step < steps; ++step) {
+        const bool more = step + 1 < steps;
+        if (more) {
+            const int64_t r_next = r_begin + (int64_t)(step + 1) * BK;
+            lx.load(p.conv, r_next, room_of(step + 1), tid);
+            ly.template load<kWholeSteps>(p.conv, r_next, room_of(step + 1), tid);
+        }
+        // The operands of the next k-quad are read before this quad's MFMAs issue, and the
+        // scheduling barriers keep that order: each LDS read has a whole MFMA group to land
+        // (left to itself the compiler sinks every read to just before its use).
 #pragma unroll
-            for (int q = 0; q < kQuads - 2; ++q) {
-                const int cur = q & 1;
-                if (q + 1 < kQuads - 2) {
-                    read_operands(4 * (q + 1), av[cur ^ 1], bv[cur ^ 1]);
-                } else {
-                    read_operands(4 * (kQuads - 2), hold_a[0], hold_b[0]);
-                    read_operands(4 * (kQuads - 1), hold_a[1], hold_b[1]);
-                }
-                __builtin_amdgcn_sched_barrier(0);
-                mma_quad(av[cur], bv[cur]);
-                __builtin_amdgcn_sched_barrier(0);
+        for (int q = 0; q < kQuads - 2; ++q) {
+            const int cur = q & 1;
+            if (q + 1 < kQuads - 2) {
+                read_operands(4 * (q + 1), av[cur ^ 1], bv[cur ^ 1]);
+            } else {
+                read_operands(4 * (kQuads - 2), hold_a[0], hold_b[0]);
+                read_operands(4 * (kQuads - 1), hold_a[1], hold_b[1]);
             }
-            // After the last step the stores, the barrier and the reads below handle stale registers
-            // and LDS nothing reads: unconditional, they keep the loop free of flag tests.
-            __syncthreads();  // every wave is done reading this stage
-            lx.store(xs, tid, bf16);
-            ly.store(ys, tid, bf16);
-            mma_quad(hold_a[0], hold_b[0]);
             __builtin_amdgcn_sched_barrier(0);
-            __syncthreads();  // the next stage is in LDS
-            read_operands(0, av[0], bv[0]);
-            mma_quad(hold_a[1], hold_b[1]);
+            mma_quad(av[cur], bv[cur]);
             __builtin_amdgcn_sched_barrier(0);
         }
-    } else {
-        for (int32_t step = 0; step < steps; ++step) {
-            const bool more = step + 1 < steps;
-            if (more) {
-                const int64_t r_next = r_begin + (int64_t)(step + 1) * BK;
-                lx.load(p.conv, r_next, room_of(step + 1), tid);
-                ly.template load<kWholeSteps>(p.conv, r_next, room_of(step + 1), tid);
-            }
-            read_operands(0, av[0], bv[0]);
-#pragma unroll
-            for (int q = 0; q < kQuads; ++q) {
-                const int cur = q & 1;
-                if (q + 1 < kQuads) read_operands(4 * (q + 1), av[cur ^ 1], bv[cur ^ 1]);
-                __builtin_amdgcn_sched_barrier(0);
-                mma_quad(av[cur], bv[cur]);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-            __syncthreads();
-            if (more) {
-                lx.store(xs, tid, bf16);
-                ly.store(ys, tid, bf16);
-                __syncthreads();
-            }
-        }
+        // After the last step the stores, the barrier and the reads below handle stale registers
+        // and LDS nothing reads: unconditional, they keep the loop free of flag tests.
+        __syncthreads();  // every wave is done reading this stage
+        lx.store(xs, tid, bf16);
+        ly.store(ys, tid, bf16);
+        mma_quad(hold_a[0], hold_b[0]);
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();  // the next stage is in LDS
+        read_operands(0, av[0], bv[0]);
+        mma_quad(hold_a[1], hold_b[1]);
+        __builtin_amdgcn_sched_barrier(0);
     }
 
     // acc[a][b][v] is tile row wm*TM + FM*(4*quad + v) + a, column wn*TN + FN*l16 + b: a lane's
@@ -1091,7 +1063,7 @@ struct Choice {
 
 Choice choose(int64_t m, int64_t n, int64_t k, int64_t batch, int64_t cus, bool pool_epilogue) {
     const Choice large{Shape::Large, 128, 128, 32, 2}, tall{Shape::Tall, 128, 64, 32, 3},
-        small{Shape::Small, 64, 64, 32, 5};
+        small{Shape::Small, 64, 64, 32, 4};
     if (m < 128 && !pool_epilogue) return small;
     if (n < 128) return n <= 64 || pool_epilogue ? tall : small;
     const int64_t tiles = ((m + 127) / 128) * ((n + 127) / 128) * batch;
@@ -1115,7 +1087,7 @@ struct DenseSchedule {
 
 DenseSchedule dense_schedule(int64_t m, int64_t n, int64_t k, int64_t batch, int64_t cus) {
     const Choice shapes[3] = {{Shape::Large, 128, 128, 32, 2}, {Shape::Tall, 128, 64, 32, 3},
-                              {Shape::Small, 64, 64, 32, 5}};
+                              {Shape::Small, 64, 64, 32, 4}};
     const double eff[3] = {1.0, 0.96, 0.92};
     const int64_t out_len = batch * m * n;
     DenseSchedule best{shapes[0], 1};
