@@ -581,8 +581,10 @@ __device__ __forceinline__ float finish_value(const float *bias, const float *d,
 // XMODE: 0 dense X, 1 convolution rows mode, 2 convolution cols mode, 3 cols mode over aligned
 // pixel steps, 4 rows mode through buffer loads.
 // EPI: 0 store C (+ bias), 1 bias + ReLU + max pool of whole windows (rows are output pixels).
-// Blocks per CU the register budget is held to (two large, three tall, four small tiles).
-constexpr int gemm_blocks_per_cu(int bm, int bn) { return bm == 128 && bn == 128 ? 2 : bm == 128 ? 3 : 4; }
+// Blocks per CU the register budget is held to (two large, three tall or wide, four small tiles).
+constexpr int gemm_blocks_per_cu(int bm, int bn) {
+    return bm == 128 && bn == 128 ? 2 : bm == 128 || bn == 128 ? 3 : 4;
+}
 
 template <int BM, int BN, int BK, int WM, int WN, bool XR, bool YR, int VX, int VY, int XMODE, int EPI>
 __global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
@@ -1052,20 +1054,23 @@ bool vec_ok(const float *base, int64_t contiguous_extent, int64_t other_stride) 
 }
 
 // Tile shapes, all 32 deep per LDS stage: large 128x128 when both output extents fill it; 128x64
-// when the columns are few (<= 64); 64x64 otherwise.  Resident blocks per CU follow from the
-// register budget of each shape.
-enum class Shape { Large, Tall, Small };
+// when the columns are few (<= 64); 64x64 otherwise; 64x128 for weight gradients whose rows leave
+// the last 128-row tile at most half full (conv2's 576 patch rows: 4.5 large tiles, 9 wide ones).
+// Resident blocks per CU follow from the register budget of each shape.
+enum class Shape { Large, Tall, Small, Wide };
 
 struct Choice {
     Shape shape;
     int bm, bn, bk, per_cu;
 };
 
-Choice choose(int64_t m, int64_t n, int64_t k, int64_t batch, int64_t cus, bool pool_epilogue) {
+Choice choose(int64_t m, int64_t n, int64_t k, int64_t batch, int64_t cus, bool pool_epilogue,
+              bool wide_ok = false) {
     const Choice large{Shape::Large, 128, 128, 32, 2}, tall{Shape::Tall, 128, 64, 32, 3},
-        small{Shape::Small, 64, 64, 32, 4};
+        small{Shape::Small, 64, 64, 32, 4}, wide{Shape::Wide, 64, 128, 32, 3};
     if (m < 128 && !pool_epilogue) return small;
     if (n < 128) return n <= 64 || pool_epilogue ? tall : small;
+    if (wide_ok && m % 128 != 0 && m % 128 <= 64) return wide;
     const int64_t tiles = ((m + 127) / 128) * ((n + 127) / 128) * batch;
     // A short reduction over few large tiles (e.g. a classifier layer) would leave most CUs idle
     // and each block only a few K steps: four times as many small tiles finish sooner.
@@ -1215,7 +1220,7 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out, const 
         }
     p.bf16 = device->bf16_matmul;
     const int64_t cus = device->multiprocessors;
-    Choice ch = choose(p.m, p.n, p.k, batch, cus, EPI == 1);
+    Choice ch = choose(p.m, p.n, p.k, batch, cus, EPI == 1, XMODE == 3);
     int64_t scheduled_splits = 0;
     if constexpr (XMODE == 0 && EPI == 0) {
         const int64_t large_tiles = ((p.m + 127) / 128) * ((p.n + 127) / 128) * batch;
@@ -1318,8 +1323,10 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out, const 
             launch_vec<128, 128, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, device->stream, vx, vy);
         else if (ch.shape == Shape::Tall)
             launch_vec<128, 64, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, device->stream, vx, vy);
-        else
+        else if (ch.shape == Shape::Small)
             launch_vec<64, 64, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, device->stream, vx, vy);
+        else if constexpr (XMODE == 3)  // Wide: cols-mode weight gradients only
+            launch_vec<64, 128, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, device->stream, vx, vy);
     }
     int status = axis::launch_status("gemm_kernel");
     if (status) return status;
