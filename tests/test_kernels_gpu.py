@@ -764,15 +764,18 @@ def test_bf16_convolution_entries(dev_bf16, oracle, layout, b, c, h, w, n):
 
 # ---------------------------------------------------------------- implicit-GEMM convolution
 
-# Outputs of 16x16, 8x8, 32x32 (stride 2, and padding 0) and 64x64 pixels take the weight
-# gradient's aligned-step loader; the others its general one.  The last two are data gradients of
-# few channels over many pixels (aligned tap steps, then a ragged last tile with the general decode).
+# Outputs of 16x16, 8x8, 32x32 (stride 2, and padding 0), 64x64 and 128x128 pixels take the weight
+# gradient's aligned-step loader (128 columns: steps inside the row as well as at its two ends; a 5x5
+# kernel with padding 2 over 16-wide rows: two rows per step); the others its general one.  Two
+# cases are data gradients of few channels over many pixels (aligned tap steps, then a ragged last
+# tile with the general decode); 64 channels under 3x3 (576 patch rows) take 64x128 tiles.
 @pytest.mark.parametrize("b,h,w,c,n,k,s,p", [(2, 9, 7, 8, 16, 3, 1, 1), (3, 16, 16, 64, 128, 3, 1, 1),
                                              (2, 11, 10, 5, 7, 3, 1, 0), (2, 9, 8, 12, 20, 3, 2, 1),
                                              (1, 8, 8, 128, 256, 3, 1, 1), (2, 6, 6, 4, 8, 2, 1, 1),
                                              (2, 64, 64, 8, 16, 3, 2, 1), (2, 34, 34, 4, 8, 3, 1, 0),
                                              (1, 64, 64, 3, 64, 3, 1, 1), (32, 64, 64, 32, 64, 3, 1, 1),
-                                             (34, 63, 63, 24, 40, 3, 1, 1)])
+                                             (34, 63, 63, 24, 40, 3, 1, 1), (1, 128, 128, 4, 8, 3, 1, 1),
+                                             (1, 128, 128, 8, 16, 3, 2, 1), (2, 16, 16, 8, 16, 5, 1, 2)])
 def test_conv2d_entries_match_explicit_lowering(dev, oracle, b, h, w, c, n, k, s, p):
     rng = np.random.default_rng(b * 100 + c)
     x = rng.standard_normal(b * h * w * c).astype(np.float32)
