@@ -151,8 +151,8 @@ __device__ __forceinline__ void load_into(float *reg, const float *src, bool val
 // Buffer loads: an offset at or past the resource's record count (2^31 - 1 bytes) reads as zero,
 // so padding taps and reduction tails need neither a branch nor zeroed registers.
 constexpr uint32_t kOutside = 0x80000000u;
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const float *base) {
-    return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, 0x7fffffff, 0x00020000);
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const float *base, int32_t bytes = 0x7fffffff) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, bytes, 0x00020000);
 }
 template <int VEC>
 __device__ __forceinline__ void buffer_into(float *reg, __amdgpu_buffer_rsrc_t rsrc, uint32_t byte_offset) {
@@ -282,13 +282,23 @@ struct DenseLoader : Staging<BT, BK, NT, RCONTIG, VEC> {
             }
             step = q0 * taps.qa + (int64_t)pos * taps.pb + taps.pc;
         }
-        const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(uniform_ptr(tile_base + step));
-        // Branch-free: split into whole-step and partial-step paths, the loads' wait counts merge
-        // conservatively and the next loads wait on this step's.  room - r_wave is scalar work;
-        // r-contiguous operands share one compare for every vector.
+        if constexpr (RCONTIG) {
+            const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(uniform_ptr(tile_base + step));
+            // Branch-free: split into whole-step and partial-step paths, the loads' wait counts
+            // merge conservatively and the next loads wait on this step's.  room - r_wave is
+            // scalar work, and every vector shares the one compare.
 #pragma unroll
-        for (int e = 0; e < S::kVecs; ++e)
-            buffer_into<VEC>(this->reg + e * VEC, rsrc, WHOLE || r_lane < room - r_wave[e] ? voff[e] : kOutside);
+            for (int e = 0; e < S::kVecs; ++e)
+                buffer_into<VEC>(this->reg + e * VEC, rsrc, WHOLE || r_lane < room - r_wave[e] ? voff[e] : kOutside);
+        } else {
+            // t-contiguous rows (s_t = 1 and rows no longer than their pitch, which the host
+            // checks): a row past the step's depth starts at or after byte room * s_r * 4 of the
+            // step, so the resource's record count masks it with no vector instruction.
+            const int32_t bytes = WHOLE || room >= BK ? 0x7fffffff : (int32_t)(room * s_r * 4);
+            const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(uniform_ptr(tile_base + step), bytes);
+#pragma unroll
+            for (int e = 0; e < S::kVecs; ++e) buffer_into<VEC>(this->reg + e * VEC, rsrc, voff[e]);
+        }
     }
 };
 
@@ -1261,6 +1271,10 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out, const 
         return axis::fail(AXIS_ERROR_INVALID, "matmul operand row pitch must stay below 4,227,000 elements");
     if (!reach(p.y_sj, p.y_sr))
         return axis::fail(AXIS_ERROR_INVALID, "matmul operand row pitch must stay below 4,227,000 elements");
+    // t-contiguous dense operands bound a K step's rows by the resource's record count: unit
+    // element stride and rows no longer than their pitch (every entry point lays them out so)
+    if ((XMODE == 0 && !XR && (p.x_si != 1 || p.x_sr < p.m)) || (!YR && (p.y_sj != 1 || p.y_sr < p.n)))
+        return axis::fail(AXIS_ERROR_INVALID, "t-contiguous product operand without unit stride and full-row pitch");
     bool vx;
     if constexpr (XMODE == 0)
         vx = XR ? vec_ok(p.x, p.k, p.x_si) && p.x_batch % 4 == 0
