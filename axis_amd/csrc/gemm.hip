@@ -1088,11 +1088,12 @@ Choice choose(int64_t m, int64_t n, int64_t k, int64_t batch, int64_t cus, bool 
     return large;
 }
 
-// Dense products whose 128x128 tiles number fewer than two per CU: every (tile shape, slice count)
-// is priced as the time of the busiest CU -- ceil(blocks / CUs) blocks of BM x BN x chunk products at
-// a per-CU rate measured on these kernels (0.46 GFLOP/ms with two or more resident blocks; a CU
-// left one resident block at a time runs 16% slower) scaled by the shape's efficiency -- plus the slice sum
-// (partials written and read once at ~5 TB/s and a launch).  The 8192 x 784 x 1024 products of a
+// Dense products whose 128x128 tiles number fewer than two per CU (reductions of 4 K steps or
+// more): every (tile shape, slice count) is priced as the time of the busiest CU --
+// ceil(blocks / CUs) blocks of BM x BN x chunk products at a per-CU rate measured on these kernels
+// (0.46 GFLOP/ms with two or more resident blocks; a CU left one resident block at a time runs 16%
+// slower) scaled by the shape's efficiency, at least the load latency of each round's K steps --
+// plus the slice sum (partials written and read once at ~5 TB/s and a launch).  The 8192 x 784 x 1024 products of a
 // 784-wide layer: 128x128 tiles leave 64 CUs one block and 192 two (143 us); 64x64 tiles, unsplit
 // for the data gradient and in six slices for the weight gradient, run in 130 us.
 struct DenseSchedule {
@@ -1111,7 +1112,7 @@ DenseSchedule dense_schedule(int64_t m, int64_t n, int64_t k, int64_t batch, int
         const Choice &sh = shapes[c];
         if (sh.shape == Shape::Tall && n > 64) continue;
         const int64_t tiles = ((m + sh.bm - 1) / sh.bm) * ((n + sh.bn - 1) / sh.bn) * batch;
-        const int64_t most = std::max<int64_t>(1, k / (sh.bk * 4));
+        const int64_t most = std::max<int64_t>(1, k / (sh.bk * 2));
         for (int64_t want = 1; want <= std::min<int64_t>(most, 64); ++want) {
             int64_t chunk = (k + want - 1) / want;
             chunk = (chunk + sh.bk - 1) / sh.bk * sh.bk;
@@ -1122,6 +1123,10 @@ DenseSchedule dense_schedule(int64_t m, int64_t n, int64_t k, int64_t batch, int
             const int64_t per_cu = (blocks + cus - 1) / cus;
             const double occ = std::min<int64_t>(per_cu, sh.per_cu) >= 2 ? 1.0 : 0.84;
             double us = (double)per_cu * 2.0 * sh.bm * sh.bn * (double)chunk / (0.46e6 * eff[c] * occ);
+            // latency floor: a block's K steps each wait on their loads when the CU holds too few
+            // blocks to cover them (~1 us per step, ~2 us to start), once per round of resident blocks
+            const int64_t rounds = (per_cu + sh.per_cu - 1) / sh.per_cu;
+            us = std::max(us, (double)rounds * (1.0 * (double)(chunk / sh.bk) + 2.0));
             if (splits > 1) us += (double)(splits + 1) * (double)out_len * 4.0 / 5.0e6 + 3.0;
             if (us < best_us) {
                 best_us = us;
@@ -1234,7 +1239,7 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out, const 
     int64_t scheduled_splits = 0;
     if constexpr (XMODE == 0 && EPI == 0) {
         const int64_t large_tiles = ((p.m + 127) / 128) * ((p.n + 127) / 128) * batch;
-        if (!p.perm_c && large_tiles < 2 * cus && p.k >= 16 * 32) {
+        if (!p.perm_c && large_tiles < 2 * cus && p.k >= 4 * 32) {
             const DenseSchedule d = dense_schedule(p.m, p.n, p.k, batch, cus);
             ch = d.choice;
             scheduled_splits = d.splits;
@@ -1244,10 +1249,11 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out, const 
     p.tiles_m = static_cast<int32_t>((p.m + ch.bm - 1) / ch.bm);
     p.tiles_n = static_cast<int32_t>((p.n + ch.bn - 1) / ch.bn);
     const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n * batch;
-    // Split the reduction when the tiles alone cannot fill the chip: aim at one full round of
-    // resident blocks so no round runs nearly empty.  The pooling epilogue needs whole sums.
-    // Reductions under 16 K steps are not split (the extra sum launch would cost more than it
-    // saves).  The partial slices stay within 64 MiB.
+    // Split the reduction when the tiles alone cannot fill the chip (dense products: as the
+    // schedule above decided): aim at one full round of resident blocks so no round runs nearly
+    // empty.  The pooling epilogue needs whole sums.  Other reductions under 16 K steps are not
+    // split (the extra sum launch would cost more than it saves).  The partial slices stay within
+    // 64 MiB.
     const int64_t slots = cus * ch.per_cu;
     const int64_t out_len = batch * p.m * p.n;
     int64_t splits = 1;
