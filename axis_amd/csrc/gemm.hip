@@ -23,9 +23,11 @@
 //
 // Tiles are staged through LDS as [r][i] / [r][j] so every MFMA operand read is a unit-stride
 // LDS access across the wave.  The next K tile is prefetched into registers while the current
-// one feeds the MFMAs.  When the output has too few tiles to fill 256 CUs, the reduction is
-// split into slices whose partial tiles are summed afterwards in a fixed order (deterministic,
-// no atomics).
+// one feeds the MFMAs, and the last two k-quads of each stage are held in registers across the
+// stage barriers.  MFMA and vector instructions do not overlap on this part (one wave of each on
+// a SIMD takes the sum of their times), so the K loop keeps vector work to a few instructions
+// per step.  When the output has too few tiles to fill 256 CUs, the reduction is split into
+// slices whose partial tiles are summed afterwards in a fixed order (deterministic, no atomics).
 #include <algorithm>
 #include <cfloat>
 #include <mutex>
@@ -47,8 +49,8 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 // Split partial sums of the allocation-free weight gradient (axis_matmul_right_backward_noalloc).
 // One copy per GPU, alive until the process ends.  Host code never passes this name to a kernel:
 // it is a host-side stand-in, and kernels take the device address hipGetSymbolAddress returns
-// (axis_device_s::static_scratch).  Under the split rule of run_gemm one launch needs at most
-// slots * tile area + its range sums (768 * 128 * 128 + 3% floats on 256 CUs, about 53 MB).
+// (axis_device_s::static_scratch).  The split rules of run_gemm keep a launch's partial slices
+// within 64 MiB; one whose slices and range sums would not fit here is rejected before it runs.
 constexpr int64_t kStaticScratchFloats = int64_t(16) << 20;  // 64 MiB
 static __device__ __align__(256) float scratch[kStaticScratchFloats];
 
