@@ -182,7 +182,11 @@ struct Staging {
     static_assert(BT % 64 == 0, "the swizzle permutes columns inside aligned groups of 64");
     static constexpr int kElems = BT * BK / NT;  // floats per thread
     static constexpr int kVecs = kElems / VEC;
-    static constexpr int LD = BT + 4;
+    // Row pitch: t-contiguous operands BT + 4 (their 16-byte stores along t spread over the banks
+    // by the padding); r-contiguous ones BT + 64, a multiple of 64 words, so the four rows a lane
+    // writes sit 3 x 256 bytes apart and two ds_write2st64 reach them from one address register
+    // (the XOR swizzle alone keeps those stores and the operand reads free of bank conflicts).
+    static constexpr int LD = RCONTIG ? BT + 64 : BT + 4;
     static constexpr int kPer = RCONTIG ? BK / VEC : BT / VEC;  // vectors per contiguous line
     float reg[kElems];
 
