@@ -721,43 +721,62 @@ __global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
     // two 128x128, three 128x64 or four 64x64 blocks per CU).
     constexpr int kQuads = BK / 4;
     static_assert(kQuads >= 3, "the held-quad schedule needs three k-quads per stage");
-    float av[2][FM], bv[2][FN];
-    float hold_a[2][FM], hold_b[2][FN];
-    if (steps > 0) read_operands(0, av[0], bv[0]);
-    for (int32_t step = 0; step < steps; ++step) {
-        const bool more = step + 1 < steps;
-        if (more) {
-            const int64_t r_next = r_begin + (int64_t)(step + 1) * BK;
-            lx.load(p.conv, r_next, room_of(step + 1), tid);
-            ly.template load<kWholeSteps>(p.conv, r_next, room_of(step + 1), tid);
-        }
-        // The operands of the next k-quad are read before this quad's MFMAs issue, and the
-        // scheduling barriers keep that order: each LDS read has a whole MFMA group to land
-        // (left to itself the compiler sinks every read to just before its use).
-#pragma unroll
-        for (int q = 0; q < kQuads - 2; ++q) {
-            const int cur = q & 1;
-            if (q + 1 < kQuads - 2) {
-                read_operands(4 * (q + 1), av[cur ^ 1], bv[cur ^ 1]);
-            } else {
-                read_operands(4 * (kQuads - 2), hold_a[0], hold_b[0]);
-                read_operands(4 * (kQuads - 1), hold_a[1], hold_b[1]);
+    // The K loop in two forms for dense products: every step whole (the depth tests of
+    // r-contiguous operands compiled out) or a partial last step; a launch takes one.
+    // Convolution launches keep one form (their dense operand is bounded by the record count).
+    auto k_loop = [&](auto whole) {
+        constexpr bool kW = decltype(whole)::value;
+        float av[2][FM], bv[2][FN];
+        float hold_a[2][FM], hold_b[2][FN];
+        if (steps > 0) read_operands(0, av[0], bv[0]);
+        for (int32_t step = 0; step < steps; ++step) {
+            const bool more = step + 1 < steps;
+            if (more) {
+                const int64_t r_next = r_begin + (int64_t)(step + 1) * BK;
+                if constexpr (XMODE == 0)
+                    lx.template load<kW>(p.conv, r_next, room_of(step + 1), tid);
+                else
+                    lx.load(p.conv, r_next, room_of(step + 1), tid);
+                ly.template load<kW>(p.conv, r_next, room_of(step + 1), tid);
             }
+            // The operands of the next k-quad are read before this quad's MFMAs issue, and the
+            // scheduling barriers keep that order: each LDS read has a whole MFMA group to land
+            // (left to itself the compiler sinks every read to just before its use).
+#pragma unroll
+            for (int q = 0; q < kQuads - 2; ++q) {
+                const int cur = q & 1;
+                if (q + 1 < kQuads - 2) {
+                    read_operands(4 * (q + 1), av[cur ^ 1], bv[cur ^ 1]);
+                } else {
+                    read_operands(4 * (kQuads - 2), hold_a[0], hold_b[0]);
+                    read_operands(4 * (kQuads - 1), hold_a[1], hold_b[1]);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                mma_quad(av[cur], bv[cur]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            // After the last step the stores, the barrier and the reads below handle stale
+            // registers and LDS nothing reads: unconditional, they keep the loop free of flag tests.
+            __syncthreads();  // every wave is done reading this stage
+            lx.store(xs, tid, bf16);
+            ly.store(ys, tid, bf16);
+            mma_quad(hold_a[0], hold_b[0]);
             __builtin_amdgcn_sched_barrier(0);
-            mma_quad(av[cur], bv[cur]);
+            __syncthreads();  // the next stage is in LDS
+            read_operands(0, av[0], bv[0]);
+            mma_quad(hold_a[1], hold_b[1]);
             __builtin_amdgcn_sched_barrier(0);
         }
-        // After the last step the stores, the barrier and the reads below handle stale registers
-        // and LDS nothing reads: unconditional, they keep the loop free of flag tests.
-        __syncthreads();  // every wave is done reading this stage
-        lx.store(xs, tid, bf16);
-        ly.store(ys, tid, bf16);
-        mma_quad(hold_a[0], hold_b[0]);
-        __builtin_amdgcn_sched_barrier(0);
-        __syncthreads();  // the next stage is in LDS
-        read_operands(0, av[0], bv[0]);
-        mma_quad(hold_a[1], hold_b[1]);
-        __builtin_amdgcn_sched_barrier(0);
+    };
+    if constexpr (kWholeSteps) {
+        k_loop(std::true_type{});
+    } else if constexpr (XMODE != 0) {
+        k_loop(std::false_type{});
+    } else {
+        if (tail == BK)
+            k_loop(std::true_type{});
+        else
+            k_loop(std::false_type{});
     }
 
     // acc[a][b][v] is tile row wm*TM + FM*(4*quad + v) + a, column wn*TN + FN*l16 + b: a lane's
