@@ -411,7 +411,9 @@ def min_plans(dims, strides, axis, cap=True):
     extent = dims[red][1]
     out_dims = [(a, e) for a, e in dims if a != axis]
     olen = shape_len(out_dims)
-    grid = np.indices([e for _, e in out_dims]).reshape(len(out_dims), -1)
+    # a rank-0 result (the only axis reduced) is one group
+    grid = (np.indices([e for _, e in out_dims]).reshape(len(out_dims), -1) if out_dims
+            else np.zeros((0, 1), np.int64))
     base = np.zeros(olen, np.int64)
     k = 0
     for d in range(len(dims)):

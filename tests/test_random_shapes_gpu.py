@@ -215,3 +215,206 @@ def test_random_relu_pool_shapes(dev, oracle, b, h, w, c, n, k, ph, pw, channel_
                  (I32 * 2)(ph, pw), (I32 * 2)(0, 0))
         assert np.array_equal(dev.read(p2, pooled_len), got)
         assert np.array_equal(dev.read(a2, pooled_len, np.uint8), got_arg)
+
+
+# ---------------------------------------------------------------- bit-exact index and reduction kernels
+
+def _unfold_cases():
+    rng = np.random.default_rng(4242)
+    cases = []
+    while len(cases) < 16:
+        kh, kw = int(rng.integers(1, 5)), int(rng.integers(1, 5))
+        sy, sx = int(rng.integers(1, 4)), int(rng.integers(1, 4))
+        py, px = int(rng.integers(0, kh)), int(rng.integers(0, kw))
+        h, w = int(rng.integers(1, 20)), int(rng.integers(1, 20))
+        if h + 2 * py < kh or w + 2 * px < kw:
+            continue
+        groups = int(rng.choice([1, 1, 2, 3]))
+        c = groups * int(rng.integers(1, 6))
+        b = int(rng.integers(1, 4))
+        names = ["batch", "channel", "height", "width"]
+        order = [names[i] for i in rng.permutation(4)]
+        fill = float(rng.choice([0.0, -np.inf]))
+        cases.append((b, c, h, w, groups, [kh, kw], [sy, sx], [py, px], order, fill))
+    return cases
+
+
+UNFOLD_RANDOM = _unfold_cases()
+
+
+@pytest.mark.parametrize("b,c,h,w,groups,kernel,stride,padding,order,fill", UNFOLD_RANDOM)
+def test_random_unfold_and_col2im(dev, oracle, b, c, h, w, groups, kernel, stride, padding, order, fill):
+    import ctypes
+
+    dims = [("batch", b), ("channel", c), ("height", h), ("width", w)]
+    strides = oracle.layout_for(dims, order)
+    u = oracle.unfold_spec(dims, strides, "channel", ["height", "width"], ("group", groups),
+                           ("patch", c // groups * kernel[0] * kernel[1]), kernel, stride, padding, fill)
+    spec = hip.UnfoldSpec()
+    ctypes.memmove(ctypes.byref(spec), ctypes.byref(u.spec), ctypes.sizeof(spec))
+    rng = np.random.default_rng(b * 1000 + c * 100 + h * 10 + w)
+    x = rng.standard_normal(oracle.shape_len(dims)).astype(np.float32)
+    dx, out = _up(dev, x), dev.empty(spec.output_len)
+    dev.call("axis_unfold", dx.vp, out.vp, ctypes.byref(spec))
+    assert np.array_equal(dev.read(out, spec.output_len), oracle.unfold2d(x, u))
+    y = rng.standard_normal(spec.output_len).astype(np.float32)
+    dy, back = _up(dev, y), dev.empty(spec.input_len)
+    dev.call("axis_unfold_backward", dy.vp, back.vp, ctypes.byref(spec))
+    assert np.array_equal(dev.read(back, spec.input_len), oracle.unfold2d_backward(y, u, len(x)))
+
+
+def _pool_cases():
+    rng = np.random.default_rng(777)
+    cases = []
+    while len(cases) < 12:
+        kh, kw = int(rng.integers(1, 5)), int(rng.integers(1, 5))
+        sy, sx = int(rng.integers(1, 4)), int(rng.integers(1, 4))
+        py, px = int(rng.integers(0, (kh + 1) // 2)), int(rng.integers(0, (kw + 1) // 2))
+        h, w = int(rng.integers(kh, 24)), int(rng.integers(kw, 24))
+        cases.append((int(rng.integers(1, 4)), h, w, int(rng.integers(1, 70)), [kh, kw], [sy, sx], [py, px]))
+    return cases
+
+
+@pytest.mark.parametrize("b,h,w,c,kernel,stride,padding", _pool_cases())
+def test_random_max_pool(dev, oracle, b, h, w, c, kernel, stride, padding):
+    from axis_amd.hip import I64 as L
+
+    rng = np.random.default_rng(b * 7 + h * 5 + w * 3 + c)
+    x = rng.integers(-3, 4, b * h * w * c).astype(np.float32)  # ties everywhere
+    x[::23] = np.nan
+    x[::29] = np.inf
+    dims = [("batch", b), ("height", h), ("width", w), ("c", c)]
+    u = oracle.unfold_spec(dims, oracle.contiguous(dims), "c", ["height", "width"], ("c", c),
+                           ("pool", kernel[0] * kernel[1]), kernel, stride, padding, float("-inf"))
+    q = oracle.scale(oracle.unfold2d(x, u), -1.0)
+    _, fwd, rev = oracle.min_plans(u.shape, u.strides, "pool")
+    mn, mask, _ = oracle.grouped_minimum(q, fwd, rev)
+    ref = oracle.scale(mn, -1.0)
+    n_out = len(ref)
+    gout = rng.standard_normal(n_out).astype(np.float32)
+    gg = oracle.mask_gradient(oracle.grouped(oracle.scale(gout, -1.0), None, rev, 1.0), mask)
+    ref_dx = oracle.unfold2d_backward(oracle.scale(gg, -1.0), u, len(x))
+    k, s, p = (I32 * 2)(*kernel), (I32 * 2)(*stride), (I32 * 2)(*padding)
+    dx, out, arg = _up(dev, x), dev.empty(n_out), dev.empty(n_out, np.uint8)
+    dev.call("axis_max_pool2d", dx.vp, out.vp, arg.vp, L(b), I32(h), I32(w), L(c), k, s, p)
+    got = dev.read(out, n_out)
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    assert np.array_equal(got[~np.isnan(ref)], ref[~np.isnan(ref)])
+    dg, back = _up(dev, gout), dev.empty(len(x))
+    dev.call("axis_max_pool2d_backward", dg.vp, arg.vp, back.vp, L(b), I32(h), I32(w), L(c), k, s, p)
+    assert np.array_equal(dev.read(back, len(x)), ref_dx)
+
+
+def _axes_cases():
+    rng = np.random.default_rng(99)
+    cases = []
+    for i in range(14):
+        rank = int(rng.integers(1, 5))
+        names = "abcd"[:rank]
+        dims = [(names[j], int(rng.choice([1, int(rng.integers(2, 9)), int(rng.integers(9, 300))]))) for j in range(rank)]
+        while int(np.prod([e for _, e in dims])) > 400000:
+            dims = [(n_, max(1, e // 2)) for n_, e in dims]
+        order = [names[j] for j in rng.permutation(rank)]
+        k = int(rng.integers(1, rank + 1))
+        axes = [names[j] for j in sorted(rng.choice(rank, size=k, replace=False))]
+        cases.append((dims, order, axes, bool(i % 2)))
+    return cases
+
+
+@pytest.mark.parametrize("dims,order,axes,mean", _axes_cases())
+def test_random_reduce_axes(dev, oracle, dims, order, axes, mean):
+    from axis_amd.hip import F32, VP
+
+    rng = np.random.default_rng(sum(e for _, e in dims) * 13 + len(axes))
+    n = int(np.prod([e for _, e in dims]))
+    a = rng.standard_normal(n).astype(np.float32)
+    strides = oracle.layout_for(dims, order)
+    out_dims, fwd, rev, factor = oracle.reduction_plans(dims, strides, axes, mean)
+    olen = int(np.prod([e for _, e in out_dims])) if out_dims else 1
+    ext = np.array([e for _, e in dims], np.int64)
+    st = np.array(strides, np.int64)
+    red = np.array([1 if name in axes else 0 for name, _ in dims], np.int32)
+    geo = (I32(len(dims)), ext.ctypes.data_as(VP), st.ctypes.data_as(VP), red.ctypes.data_as(VP), F32(factor))
+    da, out = _up(dev, a), dev.empty(olen)
+    dev.call("axis_reduce_axes", da.vp, out.vp, *geo)
+    got = dev.read(out, olen)
+    assert np.array_equal(got, oracle.grouped(a, None, fwd, factor))
+    back = dev.empty(n)
+    dev.call("axis_reduce_axes_backward", out.vp, back.vp, *geo)
+    assert np.array_equal(dev.read(back, n), oracle.grouped(got, None, rev, factor))
+
+
+def _extreme_cases():
+    rng = np.random.default_rng(31337)
+    cases = []
+    for i in range(12):
+        rank = int(rng.integers(1, 5))
+        names = "abcd"[:rank]
+        dims = [(names[j], int(rng.choice([1, int(rng.integers(2, 10)), int(rng.integers(10, 200))]))) for j in range(rank)]
+        while int(np.prod([e for _, e in dims])) > 300000:
+            dims = [(n_, max(1, e // 2)) for n_, e in dims]
+        order = [names[j] for j in rng.permutation(rank)]
+        cases.append((dims, order, names[int(rng.integers(0, rank))], bool(i % 2)))
+    return cases
+
+
+@pytest.mark.parametrize("dims,order,axis,maximum", _extreme_cases())
+def test_random_extreme_axis(dev, oracle, dims, order, axis, maximum):
+    from axis_amd.hip import VP
+
+    rng = np.random.default_rng(sum(e for _, e in dims) * 17 + int(maximum))
+    n = int(np.prod([e for _, e in dims]))
+    a = np.round(rng.standard_normal(n) * 3).astype(np.float32) / 3  # many ties
+    a[::19] = np.inf
+    a[::23] = -np.inf
+    a[::29] = np.nan
+    strides = oracle.layout_for(dims, order)
+    out_dims, fwd, rev = oracle.min_plans(dims, strides, axis)
+    olen = int(np.prod([e for _, e in out_dims])) if out_dims else 1
+    ref, ref_mask, _ = oracle.grouped_minimum(a, fwd, rev, maximum)
+    ext = np.array([e for _, e in dims], np.int64)
+    st = np.array(strides, np.int64)
+    geo = (I32(len(dims)), ext.ctypes.data_as(VP), st.ctypes.data_as(VP), I32([nm for nm, _ in dims].index(axis)))
+    da, out, mask = _up(dev, a), dev.empty(olen), dev.empty(n)
+    dev.call("axis_extreme_axis", da.vp, *geo, I32(1 if maximum else 0), out.vp, mask.vp)
+    got = dev.read(out, olen)
+    assert np.array_equal(np.isnan(got), np.isnan(ref)) and np.array_equal(got[~np.isnan(ref)], ref[~np.isnan(ref)])
+    assert np.array_equal(dev.read(mask, n), ref_mask)
+    g = rng.standard_normal(olen).astype(np.float32)
+    dg, back = _up(dev, g), dev.empty(n)
+    dev.call("axis_extreme_axis_backward", dg.vp, mask.vp, *geo, back.vp)
+    expect = oracle.mask_gradient(oracle.grouped(g, None, rev, 1.0), ref_mask)
+    assert np.array_equal(dev.read(back, n).view(np.uint32), expect.view(np.uint32))
+
+
+def _permute_cases():
+    rng = np.random.default_rng(2718)
+    cases = []
+    for _ in range(16):
+        rank = int(rng.integers(2, 6))
+        shape = tuple(int(rng.choice([1, int(rng.integers(2, 8)), int(rng.integers(8, 90))])) for _ in range(rank))
+        while int(np.prod(shape)) > 500000:
+            shape = tuple(max(1, e // 2) for e in shape)
+        cases.append((shape, tuple(int(p) for p in rng.permutation(rank))))
+    return cases
+
+
+@pytest.mark.parametrize("shape,perm", _permute_cases())
+def test_random_permutations(dev, oracle, shape, perm):
+    from axis_amd.hip import VP
+
+    rng = np.random.default_rng(int(np.prod(shape)) + len(shape))
+    n = int(np.prod(shape))
+    x = rng.standard_normal(n).astype(np.float32)
+    src = [int(np.prod(shape[i + 1:])) for i in range(len(shape))]
+    dst_shape = [shape[p] for p in perm]
+    dst_of_axis = {perm[k]: int(np.prod(dst_shape[k + 1:])) for k in range(len(perm))}
+    md = np.array([v for i, e in enumerate(shape) for v in (e, src[i], dst_of_axis[i])], np.int32)
+    dx, out, back = _up(dev, x), dev.empty(n), dev.empty(n)
+    dev.call("axis_select_axis", dx.vp, out.vp, md.ctypes.data_as(VP), I32(len(shape)), I32(0), I64(n))
+    got = dev.read(out, n)
+    assert np.array_equal(got, x.reshape(shape).transpose(perm).reshape(-1))
+    if n <= 1 << 16:
+        assert np.array_equal(got, oracle.select_axis(x, md, len(shape), 0, n))
+    dev.call("axis_select_axis_backward", out.vp, back.vp, md.ctypes.data_as(VP), I32(len(shape)), I32(0), I64(n))
+    assert np.array_equal(dev.read(back, n), x)
