@@ -396,53 +396,56 @@ struct BiasAdd {
 
 // Stage one of the bias gradient: partial[q][c] = sum of rows [512q, 512q+512) of column c,
 // sequentially; optionally masked by relu_input > 0 (and the masked gradient written out).
-// One lane per (chunk, column) pair, columns fastest, so narrow activations still fill blocks.
+// Block (column group, chunk): the chunk's rows of 16 columns are staged in LDS first -- every
+// load of the chunk in flight at once, coalesced in 64-byte row segments -- then one lane per
+// column adds its 512 (or fewer) rows in row order.  A lane summing straight from memory waits on
+// one round trip per batch of loads: 8.4 us for a [256, 1000] gradient against ~3 us staged.
+constexpr int kChunkCols = 16;
 template <bool MASK>
 __global__ void __launch_bounds__(kBlock) column_chunk_kernel(const float *__restrict__ g,
                                                               const float *__restrict__ relu_input,
                                                               float *__restrict__ masked_out,
                                                               float *__restrict__ partial,
-                                                              int64_t rows, int64_t width,
-                                                              int64_t pairs, float *__restrict__ out) {
-    const int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-    if (t >= pairs) return;
-    const int64_t q = t / width;
-    const int64_t c = t - q * width;
-    const int64_t r0 = q * axis::kGroupedChunk;
-    const int64_t r1 = r0 + axis::kGroupedChunk < rows ? r0 + axis::kGroupedChunk : rows;
-    // Rows in order; the loads of 16 rows are issued before their adds.
-    constexpr int kBatch = 16;
-    float sum = 0.0f;
-    int64_t r = r0;
-    for (; r + kBatch <= r1; r += kBatch) {
-        float v[kBatch];
+                                                              int64_t rows, int64_t width, int64_t chunks,
+                                                              float *__restrict__ out) {
+    static_assert(axis::kGroupedChunk * kChunkCols % kBlock == 0, "whole staging passes");
+    constexpr int kPasses = axis::kGroupedChunk * kChunkCols / kBlock;
+    constexpr int kRowsPerPass = kBlock / kChunkCols;
+    __shared__ float staged[axis::kGroupedChunk][kChunkCols + 1];
+    const int tid = threadIdx.x;
+    const int cl = tid % kChunkCols;
+    const int64_t c = (int64_t)blockIdx.x * kChunkCols + cl;
+    for (int64_t q = blockIdx.y; q < chunks; q += gridDim.y) {
+        const int64_t r0 = q * axis::kGroupedChunk;
+        const int n_rows = (int)(r0 + axis::kGroupedChunk < rows ? axis::kGroupedChunk : rows - r0);
+        float v[kPasses];
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) v[u] = g[(r + u) * width + c];
-        if (MASK) {
-#pragma unroll
-            for (int u = 0; u < kBatch; ++u) {
-                const int64_t idx = (r + u) * width + c;
-                v[u] = relu_input[idx] > 0.0f ? v[u] : 0.0f;
-                masked_out[idx] = v[u];
+        for (int u = 0; u < kPasses; ++u) {
+            const int r = u * kRowsPerPass + tid / kChunkCols;
+            v[u] = 0.0f;
+            if (r < n_rows && c < width) {
+                const int64_t idx = (r0 + r) * width + c;
+                v[u] = g[idx];
+                if (MASK) {
+                    v[u] = relu_input[idx] > 0.0f ? v[u] : 0.0f;
+                    masked_out[idx] = v[u];
+                }
             }
         }
+        __syncthreads();  // the previous chunk's sums have read the stage
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) sum = sum + v[u];
-    }
-    for (; r < r1; ++r) {
-        const int64_t idx = r * width + c;
-        float v = g[idx];
-        if (MASK) {
-            v = relu_input[idx] > 0.0f ? v : 0.0f;
-            masked_out[idx] = v;
+        for (int u = 0; u < kPasses; ++u) staged[u * kRowsPerPass + tid / kChunkCols][cl] = v[u];
+        __syncthreads();
+        if (tid < kChunkCols && c < width) {
+            float sum = 0.0f;
+            for (int r = 0; r < n_rows; ++r) sum = sum + staged[r][tid];
+            // A single chunk is also the whole sum: the combine's 0 + p0 (scale 1) written here.
+            if (out)
+                out[c] = 0.0f + sum;
+            else
+                partial[q * width + c] = sum;
         }
-        sum = sum + v;
     }
-    // A single chunk is also the whole sum: the combine's 0 + p0 (scale 1) written here.
-    if (out)
-        out[c] = 0.0f + sum;
-    else
-        partial[q * width + c] = sum;
 }
 
 // out[o][i] = factor * sum_r a[o][r][i] in the reference's chunked order.
@@ -796,18 +799,18 @@ int axis_bias_gradient(axis_device device, const float *gradient, const float *r
     AXIS_REQUIRE(rows >= 1 && width >= 1, "bias_gradient extents must be positive");
     const int64_t chunks = (rows + axis::kGroupedChunk - 1) / axis::kGroupedChunk;
     const int64_t pairs = chunks * width;
-    AXIS_REQUIRE(pairs / kBlock < INT32_MAX && width < INT32_MAX, "bias_gradient too large");
+    AXIS_REQUIRE(width / kChunkCols < INT32_MAX, "bias_gradient too large");
     axis::Scratch partial;
     if (chunks > 1)
         if (int s = partial.get(device, sizeof(float) * (size_t)pairs)) return s;
     float *direct = chunks == 1 ? out : nullptr;
-    const unsigned grid = axis::blocks_for(pairs, kBlock, INT32_MAX);
+    const dim3 grid((unsigned)((width + kChunkCols - 1) / kChunkCols), (unsigned)std::min<int64_t>(chunks, 65535));
     if (relu_input)
         column_chunk_kernel<true><<<grid, kBlock, 0, device->stream>>>(
-            gradient, relu_input, masked_out, partial.as<float>(), rows, width, pairs, direct);
+            gradient, relu_input, masked_out, partial.as<float>(), rows, width, chunks, direct);
     else
         column_chunk_kernel<false><<<grid, kBlock, 0, device->stream>>>(
-            gradient, nullptr, nullptr, partial.as<float>(), rows, width, pairs, direct);
+            gradient, nullptr, nullptr, partial.as<float>(), rows, width, chunks, direct);
     if (int s = axis::launch_status("column_chunk_kernel")) return s;
     if (chunks == 1) return AXIS_OK;
     axis::column_combine_kernel<<<(unsigned)width, 256, 0, device->stream>>>(partial.as<float>(), chunks,

@@ -1620,6 +1620,28 @@ int axis_matmul(axis_device device, const float *a, const float *b, float *out, 
     return run_gemm<true, false, 0, 0>(device, p, batch, out);
 }
 
+int axis_matmul_bias(axis_device device, const float *a, const float *b, const float *bias, float *out,
+                     int64_t batch, int64_t m, int64_t k, int64_t n) {
+    AXIS_ENTER(device);
+    if (int s = check_dims(a, b, out, batch, m, k, n)) return s;
+    AXIS_REQUIRE(bias, "null matmul bias");
+    AXIS_REQUIRE(bias + n <= out || bias >= out + batch * m * n, "matmul bias must not alias the output");
+    GemmParams p{};
+    p.x = a;
+    p.y = b;
+    p.bias = bias;
+    p.m = m;
+    p.n = n;
+    p.k = k;
+    p.x_si = k;
+    p.x_sr = 1;
+    p.y_sr = n;
+    p.y_sj = 1;
+    p.x_batch = m * k;
+    p.y_batch = k * n;
+    return run_gemm<true, false, 0, 0>(device, p, batch, out);
+}
+
 int axis_matmul_axpby(axis_device device, const float *a, const float *b, const float *d, float *out,
                       int64_t batch, int64_t m, int64_t k, int64_t n, float alpha, float beta) {
     AXIS_ENTER(device);

@@ -75,6 +75,8 @@ struct Layout {
 struct DeviceImpl {
     axis_device handle = nullptr;
     int ordinal = 0;
+    // One float holding 1.0, written once: the seed adjoint of backward() (read-only by every rule).
+    void *one = nullptr;
     ~DeviceImpl();
 };
 
@@ -82,6 +84,7 @@ struct BufferImpl {
     std::shared_ptr<DeviceImpl> device;
     void *ptr = nullptr;
     int64_t bytes = 0;
+    bool owned = true;  // false for views of device-held memory (the seed)
     ~BufferImpl();
     float *f32() const { return static_cast<float *>(ptr); }
     int64_t floats() const { return bytes / 4; }
@@ -135,6 +138,8 @@ class Device {
     void synchronize() const;
     Buffer zeros_buffer(int64_t len) const;
     Buffer filled(int64_t len, float value) const;
+    // A read-only [1] buffer holding 1.0, filled once per device.
+    Buffer seed_one() const;
     Plan plan(const std::vector<int32_t> &offsets, const std::vector<int32_t> &left,
               const std::vector<int32_t> &right, bool uncapped = false) const;
 
@@ -144,6 +149,8 @@ class Device {
     Buffer relu_backward(const Buffer &g, const Buffer &a) const;
     Buffer mask_gradient(const Buffer &g, const Buffer &winners) const;
     Buffer matmul(const Buffer &a, const Buffer &b, int64_t batch, int64_t m, int64_t k, int64_t n) const;
+    Buffer matmul_bias(const Buffer &a, const Buffer &b, const Buffer &bias, int64_t batch, int64_t m, int64_t k,
+                       int64_t n) const;
     Buffer matmul_left_backward(const Buffer &g, const Buffer &rhs, int64_t batch, int64_t m,
                                 int64_t k, int64_t n) const;
     // beta * d + alpha * (a . b), each product and the sum rounded once (Newton-Schulz steps)
@@ -268,6 +275,9 @@ class Tensor {
     Tensor scale(float factor) const;
     Tensor relu() const;
     Tensor contract(const Tensor &rhs, const std::vector<Axis> &axes) const;
+    // contract(rhs, axes).add(bias) for a bias over exactly the rhs's kept axes: one product with
+    // the bias added in its epilogue (same values; falls back to the two operations otherwise).
+    Tensor contract_add(const Tensor &rhs, const std::vector<Axis> &axes, const Tensor &bias) const;
     Tensor rename(const Axis &from, const Axis &to) const;
     Tensor merge(const std::vector<Axis> &axes, const Axis &axis) const;
     Tensor with_layout(const std::vector<Axis> &order) const;

@@ -136,11 +136,14 @@ int64_t Layout::offset(const std::vector<int64_t> &coords) const {
 // ------------------------------------------------------------------ device
 
 DeviceImpl::~DeviceImpl() {
-    if (handle) axis_device_destroy(handle);
+    if (handle) {
+        if (one) axis_free(handle, one);
+        axis_device_destroy(handle);
+    }
 }
 
 BufferImpl::~BufferImpl() {
-    if (ptr && device && device->handle) axis_free(device->handle, ptr);
+    if (owned && ptr && device && device->handle) axis_free(device->handle, ptr);
 }
 
 PlanImpl::~PlanImpl() {
@@ -206,6 +209,24 @@ Buffer Device::filled(int64_t len, float value) const {
     return b;
 }
 
+Buffer Device::seed_one() const {
+    if (!impl->one) {
+        void *p = nullptr;
+        check(axis_alloc(h(), 4, &p), "allocate");
+        if (int st = axis_fill(h(), static_cast<float *>(p), 1.0f, 1)) {
+            axis_free(h(), p);
+            check(st, "fill");
+        }
+        impl->one = p;
+    }
+    auto b = std::make_shared<BufferImpl>();
+    b->device = impl;
+    b->ptr = impl->one;
+    b->bytes = 4;
+    b->owned = false;
+    return b;
+}
+
 Plan Device::plan(const std::vector<int32_t> &offsets, const std::vector<int32_t> &left,
                   const std::vector<int32_t> &right, bool uncapped) const {
     auto p = std::make_shared<PlanImpl>();
@@ -251,6 +272,13 @@ Buffer Device::matmul(const Buffer &a, const Buffer &b, int64_t batch, int64_t m
                       int64_t n) const {
     Buffer out = alloc(batch * m * n);
     check(axis_matmul(h(), a->f32(), b->f32(), out->f32(), batch, m, k, n), "matmul");
+    return out;
+}
+
+Buffer Device::matmul_bias(const Buffer &a, const Buffer &b, const Buffer &bias, int64_t batch, int64_t m,
+                           int64_t k, int64_t n) const {
+    Buffer out = alloc(batch * m * n);
+    check(axis_matmul_bias(h(), a->f32(), b->f32(), bias->f32(), out->f32(), batch, m, k, n), "matmul_bias");
     return out;
 }
 

@@ -98,8 +98,9 @@ Tensor Linear::forward(const Tensor &x) {
     if (!bound) raise("Linear must be built before forward");
     auto &[extent, weight, b] = *bound;
     (void)extent;
-    Tensor projected = x.rename(input, input_role).contract(weight.tensor(), {input_role});
-    if (b) projected = projected.add(b->tensor());
+    const Tensor renamed = x.rename(input, input_role);
+    Tensor projected = b ? renamed.contract_add(weight.tensor(), {input_role}, b->tensor())
+                         : renamed.contract(weight.tensor(), {input_role});
     return projected.rename(output_role, output.axis);
 }
 

@@ -413,92 +413,141 @@ Tensor Tensor::merge(const std::vector<Axis> &axes_in, const Axis &axis) const {
 
 // ------------------------------------------------------------------ contraction (tensor.rs:4051-4172)
 
-Tensor Tensor::contract(const Tensor &rhs, const std::vector<Axis> &axes_in) const {
-    require_same_device(*this, rhs);
-    shared_extents(*this, rhs);
-    auto axes = select_axes(shape(), axes_in);
-    select_axes(rhs.shape(), axes);
-    if (axes.empty()) raise("outer products (contraction over no axes) are not part of this backend");
-    int64_t k = 1;
-    for (auto &a : axes) k *= extent(a);
+namespace {
+
+// The batched-matmul reading of a contraction (tensor.rs contract): shared axes kept by both sides
+// are batch axes, then the lhs's kept axes (m), the contracted axes (k) and the rhs's kept axes (n).
+struct ContractPlan {
+    std::vector<Axis> axes, batch_axes, left_axes, right_axes, left_order, right_order, output_order;
+    Shape out_shape;
+    int64_t batch = 1, m = 1, k = 1, n = 1;
+};
+
+ContractPlan plan_contract(const Tensor &lhs, const Tensor &rhs, const std::vector<Axis> &axes_in) {
+    ContractPlan c;
+    c.axes = select_axes(lhs.shape(), axes_in);
+    select_axes(rhs.shape(), c.axes);
+    if (c.axes.empty()) raise("outer products (contraction over no axes) are not part of this backend");
+    for (auto &a : c.axes) c.k *= lhs.extent(a);
     std::vector<Dim> dims;
-    for (auto &d : shape().dims)
-        if (!contains(axes, d.axis)) dims.push_back(d);
+    for (auto &d : lhs.shape().dims)
+        if (!contains(c.axes, d.axis)) dims.push_back(d);
     for (auto &d : rhs.shape().dims) {
-        bool present = contains(axes, d.axis);
+        bool present = contains(c.axes, d.axis);
         for (auto &e : dims) present = present || e.axis == d.axis;
         if (!present) dims.push_back(d);
     }
-    Shape out_shape = Shape::make(dims);
-    std::vector<Axis> batch_axes, left_axes, right_axes;
-    for (auto &a : shape().axes()) {
-        if (contains(axes, a)) continue;
+    c.out_shape = Shape::make(dims);
+    for (auto &a : lhs.shape().axes()) {
+        if (contains(c.axes, a)) continue;
         if (rhs.shape().contains(a))
-            batch_axes.push_back(a);
+            c.batch_axes.push_back(a);
         else
-            left_axes.push_back(a);
+            c.left_axes.push_back(a);
     }
     for (auto &a : rhs.shape().axes())
-        if (!contains(axes, a) && !shape().contains(a)) right_axes.push_back(a);
-    std::vector<Axis> left_order = batch_axes, right_order = batch_axes;
-    left_order.insert(left_order.end(), left_axes.begin(), left_axes.end());
-    left_order.insert(left_order.end(), axes.begin(), axes.end());
-    right_order.insert(right_order.end(), axes.begin(), axes.end());
-    right_order.insert(right_order.end(), right_axes.begin(), right_axes.end());
-    auto ordered = [](const Tensor &t, const std::vector<Axis> &order) {
-        Layout l = Layout::make(t.shape(), order);
-        return t.layout() == l ? t : t.with_layout(order);
-    };
-    auto laid_out = [](const Tensor &t, const std::vector<Axis> &order) {
-        return t.layout() == Layout::make(t.shape(), order);
-    };
-    int64_t batch = 1, m = 1, n = 1;
-    for (auto &a : batch_axes) batch *= extent(a);
-    for (auto &a : left_axes) m *= extent(a);
-    for (auto &a : right_axes) n *= rhs.extent(a);
-    std::vector<Axis> output_order = batch_axes;
-    output_order.insert(output_order.end(), left_axes.begin(), left_axes.end());
-    output_order.insert(output_order.end(), right_axes.begin(), right_axes.end());
+        if (!contains(c.axes, a) && !lhs.shape().contains(a)) c.right_axes.push_back(a);
+    c.left_order = c.batch_axes;
+    c.right_order = c.batch_axes;
+    c.left_order.insert(c.left_order.end(), c.left_axes.begin(), c.left_axes.end());
+    c.left_order.insert(c.left_order.end(), c.axes.begin(), c.axes.end());
+    c.right_order.insert(c.right_order.end(), c.axes.begin(), c.axes.end());
+    c.right_order.insert(c.right_order.end(), c.right_axes.begin(), c.right_axes.end());
+    for (auto &a : c.batch_axes) c.batch *= lhs.extent(a);
+    for (auto &a : c.left_axes) c.m *= lhs.extent(a);
+    for (auto &a : c.right_axes) c.n *= rhs.extent(a);
+    c.output_order = c.batch_axes;
+    c.output_order.insert(c.output_order.end(), c.left_axes.begin(), c.left_axes.end());
+    c.output_order.insert(c.output_order.end(), c.right_axes.begin(), c.right_axes.end());
+    return c;
+}
+
+Tensor laid_out_as(const Tensor &t, const std::vector<Axis> &order) {
+    Layout l = Layout::make(t.shape(), order);
+    return t.layout() == l ? t : t.with_layout(order);
+}
+
+bool is_laid_out(const Tensor &t, const std::vector<Axis> &order) {
+    return t.layout() == Layout::make(t.shape(), order);
+}
+
+// The product's gradient edges: rules save the other operand in its [batch, m, k] / [batch, k, n]
+// layout.
+void matmul_edges(const ContractPlan &c, const Tensor &left, const Tensor &right, std::vector<Edge> &edges) {
+    if (left.requires_grad()) {
+        Rule r = rule(Rule::MatmulLeft);
+        r.a = right.value();
+        r.batch = c.batch, r.m = c.m, r.k = c.k, r.n = c.n;
+        edges.push_back(Edge{left, r});
+    }
+    if (right.requires_grad()) {
+        Rule r = rule(Rule::MatmulRight);
+        r.a = left.value();
+        r.batch = c.batch, r.m = c.m, r.k = c.k, r.n = c.n;
+        edges.push_back(Edge{right, r});
+    }
+}
+
+}  // namespace
+
+Tensor Tensor::contract(const Tensor &rhs, const std::vector<Axis> &axes_in) const {
+    require_same_device(*this, rhs);
+    shared_extents(*this, rhs);
+    const ContractPlan c = plan_contract(*this, rhs, axes_in);
     // An untracked product (no gradient rules to save) reads a transposed operand in place: a
     // contraction-major lhs through the TN kernel, a contraction-minor rhs through the NT kernel
     // (matmul_right_backward / matmul_left_backward compute exactly those products, in the same
     // reduction order).  Tracked products keep the reference's [batch, m, k] x [batch, k, n] operands
     // because their saved rules assume that layout.
     if (!requires_grad() && !rhs.requires_grad()) {
-        std::vector<Axis> left_t = batch_axes, right_t = batch_axes;
-        left_t.insert(left_t.end(), axes.begin(), axes.end());
-        left_t.insert(left_t.end(), left_axes.begin(), left_axes.end());
-        right_t.insert(right_t.end(), right_axes.begin(), right_axes.end());
-        right_t.insert(right_t.end(), axes.begin(), axes.end());
-        const bool lhs_plain = laid_out(*this, left_order), rhs_plain = laid_out(rhs, right_order);
+        std::vector<Axis> left_t = c.batch_axes, right_t = c.batch_axes;
+        left_t.insert(left_t.end(), c.axes.begin(), c.axes.end());
+        left_t.insert(left_t.end(), c.left_axes.begin(), c.left_axes.end());
+        right_t.insert(right_t.end(), c.right_axes.begin(), c.right_axes.end());
+        right_t.insert(right_t.end(), c.axes.begin(), c.axes.end());
+        const bool lhs_plain = is_laid_out(*this, c.left_order), rhs_plain = is_laid_out(rhs, c.right_order);
         Buffer value;
-        if (!lhs_plain && laid_out(*this, left_t)) {
-            Tensor right = ordered(rhs, right_order);
-            value = device().matmul_right_backward(this->value(), right.value(), batch, k, m, n);
-        } else if (!rhs_plain && laid_out(rhs, right_t)) {
-            Tensor left = ordered(*this, left_order);
-            value = device().matmul_left_backward(left.value(), rhs.value(), batch, m, n, k);
+        if (!lhs_plain && is_laid_out(*this, left_t)) {
+            Tensor right = laid_out_as(rhs, c.right_order);
+            value = device().matmul_right_backward(this->value(), right.value(), c.batch, c.k, c.m, c.n);
+        } else if (!rhs_plain && is_laid_out(rhs, right_t)) {
+            Tensor left = laid_out_as(*this, c.left_order);
+            value = device().matmul_left_backward(left.value(), rhs.value(), c.batch, c.m, c.n, c.k);
         }
         if (value)
-            return node(out_shape, Layout::make(out_shape, output_order), value, device(), {}, false);
+            return node(c.out_shape, Layout::make(c.out_shape, c.output_order), value, device(), {}, false);
     }
-    Tensor left = ordered(*this, left_order), right = ordered(rhs, right_order);
-    Buffer value = device().matmul(left.value(), right.value(), batch, m, k, n);
+    Tensor left = laid_out_as(*this, c.left_order), right = laid_out_as(rhs, c.right_order);
+    Buffer value = device().matmul(left.value(), right.value(), c.batch, c.m, c.k, c.n);
     std::vector<Edge> edges;
-    if (left.requires_grad()) {
-        Rule r = rule(Rule::MatmulLeft);
-        r.a = right.value();
-        r.batch = batch, r.m = m, r.k = k, r.n = n;
-        edges.push_back(Edge{left, r});
-    }
-    if (right.requires_grad()) {
-        Rule r = rule(Rule::MatmulRight);
-        r.a = left.value();
-        r.batch = batch, r.m = m, r.k = k, r.n = n;
-        edges.push_back(Edge{right, r});
-    }
-    return node(out_shape, Layout::make(out_shape, output_order), value, device(), std::move(edges),
+    matmul_edges(c, left, right, edges);
+    return node(c.out_shape, Layout::make(c.out_shape, c.output_order), value, device(), std::move(edges),
                 false);
+}
+
+Tensor Tensor::contract_add(const Tensor &rhs, const std::vector<Axis> &axes_in, const Tensor &bias) const {
+    require_same_device(*this, rhs);
+    require_same_device(*this, bias);
+    shared_extents(*this, rhs);
+    const ContractPlan c = plan_contract(*this, rhs, axes_in);
+    // The fused form is the separate add's own fused case: a contiguous product (its output order
+    // is its shape's order) plus a contiguous bias over exactly its trailing (rhs-kept) axes.
+    const bool fusable = (requires_grad() || rhs.requires_grad()) && bias.is_contiguous() &&
+                         bias.shape().axes() == c.right_axes &&
+                         Layout::make(c.out_shape, c.output_order) == Layout::contiguous(c.out_shape);
+    if (!fusable) return contract(rhs, axes_in).add(bias);
+    shared_extents(bias, rhs);
+    Tensor left = laid_out_as(*this, c.left_order), right = laid_out_as(rhs, c.right_order);
+    Buffer value = device().matmul_bias(left.value(), right.value(), bias.value(), c.batch, c.m, c.k, c.n);
+    std::vector<Edge> edges;
+    matmul_edges(c, left, right, edges);
+    if (bias.requires_grad()) {
+        Rule rb = rule(Rule::BiasBroadcast);
+        rb.outer = c.batch * c.m;
+        rb.inner = c.n;
+        edges.push_back(Edge{bias, rb});
+    }
+    return node(c.out_shape, Layout::contiguous(c.out_shape), value, device(), std::move(edges), false);
 }
 
 // ------------------------------------------------------------------ reductions (tensor.rs:2755-2946)
@@ -913,7 +962,12 @@ void Tensor::backward() const {
     // Weight gradients produced together with a ReLU/pool backward, keyed by the convolution's
     // pre-activation node: that node then carries no adjoint buffer.
     std::unordered_map<uint64_t, Buffer> fused_weight;
-    adjoints[id()] = dev.filled(1, 1.0f);
+    // The seed is the device's shared 1.0 when every rule of the root reads it into a fresh buffer;
+    // an Identity edge would hand the buffer itself on (possibly to a leaf's stored gradient).
+    bool seed_shared = static_cast<bool>(n->edges);
+    if (n->edges)
+        for (auto &e : *n->edges) seed_shared = seed_shared && e.rule.kind != Rule::Identity;
+    adjoints[id()] = seed_shared ? dev.seed_one() : dev.filled(1, 1.0f);
     std::vector<std::pair<Tensor, Buffer>> leaves;
     for (auto it = order.rbegin(); it != order.rend(); ++it) {
         const Tensor &nd = *it;

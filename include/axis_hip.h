@@ -91,6 +91,12 @@ int axis_timing_read(axis_device device, const char *family, int64_t *launches, 
  * out [batch,m,n], all row-major.  fp32 on MFMA. */
 int axis_matmul(axis_device device, const float *a, const float *b, float *out, int64_t batch,
                 int64_t m, int64_t k, int64_t n);
+/* Linear::forward with a bias (model/nn.rs:268-280): Device::matmul (backend.rs:934-957), then the
+ * bias add of the projected output (tensor.rs:779-818 broadcasting `bias` [n] along the rows):
+ * out[b][i][j] = (a[b] . b[b])[i][j] + bias[j], the product rounded once and the add once, as the
+ * two operations round them.  bias must not alias out. */
+int axis_matmul_bias(axis_device device, const float *a, const float *b, const float *bias, float *out,
+                     int64_t batch, int64_t m, int64_t k, int64_t n);
 /* out[b] = beta * d[b] + alpha * (a[b] . b[b]) for row-major [m,k] x [k,n] (d and out [m,n], d not
  * aliasing out): the Newton-Schulz steps of Muon::zeroth_power (optim.rs:728-752),
  * `gram.scale(b).add(gram2.scale(c))` and `x.scale(a).add(b.x)`, with the product's scale, the

@@ -55,6 +55,28 @@ def test_matmul_family(dev, oracle, batch, m, k, n):
     assert rel_err(dev.read(out, batch * k * n), oracle.matmul_right_backward(a, g, batch, m, k, n)) < 1e-5
 
 
+@pytest.mark.parametrize("batch,m,k,n", [(1, 256, 256, 1000), (1, 256, 1000, 256), (2, 33, 27, 64),
+                                         (1, 130, 129, 131), (1, 4096, 512, 64), (1, 7, 3000, 5)])
+def test_matmul_bias_equals_product_then_bias_add(dev, dev_bf16, batch, m, k, n):
+    # Linear's product + bias in one launch: bit-identical to axis_matmul then axis_bias_add, on
+    # unsplit, split-K (classifier shapes) and batched products, fp32 and bf16 handles
+    rng = np.random.default_rng(batch * 7 + m + k + n)
+    a = rng.standard_normal(batch * m * k).astype(np.float32)
+    b = rng.standard_normal(batch * k * n).astype(np.float32)
+    bias = rng.standard_normal(n).astype(np.float32)
+    for d in (dev, dev_bf16):
+        da, db, dbias = up(d, a), up(d, b), up(d, bias)
+        geo = (I64(batch), I64(m), I64(k), I64(n))
+        fused, prod, sep = d.empty(batch * m * n), d.empty(batch * m * n), d.empty(batch * m * n)
+        d.call("axis_matmul_bias", da.vp, db.vp, dbias.vp, fused.vp, *geo)
+        d.call("axis_matmul", da.vp, db.vp, prod.vp, *geo)
+        d.call("axis_bias_add", prod.vp, dbias.vp, sep.vp, None, I64(batch * m), I64(n))
+        got = d.read(fused, batch * m * n)
+        assert np.array_equal(got.view(np.uint32), d.read(sep, batch * m * n).view(np.uint32))
+    with pytest.raises(hip.AxisError, match="alias"):
+        d.call("axis_matmul_bias", da.vp, db.vp, fused.vp, fused.vp, *geo)
+
+
 def test_matmul_rejects_bad_extents(dev):
     buf = dev.empty(4)
     with pytest.raises(hip.AxisError, match="positive"):
