@@ -962,6 +962,9 @@ void Tensor::backward() const {
     // Weight gradients produced together with a ReLU/pool backward, keyed by the convolution's
     // pre-activation node: that node then carries no adjoint buffer.
     std::unordered_map<uint64_t, Buffer> fused_weight;
+    // Means whose backward broadcast is left to their input's only rule: the input node's adjoint is
+    // the mean's output gradient, and this factor (1 / reduced extent) goes with it.
+    std::unordered_map<uint64_t, float> lazy_mean;
     // The seed is the device's shared 1.0 when every rule of the root reads it into a fresh buffer;
     // an Identity edge would hand the buffer itself on (possibly to a leaf's stored gradient).
     bool seed_shared = static_cast<bool>(n->edges);
@@ -1013,12 +1016,20 @@ void Tensor::backward() const {
                     }
                     break;
                 }
-                case Rule::CategoricalCrossEntropy:
+                case Rule::CategoricalCrossEntropy: {
                     c = dev.alloc(r.m * r.n);
-                    check(axis_categorical_cross_entropy_backward(dev.h(), g->f32(), r.a->f32(),
-                                                                  r.b->f32(), c->f32(), r.m, r.n),
-                          "categorical_cross_entropy_backward");
+                    auto lazy = lazy_mean.find(nd.id());
+                    if (lazy != lazy_mean.end())
+                        check(axis_categorical_cross_entropy_backward_mean(dev.h(), g->f32(), lazy->second,
+                                                                           r.a->f32(), r.b->f32(), c->f32(), r.m,
+                                                                           r.n),
+                              "categorical_cross_entropy_backward");
+                    else
+                        check(axis_categorical_cross_entropy_backward(dev.h(), g->f32(), r.a->f32(),
+                                                                      r.b->f32(), c->f32(), r.m, r.n),
+                              "categorical_cross_entropy_backward");
                     break;
+                }
                 case Rule::MatmulLeft: c = dev.matmul_left_backward(g, r.a, r.batch, r.m, r.k, r.n); break;
                 case Rule::MatmulRight: c = dev.matmul_right_backward(r.a, g, r.batch, r.m, r.k, r.n); break;
                 case Rule::Group: c = dev.grouped(g, r.b ? &r.b : nullptr, r.plan, r.factor); break;
@@ -1072,12 +1083,32 @@ void Tensor::backward() const {
                           "min_backward");
                     break;
                 }
-                case Rule::MeanMiddle:
+                case Rule::MeanMiddle: {
+                    // A mean read by exactly one rule that can take the broadcast itself (the
+                    // cross-entropy of a mean over rows, the ReLU/pool backward of a mean over the
+                    // pooled height and width): hand that rule the mean's gradient and factor.
+                    const std::shared_ptr<Node> &x = e.input.n;
+                    bool lazy = false;
+                    if (uses[x->id] == 1 && x->edges && x->edges->size() == 1) {
+                        const Rule &xr = (*x->edges)[0].rule;
+                        if (xr.kind == Rule::CategoricalCrossEntropy)
+                            lazy = r.outer == 1 && r.inner == 1 && r.reduce == xr.m;
+                        else if (xr.kind == Rule::ReluPool)
+                            lazy = r.outer == xr.pool.outer && r.inner == xr.pool.channels &&
+                                   r.reduce == (int64_t)(xr.pool.height / xr.pool.kernel[0]) *
+                                                   (xr.pool.width / xr.pool.kernel[1]);
+                    }
+                    if (lazy && g->floats() == r.outer * r.inner) {
+                        c = g;
+                        lazy_mean[x->id] = r.factor;
+                        break;
+                    }
                     c = dev.alloc(r.outer * r.reduce * r.inner);
                     check(axis_broadcast_middle(dev.h(), g->f32(), c->f32(), r.outer, r.reduce, r.inner,
                                                 r.factor),
                           "broadcast_middle");
                     break;
+                }
                 case Rule::ConvData: {
                     const ConvGeometry &q = r.conv;
                     c = dev.alloc(q.batch * q.height * q.width * q.channels);
@@ -1106,6 +1137,9 @@ void Tensor::backward() const {
                     // The pre-activation node's bias gradient comes out of the same pass when that
                     // node has exactly one BiasBroadcast edge and no other reader.
                     const PoolGeometry &p = r.pool;
+                    const int64_t pooled_len = p.outer * (p.height / p.kernel[0]) * (p.width / p.kernel[1]) * p.channels;
+                    auto lazy = lazy_mean.find(nd.id());
+                    const float mean_factor = lazy != lazy_mean.end() ? lazy->second : 0.0f;
                     const std::shared_ptr<Node> &x = e.input.n;
                     const Rule *bias_rule = nullptr;
                     const Rule *weight_rule = nullptr;
@@ -1129,6 +1163,13 @@ void Tensor::backward() const {
                         // needs none): both straight from the pooled gradient, without the
                         // pre-activation gradient.
                         const ConvGeometry &q = weight_rule->conv;
+                        if (mean_factor != 0.0f) {  // this path reads one gradient per pooled value
+                            Buffer full = dev.alloc(pooled_len);
+                            check(axis_broadcast_middle(dev.h(), g->f32(), full->f32(), p.outer,
+                                                        pooled_len / (p.outer * p.channels), p.channels, mean_factor),
+                                  "broadcast_middle");
+                            g = full;
+                        }
                         Buffer dw = dev.alloc((int64_t)q.channels * q.kernel[0] * q.kernel[1] * q.out_channels);
                         Buffer db = bias_rule ? dev.alloc(p.channels) : Buffer();
                         check(axis_conv2d_relu_pool_backward_weight(
@@ -1144,11 +1185,18 @@ void Tensor::backward() const {
                     c = dev.alloc(p.outer * p.height * p.width * p.channels);
                     Buffer db;
                     if (bias_rule) db = dev.alloc(p.channels);
-                    check(axis_relu_pool_backward(dev.h(), g->f32(), r.b->f32(),
-                                                  static_cast<const uint8_t *>(r.a->ptr), c->f32(),
-                                                  db ? db->f32() : nullptr, p.outer, p.height, p.width,
-                                                  (int32_t)p.channels, p.kernel),
-                          "relu_pool_backward");
+                    if (mean_factor != 0.0f)
+                        check(axis_relu_pool_backward_mean(dev.h(), g->f32(), mean_factor, r.b->f32(),
+                                                           static_cast<const uint8_t *>(r.a->ptr), c->f32(),
+                                                           db ? db->f32() : nullptr, p.outer, p.height, p.width,
+                                                           (int32_t)p.channels, p.kernel),
+                              "relu_pool_backward");
+                    else
+                        check(axis_relu_pool_backward(dev.h(), g->f32(), r.b->f32(),
+                                                      static_cast<const uint8_t *>(r.a->ptr), c->f32(),
+                                                      db ? db->f32() : nullptr, p.outer, p.height, p.width,
+                                                      (int32_t)p.channels, p.kernel),
+                              "relu_pool_backward");
                     if (db) fused_bias[x->id] = db;
                     break;
                 }

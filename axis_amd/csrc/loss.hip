@@ -5,6 +5,8 @@
 // fp32 tolerance; the CE gradient is exact given the probabilities.
 #include <cfloat>
 
+#include <cmath>
+
 #include "common.hpp"
 
 namespace {
@@ -79,15 +81,18 @@ __global__ void __launch_bounds__(kBlock) softmax_backward_kernel(const float *_
         out[base + j] = probability[base + j] * (gradient[base + j] - d);
 }
 
+// mean_factor != 0: the row gradient is gradient[0] * mean_factor for every row -- the value the
+// backward of a mean over the rows (a broadcast times the factor) would have stored.
 __global__ void __launch_bounds__(kBlock) ce_backward_kernel(const float *__restrict__ gradient,
                                                              const float *__restrict__ probability,
                                                              const float *__restrict__ targets,
                                                              float *__restrict__ out, int64_t rows,
-                                                             int64_t width) {
+                                                             int64_t width, float mean_factor) {
     const int64_t total = rows * width;
+    const float g_all = mean_factor != 0.0f ? gradient[0] * mean_factor : 0.0f;
     for (int64_t p = (int64_t)blockIdx.x * kBlock + threadIdx.x; p < total;
          p += (int64_t)gridDim.x * kBlock)
-        out[p] = gradient[p / width] * (probability[p] - targets[p]);
+        out[p] = (mean_factor != 0.0f ? g_all : gradient[p / width]) * (probability[p] - targets[p]);
 }
 
 int check_rows(const void *a, const void *out, int64_t rows, int64_t width) {
@@ -135,7 +140,19 @@ int axis_categorical_cross_entropy_backward(axis_device device, const float *gra
     if (int s = check_rows(gradient, out, rows, width)) return s;
     AXIS_REQUIRE(probability && targets, "null probability/targets");
     ce_backward_kernel<<<axis::blocks_for(rows * width, kBlock, 16384), kBlock, 0, device->stream>>>(
-        gradient, probability, targets, out, rows, width);
+        gradient, probability, targets, out, rows, width, 0.0f);
+    return axis::launch_status("ce_backward_kernel");
+}
+
+int axis_categorical_cross_entropy_backward_mean(axis_device device, const float *gradient, float factor,
+                                                 const float *probability, const float *targets, float *out,
+                                                 int64_t rows, int64_t width) {
+    AXIS_ENTER(device);
+    if (int s = check_rows(gradient, out, rows, width)) return s;
+    AXIS_REQUIRE(probability && targets, "null probability/targets");
+    AXIS_REQUIRE(factor != 0.0f && std::isfinite(factor), "mean factor must be finite and nonzero");
+    ce_backward_kernel<<<axis::blocks_for(rows * width, kBlock, 16384), kBlock, 0, device->stream>>>(
+        gradient, probability, targets, out, rows, width, factor);
     return axis::launch_status("ce_backward_kernel");
 }
 

@@ -28,6 +28,10 @@ struct PoolArgs {
     FastDiv cvec, ow, oh;    // decode of an output-vector index
     FastDiv iw, ih;          // decode of an input-vector index
     FastDiv sy_div, sx_div;
+    // Pooled gradient given as [outer, channels] times g_factor, the same at every pooled position
+    // (the backward of a mean over the pooled height and width); otherwise one value per position.
+    bool g_broadcast;
+    float g_factor;
 };
 
 template <int VEC>
@@ -42,6 +46,20 @@ __device__ __forceinline__ void load_vec(const float *p, float (&v)[VEC]) {
         v[0] = x[0], v[1] = x[1], v[2] = x[2], v[3] = x[3];
     } else {
         v[0] = p[0];
+    }
+}
+
+// The pooled gradient of output vector t (batch o, channel c): gradient[t], or, broadcast,
+// gradient[o][c] * g_factor -- the value the mean's backward (a broadcast times the factor) stores.
+template <int VEC>
+__device__ __forceinline__ void load_gradient(const float *gradient, uint32_t t, uint32_t o, int32_t c,
+                                              const PoolArgs &a, float (&g)[VEC]) {
+    if (a.g_broadcast) {
+        load_vec<VEC>(gradient + (int64_t)o * a.channels + c, g);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) g[e] = g[e] * a.g_factor;
+    } else {
+        load_vec<VEC>(gradient + (int64_t)t * VEC, g);
     }
 }
 
@@ -150,7 +168,7 @@ __global__ void __launch_bounds__(256) relu_pool_backward_kernel(
     const int32_t c = (int32_t)cv * VEC;
     float g[VEC], y[VEC];
     int w[VEC];
-    load_vec<VEC>(gradient + (int64_t)t * VEC, g);
+    load_gradient<VEC>(gradient, t, o, c, a, g);
     load_vec<VEC>(pooled + (int64_t)t * VEC, y);
 #pragma unroll
     for (int e = 0; e < VEC; ++e) w[e] = y[e] > 0.0f ? (int)argmax[(int64_t)t * VEC + e] : -1;
@@ -195,7 +213,7 @@ __global__ void __launch_bounds__(256) relu_pool_backward_bias_kernel(
         const int32_t c = (int32_t)cv * VEC;
         float g[VEC], y[VEC];
         int w[VEC];
-        load_vec<VEC>(gradient + (int64_t)t * VEC, g);
+        load_gradient<VEC>(gradient, t, o, c, a, g);
         load_vec<VEC>(pooled + (int64_t)t * VEC, y);
 #pragma unroll
         for (int e = 0; e < VEC; ++e) {
@@ -258,13 +276,13 @@ __global__ void __launch_bounds__(256) relu_pool_bias_chunk_kernel(
         const int k = ky * a.kx + kx;
         const uint8_t win = argmax[w];
         const float v = pooled[w];
-        const float g = gradient[w];
+        const float g = a.g_broadcast ? gradient[o * a.channels + c] * a.g_factor : gradient[w];
         sum = sum + ((win == k && v > 0.0f) ? 0.0f + g : 0.0f);
         if (++kx == a.kx) kx = 0, ++px;
         if (++x == a.width) {
             x = 0, px = 0, kx = 0;
             if (++ky == a.ky) ky = 0, wbase += (int64_t)a.out_w * a.channels;
-            if (++y == a.height) y = 0;
+            if (++y == a.height) y = 0, ++o;  // o: the row's image, for a broadcast gradient
         }
     }
     partial[q * a.channels + c] = sum;
@@ -345,6 +363,10 @@ int pool_args(int64_t outer, int32_t height, int32_t width, int64_t channels, co
     return AXIS_OK;
 }
 
+int relu_pool_backward(axis_device device, const float *gradient, bool broadcast, float factor, const float *pooled,
+                       const uint8_t *argmax, float *d_pre, float *d_bias, int64_t outer, int32_t height,
+                       int32_t width, int32_t channels, const int32_t pool[2]);
+
 }  // namespace
 
 extern "C" {
@@ -408,14 +430,36 @@ int axis_relu_pool_backward(axis_device device, const float *gradient, const flo
                             const uint8_t *argmax, float *d_pre, float *d_bias, int64_t outer,
                             int32_t height, int32_t width, int32_t channels, const int32_t pool[2]) {
     AXIS_ENTER(device);
+    return relu_pool_backward(device, gradient, false, 1.0f, pooled, argmax, d_pre, d_bias, outer, height, width,
+                              channels, pool);
+}
+
+int axis_relu_pool_backward_mean(axis_device device, const float *gradient, float factor, const float *pooled,
+                                 const uint8_t *argmax, float *d_pre, float *d_bias, int64_t outer,
+                                 int32_t height, int32_t width, int32_t channels, const int32_t pool[2]) {
+    AXIS_ENTER(device);
+    return relu_pool_backward(device, gradient, true, factor, pooled, argmax, d_pre, d_bias, outer, height, width,
+                              channels, pool);
+}
+
+}  // extern "C"
+
+namespace {
+
+int relu_pool_backward(axis_device device, const float *gradient, bool broadcast, float factor, const float *pooled,
+                       const uint8_t *argmax, float *d_pre, float *d_bias, int64_t outer, int32_t height,
+                       int32_t width, int32_t channels, const int32_t pool[2]) {
     AXIS_REQUIRE(gradient && pooled && argmax && d_pre && pool, "null relu_pool_backward buffer");
     const int32_t zero[2] = {0, 0};
     PoolArgs a{};
     if (int s = pool_args(outer, height, width, channels, pool, pool, zero, &a)) return s;
+    a.g_broadcast = broadcast;
+    a.g_factor = factor;
     AXIS_REQUIRE(height % pool[0] == 0 && width % pool[1] == 0,
                  "relu_pool_backward needs windows that tile the input exactly");
     const bool vec = channels % 4 == 0 && axis::aligned16(gradient) && axis::aligned16(pooled) &&
                      axis::aligned16(d_pre) && (reinterpret_cast<uintptr_t>(argmax) & 3u) == 0;
+    // the broadcast gradient's rows are [channels]: vector loads need no more alignment than that
     const int v = vec ? 4 : 1;
     a.cvec = FastDiv((uint32_t)(channels / v));
     a.total = (uint32_t)(outer * a.out_h * a.out_w * (channels / v));
@@ -457,4 +501,4 @@ int axis_relu_pool_backward(axis_device device, const float *gradient, const flo
     return axis::launch_status("column_combine_kernel");
 }
 
-}  // extern "C"
+}  // namespace

@@ -217,6 +217,13 @@ int axis_categorical_cross_entropy(axis_device device, const float *logits, cons
 int axis_categorical_cross_entropy_backward(axis_device device, const float *gradient,
                                             const float *probability, const float *targets,
                                             float *out, int64_t rows, int64_t width);
+/* The same backward for a loss that is the mean of the rows' losses (`.mean([rows])`,
+ * tensor.rs:2837-2845, a grouped sum times 1/rows): its backward broadcasts the scalar gradient times factor (1/rows) to every
+ * row (axis_broadcast_middle), which this entry folds in: out[pos] = (gradient[0] * factor) *
+ * (probability[pos] - targets[pos]), the values of the two launches it replaces. */
+int axis_categorical_cross_entropy_backward_mean(axis_device device, const float *gradient, float factor,
+                                                 const float *probability, const float *targets, float *out,
+                                                 int64_t rows, int64_t width);
 
 /* ------------------------------------------------------------------ optimizer */
 
@@ -387,6 +394,13 @@ int axis_conv2d_relu_pool_backward_weight(axis_device device, const float *input
 int axis_relu_pool_backward(axis_device device, const float *gradient, const float *pooled,
                             const uint8_t *argmax, float *d_pre, float *d_bias, int64_t outer,
                             int32_t height, int32_t width, int32_t channels, const int32_t pool[2]);
+/* The same backward when the pooled tensor's only reader is a mean over its pooled height and width
+ * (tensor.rs:2837-2845): gradient is that mean's output gradient [outer, channels], and every
+ * pooled position's gradient is gradient[o][c] * factor (factor = 1 / pooled positions) -- the
+ * values the mean's backward (axis_broadcast_middle) would store, without storing them. */
+int axis_relu_pool_backward_mean(axis_device device, const float *gradient, float factor, const float *pooled,
+                                 const uint8_t *argmax, float *d_pre, float *d_bias, int64_t outer,
+                                 int32_t height, int32_t width, int32_t channels, const int32_t pool[2]);
 /* Softmax + categorical cross-entropy of [rows, width] logits in one pass (tensor.rs:1540-1543):
  * writes probability [rows, width] and per-row loss [rows]; each equals the separate entries. */
 int axis_softmax_cross_entropy(axis_device device, const float *logits, const float *targets,

@@ -1076,6 +1076,53 @@ def test_relu_pool_backward_bit_exact(dev, oracle, b, h, w, c, pool):
     assert np.array_equal(dev.read(d_bias2, c).view(np.uint32), got_db.view(np.uint32))
 
 
+@pytest.mark.parametrize("b,h,w,c,pool", [(256, 16, 16, 256, (2, 2)), (3, 10, 12, 6, (2, 3)), (2, 8, 8, 20, (4, 4))])
+def test_relu_pool_backward_mean_equals_broadcast_then_backward(dev, b, h, w, c, pool):
+    # the backward of mean([h, w]) over the pooled tensor folded into the ReLU/pool backward: the
+    # same bits as axis_broadcast_middle then axis_relu_pool_backward (CNN conv3 shape first)
+    rng = np.random.default_rng(b + h + w + c)
+    z = (rng.integers(-3, 4, b * h * w * c).astype(np.float32) * 0.5)
+    y = np.maximum(z, 0).astype(np.float32)
+    ph, pw = pool
+    n_in, n_out = len(z), len(z) // (ph * pw)
+    positions = n_out // (b * c)
+    win = (I32 * 2)(ph, pw)
+    dy, pooled, arg = up(dev, y), dev.empty(n_out), dev.empty(n_out, np.uint8)
+    dev.call("axis_max_pool2d", dy.vp, pooled.vp, arg.vp, I64(b), I32(h), I32(w), I64(c), win, win, (I32 * 2)(0, 0))
+    g = rng.standard_normal(b * c).astype(np.float32)
+    g[::7] = -0.0
+    factor = np.float32(1.0) / np.float32(positions)
+    dg, full = up(dev, g), dev.empty(n_out)
+    dev.call("axis_broadcast_middle", dg.vp, full.vp, I64(b), I64(positions), I64(c), F32(factor))
+    ref, ref_db = dev.empty(n_in), dev.empty(c)
+    dev.call("axis_relu_pool_backward", full.vp, pooled.vp, arg.vp, ref.vp, ref_db.vp, I64(b), I32(h), I32(w),
+             I32(c), win)
+    got, got_db = dev.empty(n_in), dev.empty(c)
+    dev.call("axis_relu_pool_backward_mean", dg.vp, F32(factor), pooled.vp, arg.vp, got.vp, got_db.vp, I64(b),
+             I32(h), I32(w), I32(c), win)
+    assert np.array_equal(dev.read(got, n_in).view(np.uint32), dev.read(ref, n_in).view(np.uint32))
+    assert np.array_equal(dev.read(got_db, c).view(np.uint32), dev.read(ref_db, c).view(np.uint32))
+
+
+@pytest.mark.parametrize("rows,width", [(256, 1000), (3, 7)])
+def test_cross_entropy_backward_mean_equals_broadcast_then_backward(dev, rows, width):
+    rng = np.random.default_rng(rows + width)
+    logits = rng.standard_normal(rows * width).astype(np.float32)
+    targets = np.zeros(rows * width, np.float32)
+    targets[np.arange(rows) * width + rng.integers(0, width, rows)] = 1.0
+    dl, dt = up(dev, logits), up(dev, targets)
+    prob, loss = dev.empty(rows * width), dev.empty(rows)
+    dev.call("axis_softmax_cross_entropy", dl.vp, dt.vp, prob.vp, loss.vp, I64(rows), I64(width))
+    seed = up(dev, np.array([0.75], np.float32))
+    factor = np.float32(1.0) / np.float32(rows)
+    rows_g, ref, got = dev.empty(rows), dev.empty(rows * width), dev.empty(rows * width)
+    dev.call("axis_broadcast_middle", seed.vp, rows_g.vp, I64(1), I64(rows), I64(1), F32(factor))
+    dev.call("axis_categorical_cross_entropy_backward", rows_g.vp, prob.vp, dt.vp, ref.vp, I64(rows), I64(width))
+    dev.call("axis_categorical_cross_entropy_backward_mean", seed.vp, F32(factor), prob.vp, dt.vp, got.vp,
+             I64(rows), I64(width))
+    assert np.array_equal(dev.read(got, rows * width).view(np.uint32), dev.read(ref, rows * width).view(np.uint32))
+
+
 @pytest.mark.parametrize("batch,m,k,n", [(1, 256, 256, 256), (1, 64, 4096, 96), (2, 130, 70, 33), (1, 512, 512, 1024)])
 def test_matmul_axpby_equals_separate_operations(dev, oracle, batch, m, k, n):
     rng = np.random.default_rng(m + k + n)
