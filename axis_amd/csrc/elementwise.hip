@@ -400,7 +400,7 @@ struct BiasAdd {
 // load of the chunk in flight at once, coalesced in 64-byte row segments -- then one lane per
 // column adds its 512 (or fewer) rows in row order.  A lane summing straight from memory waits on
 // one round trip per batch of loads: 8.4 us for a [256, 1000] gradient against ~3 us staged.
-constexpr int kChunkCols = 16;
+constexpr int kChunkCols = 8;
 template <bool MASK>
 __global__ void __launch_bounds__(kBlock) column_chunk_kernel(const float *__restrict__ g,
                                                               const float *__restrict__ relu_input,

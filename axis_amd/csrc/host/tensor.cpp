@@ -1019,12 +1019,29 @@ void Tensor::backward() const {
                 case Rule::CategoricalCrossEntropy: {
                     c = dev.alloc(r.m * r.n);
                     auto lazy = lazy_mean.find(nd.id());
-                    if (lazy != lazy_mean.end())
+                    if (lazy != lazy_mean.end()) {
+                        // The logits' producer (through renames) read by nothing else, with one
+                        // BiasBroadcast edge over the classes: its bias gradient comes out of this pass.
+                        std::shared_ptr<Node> x = e.input.n;
+                        while (uses[x->id] == 1 && x->edges && x->edges->size() == 1 &&
+                               (*x->edges)[0].rule.kind == Rule::Identity &&
+                               (*x->edges)[0].input.n->value == x->value)
+                            x = (*x->edges)[0].input.n;
+                        const Rule *bias_rule = nullptr;
+                        if (uses[x->id] == 1 && x->edges) {
+                            int biases = 0;
+                            for (auto &xe : *x->edges)
+                                if (xe.rule.kind == Rule::BiasBroadcast) bias_rule = &xe.rule, ++biases;
+                            if (biases != 1) bias_rule = nullptr;
+                        }
+                        if (bias_rule && !(bias_rule->outer == r.m && bias_rule->inner == r.n)) bias_rule = nullptr;
+                        Buffer db = bias_rule ? dev.alloc(r.n) : Buffer();
                         check(axis_categorical_cross_entropy_backward_mean(dev.h(), g->f32(), lazy->second,
-                                                                           r.a->f32(), r.b->f32(), c->f32(), r.m,
-                                                                           r.n),
+                                                                           r.a->f32(), r.b->f32(), c->f32(),
+                                                                           db ? db->f32() : nullptr, r.m, r.n),
                               "categorical_cross_entropy_backward");
-                    else
+                        if (db) fused_bias[x->id] = db;
+                    } else
                         check(axis_categorical_cross_entropy_backward(dev.h(), g->f32(), r.a->f32(),
                                                                       r.b->f32(), c->f32(), r.m, r.n),
                               "categorical_cross_entropy_backward");

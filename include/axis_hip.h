@@ -218,12 +218,14 @@ int axis_categorical_cross_entropy_backward(axis_device device, const float *gra
                                             const float *probability, const float *targets,
                                             float *out, int64_t rows, int64_t width);
 /* The same backward for a loss that is the mean of the rows' losses (`.mean([rows])`,
- * tensor.rs:2837-2845, a grouped sum times 1/rows): its backward broadcasts the scalar gradient times factor (1/rows) to every
- * row (axis_broadcast_middle), which this entry folds in: out[pos] = (gradient[0] * factor) *
- * (probability[pos] - targets[pos]), the values of the two launches it replaces. */
+ * tensor.rs:2837-2845, a grouped sum times 1/rows): its backward broadcasts the scalar gradient
+ * times factor (1/rows) to every row (axis_broadcast_middle), which this entry folds in:
+ * out[pos] = (gradient[0] * factor) * (probability[pos] - targets[pos]), the values of the two
+ * launches it replaces.  d_bias (or NULL) also receives the column sums of out in
+ * axis_bias_gradient's order (the bias gradient of the layer that produced the logits). */
 int axis_categorical_cross_entropy_backward_mean(axis_device device, const float *gradient, float factor,
                                                  const float *probability, const float *targets, float *out,
-                                                 int64_t rows, int64_t width);
+                                                 float *d_bias, int64_t rows, int64_t width);
 
 /* ------------------------------------------------------------------ optimizer */
 

@@ -1104,7 +1104,7 @@ def test_relu_pool_backward_mean_equals_broadcast_then_backward(dev, b, h, w, c,
     assert np.array_equal(dev.read(got_db, c).view(np.uint32), dev.read(ref_db, c).view(np.uint32))
 
 
-@pytest.mark.parametrize("rows,width", [(256, 1000), (3, 7)])
+@pytest.mark.parametrize("rows,width", [(256, 1000), (3, 7), (1300, 37)])
 def test_cross_entropy_backward_mean_equals_broadcast_then_backward(dev, rows, width):
     rng = np.random.default_rng(rows + width)
     logits = rng.standard_normal(rows * width).astype(np.float32)
@@ -1118,9 +1118,16 @@ def test_cross_entropy_backward_mean_equals_broadcast_then_backward(dev, rows, w
     rows_g, ref, got = dev.empty(rows), dev.empty(rows * width), dev.empty(rows * width)
     dev.call("axis_broadcast_middle", seed.vp, rows_g.vp, I64(1), I64(rows), I64(1), F32(factor))
     dev.call("axis_categorical_cross_entropy_backward", rows_g.vp, prob.vp, dt.vp, ref.vp, I64(rows), I64(width))
-    dev.call("axis_categorical_cross_entropy_backward_mean", seed.vp, F32(factor), prob.vp, dt.vp, got.vp,
+    dev.call("axis_categorical_cross_entropy_backward_mean", seed.vp, F32(factor), prob.vp, dt.vp, got.vp, None,
              I64(rows), I64(width))
     assert np.array_equal(dev.read(got, rows * width).view(np.uint32), dev.read(ref, rows * width).view(np.uint32))
+    # with the logits' bias gradient: the same values, and the column sums of axis_bias_gradient
+    got2, db, ref_db = dev.empty(rows * width), dev.empty(width), dev.empty(width)
+    dev.call("axis_categorical_cross_entropy_backward_mean", seed.vp, F32(factor), prob.vp, dt.vp, got2.vp, db.vp,
+             I64(rows), I64(width))
+    dev.call("axis_bias_gradient", ref.vp, None, None, ref_db.vp, I64(rows), I64(width))
+    assert np.array_equal(dev.read(got2, rows * width).view(np.uint32), dev.read(ref, rows * width).view(np.uint32))
+    assert np.array_equal(dev.read(db, width).view(np.uint32), dev.read(ref_db, width).view(np.uint32))
 
 
 @pytest.mark.parametrize("batch,m,k,n", [(1, 256, 256, 256), (1, 64, 4096, 96), (2, 130, 70, 33), (1, 512, 512, 1024)])
