@@ -57,7 +57,7 @@ __global__ static void __launch_bounds__(1024) column_block_sum_kernel(const flo
     const int64_t r1 = r0 + span < rows ? r0 + span : rows;
     float s = 0.0f;
     if (e < width) {
-        constexpr int kBatch = 16;
+        constexpr int kBatch = 64;  // loads in flight per lane: the range takes few round trips
         int64_t r = r0;
         for (; r + kBatch <= r1; r += kBatch) {
             float v[kBatch];
