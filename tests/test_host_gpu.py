@@ -610,6 +610,39 @@ def test_conv_relu_pool_block_lowerings(ax, device, case):
         assert x.grad() is None
 
 
+@pytest.mark.parametrize("batch,fin,fout,relu", [(256, 256, 1000, False), (64, 300, 70, True), (5, 3000, 9, False)])
+def test_linear_bias_in_product_matches_contract_then_add(ax, device, batch, fin, fout, relu):
+    # Linear with a bias runs one product with the bias in its epilogue (or its split-K sum); the
+    # reference's lowering is contract then add.  Same values and the same three gradients, bit for
+    # bit, including when a ReLU reads the output (the bias gradient then comes from the masked pass)
+    bt, fi, fo = ax.Axis("batch"), ax.Axis("fin"), ax.Axis("fout")
+    rng = np.random.default_rng(batch + fin + fout)
+    xv = rng.standard_normal(batch * fin).astype(np.float32)
+    gv = rng.standard_normal(batch * fout).astype(np.float32)
+    layer = ax.Linear(fi, fo.of(fout))
+    layer.build(ax.Shape([bt.of(batch), fi.of(fin)]), device, 3)
+    w = np.asarray(layer.parameter("weight").tensor().to_vec(), np.float32)
+    bvals = rng.standard_normal(fout).astype(np.float32)
+    layer.parameter("bias").set_values(bvals)
+    x1 = ax.Tensor.from_slice(xv, [bt.of(batch), fi.of(fin)], device).with_grad()
+    x2 = ax.Tensor.from_slice(xv, [bt.of(batch), fi.of(fin)], device).with_grad()
+    wt = ax.Tensor.from_slice(w, layer.parameter("weight").tensor().shape.dims, device).with_grad()
+    wi, wo = [d.axis for d in layer.parameter("weight").tensor().shape.dims]
+    bb = ax.Tensor.from_slice(bvals, [wo.of(fout)], device).with_grad()
+    g = ax.Tensor.from_slice(gv, [bt.of(batch), fo.of(fout)], device)
+    fused = layer.forward(x1)
+    sep = x2.rename(fi, wi).contract(wt, [wi]).add(bb).rename(wo, fo)
+    if relu:
+        fused, sep = fused.relu(), sep.relu()
+    assert np.array_equal(np.asarray(fused.to_vec()).view(np.uint32), np.asarray(sep.to_vec()).view(np.uint32))
+    fused.mul(g).sum([bt, fo]).backward()
+    sep.mul(g).sum([bt, fo]).backward()
+    pairs = [(x1.grad(), x2.grad()), (layer.parameter("weight").grad(), wt.grad()),
+             (layer.parameter("bias").grad(), bb.grad())]
+    for got, ref in pairs:
+        assert np.array_equal(np.asarray(got.to_vec()).view(np.uint32), np.asarray(ref.to_vec()).view(np.uint32))
+
+
 @pytest.mark.parametrize("lhs_t,rhs_t,tracked", [(False, True, False), (True, False, False), (True, True, False),
                                                  (False, True, True), (True, False, True)])
 def test_contract_reads_transposed_operands(ax, device, lhs_t, rhs_t, tracked):
