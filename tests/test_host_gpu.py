@@ -537,6 +537,38 @@ def test_cnn_small_batch_step_matches_oracle(ax, device, oracle):
                               ref["params"][theirs])
 
 
+def test_cnn_fused_mean_backwards_match_materialised_broadcasts(ax, device):
+    # The CNN step takes three fused backward paths that each fold a launch away: the loss's
+    # mean over the batch into the cross-entropy backward (with the classifier's bias gradient), and
+    # the mean over [height, width] into conv3's ReLU/pool backward.  A second reader of each mean's
+    # input (a zero-weighted sum) keeps the plain rules; every gradient must agree in value.
+    batch, size, classes, ch = 4, 16, 50, (3, 8, 16, 32)
+    model, features, head, bt, c0, h, w, cls = build_cnn(ax, device, batch, size, classes, ch)
+    rng = np.random.default_rng(11)
+    x = ax.Tensor.from_slice(rng.uniform(0, 1, batch * 3 * size * size).astype(np.float32),
+                             [bt.of(batch), c0.of(3), h.of(size), w.of(size)], device)
+    labels = np.zeros((batch, classes), np.float32)
+    labels[np.arange(batch), rng.integers(0, classes, batch)] = 1.0
+    y = ax.Tensor.from_slice(labels.reshape(-1), [bt.of(batch), cls.of(classes)], device)
+    names = [n for n, _ in model.named_parameters()]
+
+    def grads(plain):
+        for n in names:
+            model.parameter(n).zero_grad()
+        pooled = features.forward(x)
+        feats = pooled.mean([h, w])
+        per_row = head.forward(feats).categorical_cross_entropy_with_logits(y, cls)
+        loss = per_row.mean([bt])
+        if plain:  # second readers: the means' inputs no longer feed one rule only
+            loss = loss.add(pooled.sum(list(pooled.shape.axes())).scale(0.0)).add(per_row.sum([bt]).scale(0.0))
+        loss.backward()
+        return {n: np.asarray(model.parameter(n).grad().to_vec()) for n in names}
+
+    fused, plain = grads(False), grads(True)
+    for n in names:
+        assert np.array_equal(fused[n], plain[n]), n
+
+
 # ---------------------------------------------------------------- convolution block lowerings
 
 def _torch_block(x_nchw, weight, bias, kh, kw, stride, pad, pool):
