@@ -26,6 +26,14 @@ def test_library_exports_every_declared_symbol():
     assert b"gfx950" in lib.axis_version()
 
 
+def test_integration_binding_covers_every_entry():
+    # the reference-side Rust extern block must bind every entry point the header declares
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    text = open(os.path.join(root, "INTEGRATION.md")).read()
+    missing = [name for name in hip.header_functions() if f"pub fn {name}(" not in text]
+    assert not missing, missing
+
+
 def test_library_is_built_for_gfx950_only(tmp_path):
     build = os.path.join(os.path.dirname(hip.LIB_PATH), "_build")
     objs = [os.path.join(build, f) for f in os.listdir(build) if f.endswith(".o")
