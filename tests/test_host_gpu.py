@@ -595,6 +595,64 @@ BLOCK_CASES = [
 ]
 
 
+def _random_blocks():
+    rng = np.random.default_rng(777)
+    cases = []
+    while len(cases) < 16:
+        k = int(rng.choice([1, 3, 3, 5]))
+        stride = int(rng.choice([1, 1, 2]))
+        pool = [(2, 2, 0), (2, 2, 0), (3, 2, 1), (2, 1, 0), None][int(rng.integers(0, 5))]
+        c = int(rng.choice([int(rng.integers(1, 9)), 16, 32, 64]))
+        out = int(rng.choice([int(rng.integers(1, 40)), 64, 128]))
+        hh, ww = int(rng.integers(4, 21)), int(rng.integers(4, 21))
+        layout = "nhwc" if rng.integers(0, 3) else "nchw"
+        cases.append((layout, bool(rng.integers(0, 2)), int(rng.integers(1, 4)), c, hh, ww, out, k, stride, pool))
+    return cases
+
+
+@pytest.mark.parametrize("layout,needs_grad,b,c,hh,ww,out,k,stride,pool", _random_blocks())
+def test_random_conv_blocks_against_torch(ax, device, layout, needs_grad, b, c, hh, ww, out, k, stride, pool):
+    # seeded random geometries through whichever lowering the tape picks (fused block, implicit
+    # convolution + separate pool, explicit unfold) against torch float64 on the CPU
+    import torch
+    rng = np.random.default_rng(b * 1000 + c * 100 + hh * 10 + ww + out + k)
+    pad = k // 2
+    x_nchw = rng.standard_normal((b, c, hh, ww))
+    weight = rng.standard_normal((out, c, k, k)) * 0.3
+    bias = rng.standard_normal(out) * 0.1
+    bt_, ch, h, w, o = ax.Axis("batch"), ax.Axis("channel"), ax.Axis("height"), ax.Axis("width"), ax.Axis("out")
+    if layout == "nhwc":
+        dims, x_host = [bt_.of(b), h.of(hh), w.of(ww), ch.of(c)], x_nchw.transpose(0, 2, 3, 1)
+    else:
+        dims, x_host = [bt_.of(b), ch.of(c), h.of(hh), w.of(ww)], x_nchw
+    x = ax.Tensor.from_slice(np.ascontiguousarray(x_host, np.float32).reshape(-1), dims, device)
+    if needs_grad:
+        x = x.with_grad()
+    conv = ax.Conv2d(ch, o.of(out), [h, w], [k, k]).padding([pad, pad]).stride([stride, stride])
+    layers = [conv, ax.ReLU()]
+    if pool is not None:
+        layers.append(ax.MaxPool2d(o, [h, w], [pool[0], pool[0]]).stride([pool[1], pool[1]]).padding([pool[2], pool[2]]))
+    model = ax.Sequential(layers)
+    model.build(x.shape, device, 3)
+    conv.parameter("weight").set_values(np.ascontiguousarray(weight.transpose(1, 2, 3, 0), np.float32).reshape(-1))
+    conv.parameter("bias").set_values(bias.astype(np.float32))
+    y = model.forward(x)
+    xt, wt, btt, yt = _torch_block(x_nchw, weight, bias, k, k, stride, pad, pool)
+    y_ref = yt.detach().numpy().transpose(0, 2, 3, 1)
+    assert rel_max(y.to_vec(), y_ref.reshape(-1)) < 1e-5
+    r = rng.standard_normal(y_ref.shape)
+    rt = ax.Tensor.from_slice(r.astype(np.float32).reshape(-1), [bt_.of(b), h.of(r.shape[1]), w.of(r.shape[2]), o.of(out)],
+                              device)
+    y.mul(rt).sum([bt_, h, w, o]).backward()
+    (yt * torch.tensor(r.transpose(0, 3, 1, 2), dtype=torch.float64)).sum().backward()
+    assert rel_max(conv.parameter("weight").grad().to_vec(), wt.grad.numpy().transpose(1, 2, 3, 0).reshape(-1)) < 1e-4
+    assert rel_max(conv.parameter("bias").grad().to_vec(), btt.grad.numpy()) < 1e-4
+    if needs_grad:
+        gx = xt.grad.numpy()
+        gx = gx.transpose(0, 2, 3, 1) if layout == "nhwc" else gx
+        assert rel_max(x.grad().to_vec(), gx.reshape(-1)) < 1e-4
+
+
 @pytest.mark.parametrize("case", range(len(BLOCK_CASES)))
 def test_conv_relu_pool_block_lowerings(ax, device, case):
     layout, needs_grad, stride, pool = BLOCK_CASES[case]
