@@ -595,6 +595,52 @@ BLOCK_CASES = [
 ]
 
 
+def _random_mlps():
+    rng = np.random.default_rng(4321)
+    cases = []
+    for _ in range(10):
+        depth = int(rng.integers(1, 4))
+        sizes = [int(rng.choice([int(rng.integers(1, 40)), int(rng.integers(40, 700))])) for _ in range(depth + 1)]
+        sizes[-1] = max(sizes[-1], 2)  # classes
+        cases.append((int(rng.choice([1, int(rng.integers(2, 64)), int(rng.integers(64, 700))])), tuple(sizes)))
+    return cases
+
+
+@pytest.mark.parametrize("batch,sizes", _random_mlps())
+def test_random_mlp_step_against_torch(ax, device, batch, sizes):
+    # Linear (bias in the product) -> ReLU ... -> mean softmax cross-entropy: every fused rule of
+    # the MLP path (bias with the ReLU mask, the mean folded into the cross-entropy backward with the
+    # last bias gradient) against torch float64 autograd
+    import torch
+    model, bt, feats = build_mlp(ax, device, batch, list(sizes))
+    rng = np.random.default_rng(batch + sum(sizes))
+    xv = rng.standard_normal((batch, sizes[0])).astype(np.float32)
+    labels = rng.integers(0, sizes[-1], batch)
+    yv = np.zeros((batch, sizes[-1]), np.float32)
+    yv[np.arange(batch), labels] = 1.0
+    x = ax.Tensor.from_slice(xv.reshape(-1), [bt.of(batch), feats[0].of(sizes[0])], device)
+    y = ax.Tensor.from_slice(yv.reshape(-1), [bt.of(batch), feats[-1].of(sizes[-1])], device)
+    loss = model.forward(x).categorical_cross_entropy_with_logits(y, feats[-1]).mean([bt])
+    loss.backward()
+    h = torch.tensor(xv, dtype=torch.float64)
+    params = []
+    for j in range(len(sizes) - 1):
+        wv = np.asarray(model.parameter(f"{2 * j}.weight").tensor().to_vec(), np.float64).reshape(sizes[j], sizes[j + 1])
+        bv = np.asarray(model.parameter(f"{2 * j}.bias").tensor().to_vec(), np.float64)
+        wt = torch.tensor(wv, requires_grad=True)
+        bt_ = torch.tensor(bv, requires_grad=True)
+        params.append((f"{2 * j}", wt, bt_))
+        h = h @ wt + bt_
+        if j < len(sizes) - 2:
+            h = h.relu()
+    ref = torch.nn.functional.cross_entropy(h, torch.tensor(labels))
+    ref.backward()
+    assert abs(loss.item() - ref.item()) <= 1e-5 * max(1.0, abs(ref.item()))
+    for name, wt, bt_ in params:
+        assert rel_max(model.parameter(name + ".weight").grad().to_vec(), wt.grad.numpy().reshape(-1)) < 1e-4, name
+        assert rel_max(model.parameter(name + ".bias").grad().to_vec(), bt_.grad.numpy()) < 1e-4, name
+
+
 def _random_blocks():
     rng = np.random.default_rng(777)
     cases = []
