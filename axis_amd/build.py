@@ -28,14 +28,14 @@ HIP_FLAGS = [
     "-Wno-unused-command-line-argument",
 ]
 # Sources whose arithmetic must round exactly as written (no fused multiply-add contraction).
-EXACT = {"device.hip", "unfold.hip", "grouped.hip", "elementwise.hip", "pool.hip", "loss.hip",
+EXACT = {"device.hip", "finish.hip", "unfold.hip", "grouped.hip", "elementwise.hip", "pool.hip", "loss.hip",
          "optim.hip", "conv_small.hip", "gemm_bf16.hip"}
 # Matrix-core kernels keep their accumulators in ordinary VGPRs: the MFMA VGPR form avoids the
 # per-iteration AGPR<->VGPR copies the default allocation inserts around the K loop.
 EXTRA = {"gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
          "conv_small.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
          "gemm_bf16.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
-HIP_SOURCES = ["device.hip", "gemm.hip", "gemm_bf16.hip", "conv_small.hip", "unfold.hip", "grouped.hip", "elementwise.hip",
+HIP_SOURCES = ["device.hip", "finish.hip", "gemm.hip", "gemm_bf16.hip", "conv_small.hip", "unfold.hip", "grouped.hip", "elementwise.hip",
                "pool.hip", "loss.hip", "optim.hip"]
 
 

@@ -4,6 +4,7 @@
 #pragma once
 
 #include "common.hpp"
+#include "finish.hpp"
 
 namespace axis {
 
@@ -41,10 +42,10 @@ __global__ static void __launch_bounds__(256) column_combine_kernel(const float 
 
 // Sum over the rows of partial[rows][width] (row pitch `pitch`) in a fixed association: the 16
 // waves of a block take consecutive row ranges of ceil(rows / 16), each summed in row order, and
-// the 16 range sums are added in range order.  Used for per-block partials of this library's own
-// fused kernels (not a reference summation order).  One block per 64 columns (a lane per column,
-// so every row read is coalesced); columns below `split` go to out_a[e], the rest to
-// out_b[e - split] (skipped when out_b is null).
+// the 16 range sums are added in range order (column_block_part / column_block_store).  Used for
+// per-block partials of this library's own fused kernels (not a reference summation order).  One
+// block per 64 columns (a lane per column, so every row read is coalesced); columns below `split`
+// go to out_a[e], the rest to out_b[e - split] (skipped when out_b is null).
 __global__ static void __launch_bounds__(1024) column_block_sum_kernel(const float *__restrict__ partial,
                                                                        int64_t rows, int64_t width, int64_t pitch,
                                                                        int64_t split, float *__restrict__ out_a,
@@ -52,39 +53,31 @@ __global__ static void __launch_bounds__(1024) column_block_sum_kernel(const flo
     __shared__ float range_sum[16][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t e = (int64_t)blockIdx.x * 64 + lane;
-    const int64_t span = (rows + 15) / 16;
-    const int64_t r0 = wave * span;
-    const int64_t r1 = r0 + span < rows ? r0 + span : rows;
-    float s = 0.0f;
-    if (e < width) {
-        constexpr int kBatch = 64;  // loads in flight per lane: the range takes few round trips
-        int64_t r = r0;
-        for (; r + kBatch <= r1; r += kBatch) {
-            float v[kBatch];
-#pragma unroll
-            for (int u = 0; u < kBatch; ++u) v[u] = partial[(r + u) * pitch + e];
-#pragma unroll
-            for (int u = 0; u < kBatch; ++u) s = s + v[u];
-        }
-        for (; r < r1; ++r) s = s + partial[r * pitch + e];
-    }
-    range_sum[wave][lane] = s;
+    range_sum[wave][lane] = column_block_part(partial, rows, width, pitch, e, wave);
     __syncthreads();
-    if (wave == 0 && e < width) {
-        float total = 0.0f;
-#pragma unroll
-        for (int w = 0; w < 16; ++w) total = total + range_sum[w][lane];
-        if (e < split)
-            out_a[e] = total;
-        else if (out_b)
-            out_b[e - split] = total;
-    }
+    if (wave == 0 && e < width) column_block_store(&range_sum[0][lane], e, split, out_a, out_b);
 }
 
-inline int column_block_sum(hipStream_t stream, const float *partial, int64_t rows, int64_t width, int64_t pitch,
+// The column block sum of `partial` (held by `owner`), launched now, or recorded with `owner`'s
+// block held when the handle defers finishing sums (the outputs are then final gradients).
+inline int column_block_sum(axis_device device, Scratch &owner, int64_t rows, int64_t width, int64_t pitch,
                             int64_t split, float *out_a, float *out_b) {
-    column_block_sum_kernel<<<(unsigned)((width + 63) / 64), 1024, 0, stream>>>(partial, rows, width, pitch, split,
-                                                                              out_a, out_b);
+    const float *partial = owner.as<float>();
+    if (device->deferring) {
+        FinishTask t{};
+        t.partial = partial;
+        t.out_a = out_a;
+        t.out_b = out_b;
+        t.len = width;
+        t.count = rows;
+        t.stride = pitch;
+        t.split = split;
+        t.kind = 1;
+        t.blocks = (int32_t)((width + 15) / 16);
+        return defer_finish(device, t, owner);
+    }
+    column_block_sum_kernel<<<(unsigned)((width + 63) / 64), 1024, 0, device->stream>>>(partial, rows, width, pitch,
+                                                                                      split, out_a, out_b);
     return launch_status("column_block_sum_kernel");
 }
 

@@ -11,6 +11,7 @@
 #include <unordered_map>
 
 #include "../../include/axis_hip.h"
+#include "finish.hpp"
 
 struct axis_device_s {
     int ordinal = 0;
@@ -39,6 +40,12 @@ struct axis_device_s {
     std::vector<hipEvent_t> spare_events;
     // This GPU's copy of the allocation-free product's scratch array (gemm.hip), bound at create.
     float *static_scratch = nullptr;
+    // Deferred finishing sums (axis_finish_defer): while on, the last sum of a weight or bias
+    // gradient is recorded here instead of launched, and the scratch block it reads is held, until
+    // one batched launch (axis_finish_flush) runs every recorded sum.
+    bool deferring = false;
+    std::vector<axis::FinishTask> deferred;
+    std::vector<void *> deferred_blocks;
 };
 
 struct axis_plan_s {
@@ -80,7 +87,18 @@ struct Scratch {
         return alloc(d, bytes, &ptr);
     }
     template <class T> T *as() const { return static_cast<T *>(ptr); }
+    void *take() {  // the caller now owns the block
+        void *p = ptr;
+        ptr = nullptr;
+        return p;
+    }
 };
+
+// Records a finishing sum on a deferring handle and takes `held` (the block the sum reads) until
+// the batched launch has been enqueued (finish.hip).  A full batch is launched first.
+int defer_finish(axis_device device, const FinishTask &task, Scratch &held);
+// Launches every recorded sum in one kernel and returns their blocks to the allocator.
+int flush_finish(axis_device device);
 
 inline unsigned blocks_for(int64_t work, int per_block, int64_t cap = 1 << 20) {
     int64_t b = (work + per_block - 1) / per_block;

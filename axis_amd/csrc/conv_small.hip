@@ -560,8 +560,8 @@ int small_conv_pool_backward_weight(axis_device device, const SmallConvShape &s,
     }
     // d_weight[t][n] (t < k) and d_bias[n] (t = k) = the sum over blocks of partial[block][t][n]
     const int64_t outputs = (int64_t)(a.k + (d_bias ? 1 : 0)) * a.n;
-    return column_block_sum(device->stream, partial.as<float>(), blocks, outputs, 32 * (int64_t)a.n,
-                            (int64_t)a.k * a.n, d_weight, d_bias);
+    return column_block_sum(device, partial, blocks, outputs, 32 * (int64_t)a.n, (int64_t)a.k * a.n, d_weight,
+                            d_bias);
 }
 
 }  // namespace axis

@@ -211,6 +211,7 @@ int axis_device_destroy(axis_device device) {
 
 int axis_device_synchronize(axis_device device) {
     AXIS_ENTER(device);
+    if (int st = axis::flush_finish(device)) return st;
     AXIS_HIP(hipStreamSynchronize(device->stream));
     return AXIS_OK;
 }
@@ -231,7 +232,10 @@ int axis_alloc(axis_device device, size_t bytes, void **out) {
 int axis_free(axis_device device, void *ptr) {
     AXIS_ENTER(device);
     if (!ptr) return AXIS_OK;
-    AXIS_REQUIRE(device->live.count(ptr), "axis_free of a pointer this device did not allocate");
+    auto it = device->live.find(ptr);
+    AXIS_REQUIRE(it != device->live.end(), "axis_free of a pointer this device did not allocate");
+    // a deferred sum still to write here runs first (its block is then free to reuse)
+    if (int st = axis_finish_before_read(device, ptr, it->second)) return st;
     axis::release(device, ptr);
     return AXIS_OK;
 }
@@ -264,6 +268,7 @@ int axis_read(axis_device device, void *dst, const void *src, size_t bytes) {
     AXIS_ENTER(device);
     if (bytes == 0) return AXIS_OK;
     AXIS_REQUIRE(dst && src, "null read pointer");
+    if (int st = axis_finish_before_read(device, src, bytes)) return st;
     AXIS_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, device->stream));
     AXIS_HIP(hipStreamSynchronize(device->stream));
     return AXIS_OK;
@@ -273,6 +278,7 @@ int axis_copy(axis_device device, void *dst, const void *src, size_t bytes) {
     AXIS_ENTER(device);
     if (bytes == 0) return AXIS_OK;
     AXIS_REQUIRE(dst && src, "null copy pointer");
+    if (int st = axis_finish_before_read(device, src, bytes)) return st;
     AXIS_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, device->stream));
     return AXIS_OK;
 }

@@ -580,19 +580,7 @@ struct ConvColsStepLoader : Staging<BT, BK, NT, false, VEC> {
 };
 
 // Finishes one output value v (the whole reduction) at flat output index idx: + bias[col], then
-// beta * d + alpha * v.  Each product and the sum round separately, as the separate scale / scale
-// / add operations they replace.
-__device__ __forceinline__ float finish_value(const float *bias, const float *d, float alpha, float beta,
-                                              float v, int64_t idx, int64_t col) {
-#pragma clang fp contract(off)
-    if (bias) v = v + bias[col];
-    if (d) {
-        const float t1 = beta * d[idx];
-        const float t2 = alpha * v;
-        v = t1 + t2;
-    }
-    return v;
-}
+using axis::finish_value;
 
 // XMODE: 0 dense X, 1 convolution rows mode, 2 convolution cols mode, 3 cols mode over aligned
 // pixel steps, 4 rows mode through buffer loads.
@@ -938,10 +926,10 @@ __global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
     }
 }
 
-// Sum of reduction slices: lane group g (of 4) adds slices g, g+4, g+8, ... in order, then the
-// four group sums are added in group order -- a fixed association for a given slice count, so
-// the result is deterministic and independent of scheduling.  The bias, when present, is added
-// to the total.
+// Sum of reduction slices (split_sum_part / split_sum_store): lane group g (of 4) adds slices
+// g, g+4, g+8, ... in order, then the four group sums are added in group order -- a fixed
+// association for a given slice count, so the result is deterministic and independent of
+// scheduling.  The bias, when present, is added to the total.
 __global__ void __launch_bounds__(256) split_sum_kernel(const float *__restrict__ partial,
                                                         float *__restrict__ out, int64_t len,
                                                         int32_t splits, int64_t split_stride,
@@ -951,20 +939,11 @@ __global__ void __launch_bounds__(256) split_sum_kernel(const float *__restrict_
     __shared__ float acc[4][64];
     const int lane = threadIdx.x & 63, group = threadIdx.x >> 6;
     const int64_t i = (int64_t)blockIdx.x * 64 + lane;
-    float s = 0.f;
-    if (i < len)
-        for (int32_t k = group; k < splits; k += 4) s += partial[k * split_stride + i];
-    acc[group][lane] = s;
+    acc[group][lane] = axis::split_sum_part(partial, i, len, splits, split_stride, group);
     __syncthreads();
-    if (group == 0 && i < len) {
-        const float total = ((acc[0][lane] + acc[1][lane]) + acc[2][lane]) + acc[3][lane];
-        int64_t at = i;
-        if (perm_c) {  // row (pos, c) -> c * taps + pos
-            const int64_t row = i / n, col = i - row * n;
-            at = ((row % perm_c) * perm_taps + row / perm_c) * n + col;
-        }
-        out[at] = finish_value(bias, d, alpha, beta, total, i, i % n);
-    }
+    if (group == 0 && i < len)
+        axis::split_sum_store(out, i, acc[0][lane], acc[1][lane], acc[2][lane], acc[3][lane], bias, n, d, alpha,
+                              beta, perm_c, perm_taps);
 }
 
 // First level for many slices: mid[g][i] = sum of slices [g*span, (g+1)*span) in order.
@@ -975,9 +954,17 @@ __global__ void __launch_bounds__(256) split_range_kernel(const float *__restric
     if (i >= len) return;
     const int32_t g = blockIdx.y;
     const int32_t k1 = (g + 1) * span < splits ? (g + 1) * span : splits;
+    // slice order; eight loads in flight before their adds
+    constexpr int kAhead = 8;
     float s = 0.f;
-#pragma unroll 8
-    for (int32_t k = g * span; k < k1; ++k) s += partial[(int64_t)k * len + i];
+    for (int32_t k0 = g * span; k0 < k1; k0 += kAhead) {
+        float v[kAhead];
+#pragma unroll
+        for (int u = 0; u < kAhead; ++u) v[u] = k0 + u < k1 ? partial[(int64_t)(k0 + u) * len + i] : 0.f;
+#pragma unroll
+        for (int u = 0; u < kAhead; ++u)
+            if (k0 + u < k1) s += v[u];
+    }
     mid[(int64_t)g * len + i] = s;
 }
 
@@ -1164,29 +1151,50 @@ DenseSchedule dense_schedule(int64_t m, int64_t n, int64_t k, int64_t batch, int
 
 // Deterministic sum of reduction slices (+ bias): up to 32 slices in one pass; beyond that, ranges
 // of 32 consecutive slices first, then the range sums -- a fixed association for a given count.
+// `owner` (the block holding `partial`), when given and the handle defers finishing sums, lets
+// the last pass be recorded instead of launched: `out` is then a final gradient.
 int sum_splits(axis_device device, const float *partial, float *out, int64_t len, int64_t splits,
                const float *bias, int64_t n, const float *d, float alpha, float beta, int32_t perm_c,
-               int32_t perm_taps, float *mid_space = nullptr) {
+               int32_t perm_taps, float *mid_space = nullptr, axis::Scratch *owner = nullptr) {
     const unsigned blocks = axis::blocks_for(len, 64, INT32_MAX);
-    if (splits <= 32) {
-        split_sum_kernel<<<blocks, 256, 0, device->stream>>>(partial, out, len, (int32_t)splits, len, bias, n, d,
+    const bool defer = owner && device->deferring && len <= (int64_t)INT32_MAX * 64 / 2;
+    auto last_pass = [&](const float *slices, int64_t count, axis::Scratch &held) {
+        if (defer) {
+            axis::FinishTask t{};
+            t.partial = slices;
+            t.out_a = out;
+            t.bias = bias;
+            t.d = d;
+            t.len = len;
+            t.count = count;
+            t.stride = len;
+            t.n = n;
+            t.alpha = alpha;
+            t.beta = beta;
+            t.perm_c = perm_c;
+            t.perm_taps = perm_taps;
+            t.kind = 0;
+            t.blocks = (int32_t)((len + 63) / 64);
+            return axis::defer_finish(device, t, held);
+        }
+        split_sum_kernel<<<blocks, 256, 0, device->stream>>>(slices, out, len, (int32_t)count, len, bias, n, d,
                                                              alpha, beta, perm_c, perm_taps);
         return axis::launch_status("split_sum_kernel");
-    }
+    };
+    axis::Scratch none;
+    if (splits <= 32) return last_pass(partial, splits, defer ? *owner : none);
     const int32_t span = 32;
     const int64_t ranges = (splits + span - 1) / span;
     axis::Scratch mid;
     float *sums = mid_space;
-    if (!sums) {
+    if (!sums || defer) {
         if (int st = mid.get(device, sizeof(float) * (size_t)(ranges * len))) return st;
         sums = mid.as<float>();
     }
     dim3 grid(axis::blocks_for(len, 256, INT32_MAX), (unsigned)ranges);
     split_range_kernel<<<grid, 256, 0, device->stream>>>(partial, sums, len, (int32_t)splits, span);
     if (int st = axis::launch_status("split_range_kernel")) return st;
-    split_sum_kernel<<<blocks, 256, 0, device->stream>>>(sums, out, len, (int32_t)ranges, len, bias, n,
-                                                         d, alpha, beta, perm_c, perm_taps);
-    return axis::launch_status("split_sum_kernel");
+    return last_pass(sums, ranges, mid);
 }
 
 // Dense product on a bf16 device: both operands staged as bf16 rows, then bf16 matrix cores
@@ -1249,7 +1257,10 @@ int run_gemm_bf16(axis_device device, const GemmParams &p, int64_t batch, float 
 // ws: when non-null, the partial sums live there (nothing is allocated, nothing is timed) and a
 // launch whose partials would not fit is rejected before anything runs.
 template <bool XR, bool YR, int XMODE, int EPI>
-int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out, const Workspace *ws = nullptr) {
+// final_out: `out` is the entry's own result, read by nothing in the entry after this product, so
+// its split sum may be deferred (sum_splits).
+int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out, const Workspace *ws = nullptr,
+             bool final_out = false) {
     if constexpr (XMODE == 0 && EPI == 0)
         if (device->bf16_matmul && !p.ytaps.on && !p.perm_c) {
             if (ws) return axis::fail(AXIS_ERROR_INVALID, "the allocation-free product is fp32 only");
@@ -1377,7 +1388,7 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out, const 
     if (status) return status;
     if (splits > 1)
         status = sum_splits(device, partials, out, out_len, splits, p.bias, p.n, p.d, p.alpha, p.beta,
-                            p.perm_c, p.perm_taps, spare);
+                            p.perm_c, p.perm_taps, spare, final_out && !ws ? &partial : nullptr);
     else if (p.perm_c) {
         // mode 2 of the weight permutation with the taps as one axis
         conv_weight_permute_kernel<<<axis::blocks_for(out_len, 256, 4096), 256, 0, device->stream>>>(
@@ -1703,7 +1714,7 @@ int axis_matmul_right_backward(axis_device device, const float *lhs, const float
     p.y_sj = 1;
     p.x_batch = m * k;
     p.y_batch = m * n;
-    return run_gemm<false, false, 0, 0>(device, p, batch, out);
+    return run_gemm<false, false, 0, 0>(device, p, batch, out, nullptr, true);
 }
 
 int axis_matmul_right_backward_noalloc(axis_device device, const float *lhs, const float *gradient,
@@ -1888,7 +1899,8 @@ int axis_conv2d_backward_weight(axis_device device, const float *input,
     const bool aligned = (32 % s.out_w == 0 || s.out_w % 32 == 0) && image % 32 == 0 && s.px <= 32 * s.sx &&
                          s.py <= rows_per_step * s.sy;
     float *dst = direct ? d_weight : ordered.as<float>();
-    const int st = aligned ? run_gemm<false, false, 3, 0>(device, p, 1, dst) : run_gemm<false, false, 2, 0>(device, p, 1, dst);
+    const int st = aligned ? run_gemm<false, false, 3, 0>(device, p, 1, dst, nullptr, direct)
+                           : run_gemm<false, false, 2, 0>(device, p, 1, dst, nullptr, direct);
     if (st || direct) return st;
     return permute_weight(device, ordered.as<float>(), d_weight, s, 2, in.channels);
 }

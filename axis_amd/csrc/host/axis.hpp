@@ -136,6 +136,10 @@ class Device {
     Buffer upload_i32(const std::vector<int32_t> &values) const;
     std::vector<float> read(const Buffer &b) const;
     void synchronize() const;
+    // Weight and bias gradients' last sums recorded and run in one launch (axis_finish_*): on /
+    // off (off runs what is recorded), and the flush a read of a possibly pending buffer needs.
+    void finish_defer(bool on) const;
+    void finish_before_read(const Buffer &b) const;
     Buffer zeros_buffer(int64_t len) const;
     Buffer filled(int64_t len, float value) const;
     // A read-only [1] buffer holding 1.0, filled once per device.

@@ -201,6 +201,12 @@ std::vector<float> Device::read(const Buffer &b) const {
 
 void Device::synchronize() const { check(axis_device_synchronize(h()), "synchronize"); }
 
+void Device::finish_defer(bool on) const { check(axis_finish_defer(h(), on ? 1 : 0), "finish_defer"); }
+
+void Device::finish_before_read(const Buffer &b) const {
+    if (b) check(axis_finish_before_read(h(), b->ptr, (size_t)b->bytes), "finish_before_read");
+}
+
 Buffer Device::zeros_buffer(int64_t len) const { return filled(len, 0.0f); }
 
 Buffer Device::filled(int64_t len, float value) const {

@@ -955,6 +955,21 @@ void Tensor::backward() const {
             }
     }
     const Device &dev = device();
+    // The last sums of weight and bias gradients (split-K slices, per-block partials) are recorded
+    // and run in one launch before the commit; a rule about to read a buffer that such a sum may
+    // still have to write asks for it first (finish_before_read).
+    struct Deferral {
+        const Device &dev;
+        bool on = true;
+        explicit Deferral(const Device &d) : dev(d) { dev.finish_defer(true); }
+        void finish() {
+            on = false;
+            dev.finish_defer(false);
+        }
+        ~Deferral() {
+            if (on) (void)axis_finish_defer(dev.h(), 0);
+        }
+    } deferral(dev);
     std::unordered_map<uint64_t, Buffer> adjoints;
     // Bias gradients produced together with a ReLU backward (one pass over the activation), keyed
     // by the bias-add node whose BiasBroadcast edge they answer.
@@ -979,6 +994,7 @@ void Tensor::backward() const {
         Buffer g = found->second;
         adjoints.erase(found);
         if (nd.n->edges) {
+            dev.finish_before_read(g);
             for (auto &e : *nd.n->edges) {
                 const Rule &r = e.rule;
                 Buffer c;
@@ -1229,16 +1245,20 @@ void Tensor::backward() const {
                 }
                 uint64_t input_id = e.input.id();
                 auto existing = adjoints.find(input_id);
-                if (existing != adjoints.end())
+                if (existing != adjoints.end()) {
+                    dev.finish_before_read(existing->second);
+                    dev.finish_before_read(c);
                     existing->second = dev.binary(existing->second, c, 0);
-                else
+                } else
                     adjoints.emplace(input_id, c);
             }
         } else {
+            if (nd.n->grad) dev.finish_before_read(g);
             Buffer sum = nd.n->grad ? dev.binary(nd.n->grad, g, 0) : g;
             leaves.emplace_back(nd, sum);
         }
     }
+    deferral.finish();
     // Commit only after every device operation was enqueued successfully.
     for (auto &[leaf, gradient] : leaves) leaf.n->grad = gradient;
     for (auto &nd : order) {

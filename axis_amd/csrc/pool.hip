@@ -477,8 +477,7 @@ int relu_pool_backward(axis_device device, const float *gradient, bool broadcast
             relu_pool_backward_bias_kernel<1><<<nb, 256, 0, device->stream>>>(gradient, pooled, argmax, d_pre,
                                                                             partial.as<float>(), span, a);
         if (int s = axis::launch_status("relu_pool_backward_bias_kernel")) return s;
-        return axis::column_block_sum(device->stream, partial.as<float>(), nb, channels, channels, channels, d_bias,
-                                      nullptr);
+        return axis::column_block_sum(device, partial, nb, channels, channels, channels, d_bias, nullptr);
     }
     if (vec)
         relu_pool_backward_kernel<4><<<axis::blocks_for(a.total, 256, INT32_MAX), 256, 0, device->stream>>>(

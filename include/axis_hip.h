@@ -85,6 +85,23 @@ int axis_timing_reset(axis_device device);
 int axis_timing_read(axis_device device, const char *family, int64_t *launches, double *milliseconds,
                      double *work);
 
+/* Deferred finishing sums, off by default (no counterpart in the reference: a launch schedule of
+ * this library, used by the autograd tape's backward pass).  While enabled, the entries that
+ * produce weight and bias gradients -- axis_matmul_right_backward, axis_conv2d_backward_weight,
+ * axis_conv2d_relu_pool_backward_weight, and the d_bias of axis_relu_pool_backward(_mean) --
+ * enqueue their products and scatters but record the last sum over their partial results instead
+ * of launching it; those outputs hold their values only once the recorded sums have run.
+ * axis_finish_flush runs every recorded sum in one launch, with the same results bit for bit;
+ * axis_finish_before_read flushes when a recorded sum writes into [ptr, ptr + bytes);
+ * axis_finish_defer(device, 0) flushes and stops deferring.  axis_read, axis_copy, axis_free and
+ * axis_device_synchronize flush first themselves; any other entry that takes such an output as
+ * input must be preceded by one of the calls above. */
+int axis_finish_defer(axis_device device, int enabled);
+int axis_finish_flush(axis_device device);
+int axis_finish_before_read(axis_device device, const void *ptr, size_t bytes);
+/* Sums recorded and not yet run. */
+int axis_finish_pending(axis_device device, int64_t *tasks);
+
 /* ------------------------------------------------------------------ contractions */
 
 /* Device::matmul (backend.rs:934-957): out[b] = a[b] . b[b]; a [batch,m,k], b [batch,k,n],

@@ -1159,3 +1159,136 @@ def test_matmul_axpby_rejects_aliasing(dev):
     with pytest.raises(hip.AxisError, match="alias"):
         dev.call("axis_matmul_axpby", buf.vp, buf.vp, buf.vp, buf.vp, I64(1), I64(4), I64(4), I64(4), F32(1.0),
                  F32(1.0))
+
+
+# ---------------------------------------------------------------- deferred finishing sums
+
+def _pending(dev):
+    n = ctypes.c_int64()
+    dev.call("axis_finish_pending", ctypes.byref(n))
+    return n.value
+
+
+def _gradient_entries(dev, rng):
+    """Weight and bias gradient entries whose last sums a deferring handle records: each returns
+    (list of (output buffer, length)) after enqueueing its call."""
+    calls = []
+    for (batch, m, k, n) in [(1, 8192, 64, 48),     # split-K, one level (<= 32 slices)
+                             (1, 65536, 64, 64),    # more than 32 slices: range sums first
+                             (2, 4096, 96, 40),     # batched split-K
+                             (1, 64, 256, 256)]:    # unsplit: nothing to defer
+        lhs = up(dev, rng.standard_normal(batch * m * k).astype(np.float32))
+        g = up(dev, rng.standard_normal(batch * m * n).astype(np.float32))
+
+        def right(out, lhs=lhs, g=g, geo=(batch, m, k, n)):
+            dev.call("axis_matmul_right_backward", lhs.vp, g.vp, out.vp, *map(I64, geo))
+        calls.append((right, [batch * k * n]))
+    # convolution weight gradient (channels need no padding: the split sum writes the result)
+    b, h, w, c, n = 4, 32, 32, 64, 128
+    x = up(dev, rng.standard_normal(b * h * w * c).astype(np.float32))
+    gc = up(dev, rng.standard_normal(b * h * w * n).astype(np.float32))
+    geo = [(I32 * 2)(3, 3), (I32 * 2)(1, 1), (I32 * 2)(1, 1)]
+
+    def conv_w(out):
+        dev.call("axis_conv2d_backward_weight", x.vp, None, gc.vp, out.vp, I64(b), I32(h), I32(w), I32(c), I32(n),
+                 *geo)
+    calls.append((conv_w, [c * 9 * n]))
+    # ReLU/pool backward with the bias folded into the scatter (per-block partials)
+    z = rng.integers(-3, 4, b * h * w * n).astype(np.float32) * 0.5
+    dz = up(dev, np.maximum(z, 0).astype(np.float32))
+    win = (I32 * 2)(2, 2)
+    pooled, arg = dev.empty(len(z) // 4), dev.empty(len(z) // 4, np.uint8)
+    dev.call("axis_max_pool2d", dz.vp, pooled.vp, arg.vp, I64(b), I32(h), I32(w), I64(n), win, win, (I32 * 2)(0, 0))
+    gp = up(dev, rng.standard_normal(len(z) // 4).astype(np.float32))
+    d_pre = dev.empty(len(z))
+
+    def pool_bias(out):
+        dev.call("axis_relu_pool_backward", gp.vp, pooled.vp, arg.vp, d_pre.vp, out.vp, I64(b), I32(h), I32(w),
+                 I32(n), win)
+    calls.append((pool_bias, [n]))
+    # conv1's fused weight and bias gradient straight from the pooled gradient (one partial sum
+    # feeding two outputs)
+    b1, h1, c1, n1 = 2, 64, 3, 64
+    x1 = up(dev, rng.standard_normal(b1 * c1 * h1 * h1).astype(np.float32))
+    s1 = (I64 * 4)(c1 * h1 * h1, h1 * h1, h1, 1)
+    w1 = up(dev, rng.standard_normal(c1 * 9 * n1).astype(np.float32) * 0.2)
+    bias1 = up(dev, rng.standard_normal(n1).astype(np.float32) * 0.1)
+    pooled1, arg1 = dev.empty(b1 * 32 * 32 * n1), dev.empty(b1 * 32 * 32 * n1, np.uint8)
+    dev.call("axis_conv2d_relu_pool_forward", x1.vp, s1, w1.vp, bias1.vp, pooled1.vp, arg1.vp, I64(b1), I32(h1),
+             I32(h1), I32(c1), I32(n1), *geo, win)
+    g1 = up(dev, rng.standard_normal(b1 * 32 * 32 * n1).astype(np.float32))
+
+    def conv1_wb(out_w, out_b):
+        dev.call("axis_conv2d_relu_pool_backward_weight", x1.vp, s1, g1.vp, pooled1.vp, arg1.vp, out_w.vp, out_b.vp,
+                 I64(b1), I32(h1), I32(h1), I32(c1), I32(n1), *geo, win)
+    calls.append((conv1_wb, [c1 * 9 * n1, n1]))
+    return calls
+
+
+def test_deferred_finishing_sums_are_bit_identical(dev):
+    # every entry's outputs with the last sums deferred and run in one batched launch: the same bits
+    # as the entry run alone; outputs hold their old contents until the flush
+    rng = np.random.default_rng(2024)
+    calls = _gradient_entries(dev, rng)
+    ref = []
+    for fn, lens in calls:
+        outs = [dev.empty(n) for n in lens]
+        fn(*outs)
+        ref.append([dev.read(o, n) for o, n in zip(outs, lens)])
+    assert _pending(dev) == 0
+    sentinel = np.float32(-7.25)
+    got = []
+    dev.call("axis_finish_defer", I32(1))
+    try:
+        for fn, lens in calls:
+            outs = [dev.empty(n) for n in lens]
+            for o, n in zip(outs, lens):
+                dev.call("axis_fill", o.vp, F32(sentinel), I64(n))
+            fn(*outs)
+            got.append(outs)
+        # one task per split product (not the unsplit one), the convolution, the pool bias and conv1
+        assert _pending(dev) == 3 + 1 + 1 + 1
+        # a read of an unrelated buffer leaves them pending; one of a pending output runs them all
+        other = dev.empty(16)
+        dev.call("axis_finish_before_read", other.vp, ctypes.c_size_t(64))
+        assert _pending(dev) == 6
+        dev.call("axis_finish_before_read", got[1][0].vp, ctypes.c_size_t(4))
+        assert _pending(dev) == 0
+    finally:
+        dev.call("axis_finish_defer", I32(0))
+    for r, outs, (fn, lens) in zip(ref, got, calls):
+        for expected, o, n in zip(r, outs, lens):
+            assert np.array_equal(dev.read(o, n).view(np.uint32), expected.view(np.uint32))
+
+
+def test_deferred_finishing_sums_flush_on_read_free_and_overflow(dev):
+    # axis_read of a pending output runs the batch; more tasks than one launch carries flush early;
+    # freeing a pending output runs its sum before the block is reused
+    rng = np.random.default_rng(7)
+    m, k, n = 8192, 32, 24
+    lhs = up(dev, rng.standard_normal(m * k).astype(np.float32))
+    g = up(dev, rng.standard_normal(m * n).astype(np.float32))
+    geo = (I64(1), I64(m), I64(k), I64(n))
+    ref = dev.empty(k * n)
+    dev.call("axis_matmul_right_backward", lhs.vp, g.vp, ref.vp, *geo)
+    expected = dev.read(ref, k * n)
+    dev.call("axis_finish_defer", I32(1))
+    try:
+        outs = []
+        for i in range(30):
+            o = dev.empty(k * n)
+            dev.call("axis_matmul_right_backward", lhs.vp, g.vp, o.vp, *geo)
+            outs.append(o)
+        assert 0 < _pending(dev) < 30
+        got = dev.read(outs[-1], k * n)   # flushes
+        assert _pending(dev) == 0
+        assert np.array_equal(got.view(np.uint32), expected.view(np.uint32))
+        for o in outs:
+            assert np.array_equal(dev.read(o, k * n).view(np.uint32), expected.view(np.uint32))
+        tmp = dev.empty(k * n)
+        dev.call("axis_matmul_right_backward", lhs.vp, g.vp, tmp.vp, *geo)
+        assert _pending(dev) == 1
+        del tmp                            # axis_free of a pending output
+        assert _pending(dev) == 0
+    finally:
+        dev.call("axis_finish_defer", I32(0))
