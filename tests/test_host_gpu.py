@@ -805,3 +805,32 @@ def test_contract_reads_transposed_operands(ax, device, lhs_t, rhs_t, tracked):
         y.mul(tg).sum([i, j]).backward()
         assert rel_max(la.grad().to_vec(), (g.astype(np.float64) @ b.T.astype(np.float64)).reshape(-1)) < 1e-4
         assert rel_max(lb.grad().to_vec(), (a.T.astype(np.float64) @ g.astype(np.float64)).reshape(-1)) < 1e-4
+
+
+@pytest.mark.parametrize("batch,n", [(4096, 64), (3000, 40)])
+def test_tied_weight_gradients_accumulate_after_deferred_sums(ax, device, batch, n):
+    # one weight used by two products: each product's weight gradient is a split-K sum the backward
+    # defers, and adding the two reads the first, which must run before the add; against torch
+    # float64 (the batch makes both weight gradients split their reductions)
+    import torch
+    rng = np.random.default_rng(batch + n)
+    bt, a, b = ax.Axis("batch"), ax.Axis("a"), ax.Axis("b")
+    wv = (rng.standard_normal((n, n)) / np.sqrt(n)).astype(np.float32)
+    xv = rng.standard_normal((batch, n)).astype(np.float32)
+    cv = rng.standard_normal((batch, n)).astype(np.float32)
+    w = ax.Parameter(ax.Tensor.from_slice(wv.reshape(-1), [a.of(n), b.of(n)], device))
+    x = ax.Tensor.from_slice(xv.reshape(-1), [bt.of(batch), a.of(n)], device)
+    coefficient = ax.Tensor.from_slice(cv.reshape(-1), [bt.of(batch), b.of(n)], device)
+    h = x.contract(w.tensor(), [a]).relu().rename(b, a)
+    out = h.contract(w.tensor(), [a])
+    loss = out.mul(coefficient).mean([bt, b])
+    loss.backward()
+    wt = torch.tensor(wv.astype(np.float64), requires_grad=True)
+    ref = ((torch.tensor(xv, dtype=torch.float64) @ wt).relu() @ wt * torch.tensor(cv, dtype=torch.float64)).mean()
+    ref.backward()
+    assert abs(loss.item() - ref.item()) <= 1e-5 * max(1.0, abs(ref.item()))
+    assert rel_max(w.grad().to_vec(), wt.grad.numpy().reshape(-1)) < 1e-4
+    # a second backward accumulates into the stored gradient
+    h = x.contract(w.tensor(), [a]).relu().rename(b, a)
+    h.contract(w.tensor(), [a]).mul(coefficient).mean([bt, b]).backward()
+    assert rel_max(w.grad().to_vec(), 2.0 * wt.grad.numpy().reshape(-1)) < 1e-4
