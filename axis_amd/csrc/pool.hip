@@ -192,44 +192,63 @@ __global__ void __launch_bounds__(256) relu_pool_backward_kernel(
 // per block and channel, summed afterwards in a fixed order (axis::column_block_sum).  The
 // association differs from the reference's 512-row chunks (fp32 tolerance, not bit equality) but
 // is the same on every run.
-template <int VEC>
+// BC: the pooled gradient is a mean's broadcast (a.g_broadcast), fixed per instance so the loop
+// carries no branch on it.
+template <int VEC, bool BC>
 __global__ void __launch_bounds__(256) relu_pool_backward_bias_kernel(
     const float *__restrict__ gradient, const float *__restrict__ pooled,
     const uint8_t *__restrict__ argmax, float *__restrict__ out, float *__restrict__ partial,
     uint32_t span, PoolArgs a) {
+    a.g_broadcast = BC;
     __shared__ float lane_sum[256][VEC];
     const uint32_t begin = blockIdx.x * span;
     const uint32_t end = begin + span < a.total ? begin + span : a.total;
     float acc[VEC];
 #pragma unroll
     for (int e = 0; e < VEC; ++e) acc[e] = 0.0f;
-    for (uint32_t t = begin + threadIdx.x; t < end; t += 256u) {
-        const uint32_t cv = a.cvec.mod(t);
-        uint32_t rest = a.cvec.div(t);
-        const int32_t ox = (int32_t)a.ow.mod(rest);
-        rest = a.ow.div(rest);
-        const int32_t oy = (int32_t)a.oh.mod(rest);
-        const uint32_t o = a.oh.div(rest);
-        const int32_t c = (int32_t)cv * VEC;
-        float g[VEC], y[VEC];
-        int w[VEC];
-        load_gradient<VEC>(gradient, t, o, c, a, g);
-        load_vec<VEC>(pooled + (int64_t)t * VEC, y);
+    // Two vectors per lane per pass (t and t + 256): both vectors' loads are in flight before the
+    // first stores; the bias terms are still added in t order.
+    for (uint32_t t0 = begin + threadIdx.x; t0 < end; t0 += 512u) {
+        const int pair = t0 + 256u < end ? 2 : 1;
+        float g[2][VEC], y[2][VEC];
+        uint32_t wb[2];
+        uint32_t o[2];
+        int32_t oy[2], ox[2], c[2];
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-            w[e] = y[e] > 0.0f ? (int)argmax[(int64_t)t * VEC + e] : -1;
-            acc[e] += (w[e] >= 0 && w[e] < a.ky * a.kx) ? 0.0f + g[e] : 0.0f;
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t t = h < pair ? t0 + 256u * h : t0;  // a missing second vector repeats the first's loads
+            const uint32_t cv = a.cvec.mod(t);
+            uint32_t rest = a.cvec.div(t);
+            ox[h] = (int32_t)a.ow.mod(rest);
+            rest = a.ow.div(rest);
+            oy[h] = (int32_t)a.oh.mod(rest);
+            o[h] = a.oh.div(rest);
+            c[h] = (int32_t)cv * VEC;
+            load_gradient<VEC>(gradient, t, o[h], c[h], a, g[h]);
+            load_vec<VEC>(pooled + (int64_t)t * VEC, y[h]);
+            // the vector's winner bytes in one load (4-byte aligned when VEC == 4)
+            wb[h] = VEC == 4 ? *reinterpret_cast<const uint32_t *>(argmax + (int64_t)t * VEC) : argmax[t];
         }
-        float *base = out + (int64_t)o * a.height * a.width * a.channels + c;
-        for (int32_t ky = 0; ky < a.ky; ++ky) {
-            const int32_t iy = oy * a.ky + ky;
-            for (int32_t kx = 0; kx < a.kx; ++kx) {
-                const int32_t ix = ox * a.kx + kx;
-                const int k = ky * a.kx + kx;
-                float r[VEC];
 #pragma unroll
-                for (int e = 0; e < VEC; ++e) r[e] = w[e] == k ? 0.0f + g[e] : 0.0f;
-                store_vec<VEC>(base + ((int64_t)iy * a.width + ix) * a.channels, r);
+        for (int h = 0; h < 2; ++h) {
+            if (h >= pair) break;
+            int w[VEC];
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) {
+                w[e] = y[h][e] > 0.0f ? (int)((wb[h] >> (8 * e)) & 0xffu) : -1;
+                acc[e] += (w[e] >= 0 && w[e] < a.ky * a.kx) ? 0.0f + g[h][e] : 0.0f;
+            }
+            float *base = out + (int64_t)o[h] * a.height * a.width * a.channels + c[h];
+            for (int32_t ky = 0; ky < a.ky; ++ky) {
+                const int32_t iy = oy[h] * a.ky + ky;
+                for (int32_t kx = 0; kx < a.kx; ++kx) {
+                    const int32_t ix = ox[h] * a.kx + kx;
+                    const int k = ky * a.kx + kx;
+                    float r[VEC];
+#pragma unroll
+                    for (int e = 0; e < VEC; ++e) r[e] = w[e] == k ? 0.0f + g[h][e] : 0.0f;
+                    store_vec<VEC>(base + ((int64_t)iy * a.width + ix) * a.channels, r);
+                }
             }
         }
     }
@@ -470,12 +489,19 @@ int relu_pool_backward(axis_device device, const float *gradient, bool broadcast
         const int32_t nb = (int32_t)((a.total + span - 1) / span);
         axis::Scratch partial;
         if (int s = partial.get(device, sizeof(float) * (size_t)nb * (size_t)channels)) return s;
-        if (vec)
-            relu_pool_backward_bias_kernel<4><<<nb, 256, 0, device->stream>>>(gradient, pooled, argmax, d_pre,
-                                                                            partial.as<float>(), span, a);
+        float *part = partial.as<float>();
+        if (vec && a.g_broadcast)
+            relu_pool_backward_bias_kernel<4, true><<<nb, 256, 0, device->stream>>>(gradient, pooled, argmax, d_pre,
+                                                                                  part, span, a);
+        else if (vec)
+            relu_pool_backward_bias_kernel<4, false><<<nb, 256, 0, device->stream>>>(gradient, pooled, argmax, d_pre,
+                                                                                   part, span, a);
+        else if (a.g_broadcast)
+            relu_pool_backward_bias_kernel<1, true><<<nb, 256, 0, device->stream>>>(gradient, pooled, argmax, d_pre,
+                                                                                  part, span, a);
         else
-            relu_pool_backward_bias_kernel<1><<<nb, 256, 0, device->stream>>>(gradient, pooled, argmax, d_pre,
-                                                                            partial.as<float>(), span, a);
+            relu_pool_backward_bias_kernel<1, false><<<nb, 256, 0, device->stream>>>(gradient, pooled, argmax, d_pre,
+                                                                                   part, span, a);
         if (int s = axis::launch_status("relu_pool_backward_bias_kernel")) return s;
         return axis::column_block_sum(device, partial, nb, channels, channels, channels, d_bias, nullptr);
     }
