@@ -258,6 +258,7 @@ int axis_upload(axis_device device, void *dst, const void *src, size_t bytes) {
     AXIS_ENTER(device);
     if (bytes == 0) return AXIS_OK;
     AXIS_REQUIRE(dst && src, "null upload pointer");
+    if (int st = axis_finish_before_read(device, dst, bytes)) return st;  // a pending sum writes there first
     AXIS_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, device->stream));
     // Pageable sources are staged by the runtime; wait so the caller may reuse `src` at once.
     AXIS_HIP(hipStreamSynchronize(device->stream));
@@ -279,6 +280,7 @@ int axis_copy(axis_device device, void *dst, const void *src, size_t bytes) {
     if (bytes == 0) return AXIS_OK;
     AXIS_REQUIRE(dst && src, "null copy pointer");
     if (int st = axis_finish_before_read(device, src, bytes)) return st;
+    if (int st = axis_finish_before_read(device, dst, bytes)) return st;
     AXIS_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, device->stream));
     return AXIS_OK;
 }
@@ -288,6 +290,7 @@ int axis_fill(axis_device device, float *out, float value, int64_t len) {
     AXIS_REQUIRE(len >= 0, "negative length");
     if (len == 0) return AXIS_OK;
     AXIS_REQUIRE(out, "null output");
+    if (int st = axis_finish_before_read(device, out, (size_t)len * sizeof(float))) return st;
     fill_kernel<<<axis::blocks_for(len, 256, 8192), 256, 0, device->stream>>>(out, value, len);
     return axis::launch_status("fill_kernel");
 }

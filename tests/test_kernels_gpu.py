@@ -1290,5 +1290,11 @@ def test_deferred_finishing_sums_flush_on_read_free_and_overflow(dev):
         assert _pending(dev) == 1
         del tmp                            # axis_free of a pending output
         assert _pending(dev) == 0
+        tmp = dev.empty(k * n)
+        dev.call("axis_matmul_right_backward", lhs.vp, g.vp, tmp.vp, *geo)
+        assert _pending(dev) == 1
+        dev.call("axis_fill", tmp.vp, F32(3.0), I64(k * n))   # a later write into it wins
+        assert _pending(dev) == 0
+        assert np.all(dev.read(tmp, k * n) == 3.0)
     finally:
         dev.call("axis_finish_defer", I32(0))
