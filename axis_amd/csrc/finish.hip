@@ -21,7 +21,8 @@ struct FinishBatch {
 };
 
 // 256 threads.  Kind 0 (split sums): as split_sum_kernel, 64 outputs per block, wave g adding the
-// slices of lane group g.  Kind 1 (column block sums): 16 columns per block, thread t summing row
+// slices of lane group g; kind 2 as split_sum4_kernel, 256 outputs per block.  Kind 1 (column
+// block sums): 16 columns per block, thread t summing row
 // range t / 16 of column t % 16 -- the ranges and their order of column_block_sum_kernel, whose
 // 16-wave blocks hold the long-lived, latency-bound blocks of short sums back in a shared launch.
 __global__ void __launch_bounds__(256) finish_batch_kernel(FinishBatch b) {
@@ -30,7 +31,17 @@ __global__ void __launch_bounds__(256) finish_batch_kernel(FinishBatch b) {
     int t = 0;
     while (t + 1 < b.count && local >= b.task[t].blocks) local -= b.task[t++].blocks;
     const axis::FinishTask &k = b.task[t];
-    if (k.kind == 0) {
+    if (k.kind == 2) {
+        __shared__ axis::finish_floatx4 acc[4][64];
+        const int lane = threadIdx.x & 63, group = threadIdx.x >> 6;
+        const int64_t i4 = ((int64_t)local * 64 + lane) * 4;
+        acc[group][lane] = axis::split_sum_part4(k.partial, i4, k.len, (int32_t)k.count, k.stride, group);
+        __syncthreads();
+        if (group == 0 && i4 < k.len) {
+            axis::split_sum_store4(k.out_a, i4, acc[0][lane], acc[1][lane], acc[2][lane], acc[3][lane], k.bias, k.n,
+                                   k.d, k.alpha, k.beta, k.perm_c, k.perm_taps);
+        }
+    } else if (k.kind == 0) {
         const int lane = threadIdx.x & 63, group = threadIdx.x >> 6;
         const int64_t i = (int64_t)local * 64 + lane;
         lds[group][lane] = axis::split_sum_part(k.partial, i, k.len, (int32_t)k.count, k.stride, group);
@@ -52,7 +63,7 @@ bool overlaps(const axis::FinishTask &t, const char *lo, const char *hi) {
         const char *a = reinterpret_cast<const char *>(out);
         return out && a < hi && lo < a + floats * (int64_t)sizeof(float);
     };
-    if (t.kind == 0) return hit(t.out_a, t.len);
+    if (t.kind != 1) return hit(t.out_a, t.len);
     const int64_t below = std::min(t.split, t.len);
     return hit(t.out_a, below) || hit(t.out_b, t.len - below);
 }
@@ -69,7 +80,7 @@ int flush_finish(axis_device device) {
     for (size_t i = 0; i < device->deferred.size(); ++i) {
         b.task[i] = device->deferred[i];
         blocks += b.task[i].blocks;
-        products = products || b.task[i].kind == 0;
+        products = products || b.task[i].kind != 1;
     }
     b.count = (int32_t)device->deferred.size();
     int status = AXIS_OK;

@@ -26,7 +26,7 @@ __device__ __forceinline__ float finish_value(const float *bias, const float *d,
 
 // One pending sum.  kind 0: out_a[i] = finish(sum over `count` slices partial[k * stride + i]) for
 // i < len (slice association of split_sum_part below), written at the permuted position when
-// perm_c is set.  kind 1: column e < len of partial[count][pitch = stride] summed over its rows
+// perm_c is set; kind 2: the same, four outputs per lane (split_sum_part4).  kind 1: column e < len of partial[count][pitch = stride] summed over its rows
 // (association of column_block_part below), to out_a[e] below `split`, else out_b[e - split].
 struct FinishTask {
     const float *partial;
@@ -42,7 +42,7 @@ struct FinishTask {
     float alpha, beta;
     int32_t perm_c, perm_taps;
     int32_t kind;
-    int32_t blocks;  // blocks of the batched launch: 64 outputs (kind 0) or 16 columns (kind 1) each
+    int32_t blocks;  // blocks of the batched launch: 64 outputs (kind 0), 16 columns (kind 1), 256 outputs (kind 2)
 };
 
 // Split sums: lane group g (of 4) adds slices g, g + 4, g + 8, ... in order; the four group sums
@@ -66,6 +66,29 @@ __device__ __forceinline__ float split_sum_part(const float *__restrict__ partia
     return s;
 }
 
+typedef float finish_floatx4 __attribute__((ext_vector_type(4)));
+
+// The same sums for four consecutive outputs i4 .. i4 + 3 per lane (len % 4 == 0 and 16-byte
+// aligned slices): one 16-byte load per slice, each output's adds in the same order.
+__device__ __forceinline__ finish_floatx4 split_sum_part4(const float *__restrict__ partial, int64_t i4, int64_t len,
+                                                          int32_t splits, int64_t split_stride, int group) {
+    constexpr int kAhead = 8;
+    finish_floatx4 s = {0.f, 0.f, 0.f, 0.f};
+    if (i4 < len)
+        for (int32_t k0 = group; k0 < splits; k0 += 4 * kAhead) {
+            finish_floatx4 v[kAhead];
+#pragma unroll
+            for (int u = 0; u < kAhead; ++u)
+                v[u] = k0 + 4 * u < splits
+                           ? *reinterpret_cast<const finish_floatx4 *>(partial + (int64_t)(k0 + 4 * u) * split_stride + i4)
+                           : finish_floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int u = 0; u < kAhead; ++u)
+                if (k0 + 4 * u < splits) s += v[u];
+        }
+    return s;
+}
+
 __device__ __forceinline__ void split_sum_store(float *__restrict__ out, int64_t i, float g0, float g1, float g2,
                                                 float g3, const float *__restrict__ bias, int64_t n,
                                                 const float *__restrict__ d, float alpha, float beta,
@@ -77,6 +100,26 @@ __device__ __forceinline__ void split_sum_store(float *__restrict__ out, int64_t
         at = ((row % perm_c) * perm_taps + row / perm_c) * n + col;
     }
     out[at] = finish_value(bias, d, alpha, beta, total, i, i % n);
+}
+
+// split_sum_store for outputs i4 .. i4 + 3 (group sums g0..g3 per output): one 16-byte store when
+// the outputs are not permuted.
+__device__ __forceinline__ void split_sum_store4(float *__restrict__ out, int64_t i4, finish_floatx4 g0,
+                                                 finish_floatx4 g1, finish_floatx4 g2, finish_floatx4 g3,
+                                                 const float *__restrict__ bias, int64_t n,
+                                                 const float *__restrict__ d, float alpha, float beta,
+                                                 int32_t perm_c, int32_t perm_taps) {
+    if (perm_c) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            split_sum_store(out, i4 + e, g0[e], g1[e], g2[e], g3[e], bias, n, d, alpha, beta, perm_c, perm_taps);
+        return;
+    }
+    finish_floatx4 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        v[e] = finish_value(bias, d, alpha, beta, ((g0[e] + g1[e]) + g2[e]) + g3[e], i4 + e, (i4 + e) % n);
+    *reinterpret_cast<finish_floatx4 *>(out + i4) = v;
 }
 
 // Column block sums: 16 consecutive row ranges of ceil(rows / 16) (range w = `wave`), each summed in

@@ -946,6 +946,25 @@ __global__ void __launch_bounds__(256) split_sum_kernel(const float *__restrict_
                               beta, perm_c, perm_taps);
 }
 
+// split_sum_kernel for len % 4 == 0 over 16-byte aligned slices: 256 outputs per block, four per
+// lane, the same association per output.
+__global__ void __launch_bounds__(256) split_sum4_kernel(const float *__restrict__ partial,
+                                                         float *__restrict__ out, int64_t len,
+                                                         int32_t splits, int64_t split_stride,
+                                                         const float *__restrict__ bias, int64_t n,
+                                                         const float *__restrict__ d, float alpha,
+                                                         float beta, int32_t perm_c, int32_t perm_taps) {
+    __shared__ axis::finish_floatx4 acc[4][64];
+    const int lane = threadIdx.x & 63, group = threadIdx.x >> 6;
+    const int64_t i4 = ((int64_t)blockIdx.x * 64 + lane) * 4;
+    acc[group][lane] = axis::split_sum_part4(partial, i4, len, splits, split_stride, group);
+    __syncthreads();
+    if (group == 0 && i4 < len) {
+        axis::split_sum_store4(out, i4, acc[0][lane], acc[1][lane], acc[2][lane], acc[3][lane], bias, n, d, alpha,
+                               beta, perm_c, perm_taps);
+    }
+}
+
 // First level for many slices: mid[g][i] = sum of slices [g*span, (g+1)*span) in order.
 __global__ void __launch_bounds__(256) split_range_kernel(const float *__restrict__ partial,
                                                           float *__restrict__ mid, int64_t len,
@@ -1159,6 +1178,8 @@ int sum_splits(axis_device device, const float *partial, float *out, int64_t len
     const unsigned blocks = axis::blocks_for(len, 64, INT32_MAX);
     const bool defer = owner && device->deferring && len <= (int64_t)INT32_MAX * 64 / 2;
     auto last_pass = [&](const float *slices, int64_t count, axis::Scratch &held) {
+        // four outputs per lane when every slice and the output start 16-byte aligned
+        const bool vec4 = len % 4 == 0 && axis::aligned16(slices) && axis::aligned16(out);
         if (defer) {
             axis::FinishTask t{};
             t.partial = slices;
@@ -1173,9 +1194,14 @@ int sum_splits(axis_device device, const float *partial, float *out, int64_t len
             t.beta = beta;
             t.perm_c = perm_c;
             t.perm_taps = perm_taps;
-            t.kind = 0;
-            t.blocks = (int32_t)((len + 63) / 64);
+            t.kind = vec4 ? 2 : 0;
+            t.blocks = (int32_t)(vec4 ? (len + 255) / 256 : (len + 63) / 64);
             return axis::defer_finish(device, t, held);
+        }
+        if (vec4) {
+            split_sum4_kernel<<<axis::blocks_for(len, 256, INT32_MAX), 256, 0, device->stream>>>(
+                slices, out, len, (int32_t)count, len, bias, n, d, alpha, beta, perm_c, perm_taps);
+            return axis::launch_status("split_sum4_kernel");
         }
         split_sum_kernel<<<blocks, 256, 0, device->stream>>>(slices, out, len, (int32_t)count, len, bias, n, d,
                                                              alpha, beta, perm_c, perm_taps);
