@@ -1298,3 +1298,21 @@ def test_deferred_finishing_sums_flush_on_read_free_and_overflow(dev):
         assert np.all(dev.read(tmp, k * n) == 3.0)
     finally:
         dev.call("axis_finish_defer", I32(0))
+
+
+@pytest.mark.parametrize("m,k,n", [(8192, 64, 48), (65536, 16, 20), (4096, 7, 9)])
+def test_split_sums_vector_and_scalar_forms_agree(dev, m, k, n):
+    # a split weight gradient into a 16-byte aligned output (four outputs per lane when k*n % 4 == 0)
+    # and into one 4 bytes off (one output per lane): the same bits
+    rng = np.random.default_rng(m + k + n)
+    lhs = up(dev, rng.standard_normal(m * k).astype(np.float32))
+    g = up(dev, rng.standard_normal(m * n).astype(np.float32))
+    geo = (I64(1), I64(m), I64(k), I64(n))
+    aligned, shifted = dev.empty(k * n), dev.empty(k * n + 1)
+    dev.call("axis_matmul_right_backward", lhs.vp, g.vp, aligned.vp, *geo)
+    dev.call("axis_matmul_right_backward", lhs.vp, g.vp, VP(shifted.ptr + 4), *geo)
+    a = dev.read(aligned, k * n)
+    b = dev.read(shifted, k * n + 1)[1:]
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    ref = np.asarray(dev.read(lhs, m * k), np.float64).reshape(m, k).T @ np.asarray(dev.read(g, m * n), np.float64).reshape(m, n)
+    assert rel_err(a, ref.reshape(-1)) < 1e-5

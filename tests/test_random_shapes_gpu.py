@@ -68,7 +68,8 @@ def _pool_shapes():
 PRODUCT_SHAPES = _product_shapes()
 CONV_SHAPES = _conv_shapes()
 POOL_SHAPES = _pool_shapes()
-BF16_SHAPES = PRODUCT_SHAPES[::4]
+# every kind of product shape: ragged below one tile, ragged multi-tile, split-depth, 64-wide halves
+BF16_SHAPES = PRODUCT_SHAPES[::4] + PRODUCT_SHAPES[1::8] + PRODUCT_SHAPES[2::8] + PRODUCT_SHAPES[3::8]
 
 
 @pytest.fixture(scope="module")
