@@ -1229,15 +1229,19 @@ int run_gemm_bf16(axis_device device, const GemmParams &p, int64_t batch, float 
     constexpr int64_t D = axis::kBf16Depth;
     const int64_t kp = (p.k + D - 1) / D * D;
     const int64_t xb = p.x_batch ? batch : 1, yb = p.y_batch ? batch : 1;
+    // A product of an operand with itself under the same layout (a Gram matrix, x . x^T) stages it once.
+    const bool same = p.x == p.y && p.x_batch == p.y_batch && p.x_si == p.y_sj && p.x_sr == p.y_sr && p.m == p.n;
     axis::Scratch sx, sy, partial;
     if (int st = sx.get(device, sizeof(uint16_t) * (size_t)(xb * p.m * kp))) return st;
-    if (int st = sy.get(device, sizeof(uint16_t) * (size_t)(yb * p.n * kp))) return st;
+    if (!same)
+        if (int st = sy.get(device, sizeof(uint16_t) * (size_t)(yb * p.n * kp))) return st;
     const double k_work = (double)(p.k_work > 0 ? p.k_work : p.k);
     axis::TimedLaunch timed(device, "gemm", 2.0 * (double)batch * (double)p.m * (double)p.n * k_work);
     if (int st = axis::stage_bf16(device, {p.x, p.x_batch, p.x_si, p.x_sr}, xb, p.m, p.k, kp, sx.as<uint16_t>()))
         return st;
-    if (int st = axis::stage_bf16(device, {p.y, p.y_batch, p.y_sj, p.y_sr}, yb, p.n, p.k, kp, sy.as<uint16_t>()))
-        return st;
+    if (!same)
+        if (int st = axis::stage_bf16(device, {p.y, p.y_batch, p.y_sj, p.y_sr}, yb, p.n, p.k, kp, sy.as<uint16_t>()))
+            return st;
     const axis::Bf16Tile tile = axis::bf16_gemm_tile(p.m, p.n, batch, kp, device->multiprocessors);
     const int64_t tiles = ((p.m + tile.rows - 1) / tile.rows) * ((p.n + tile.cols - 1) / tile.cols) * batch;
     const int64_t slots = device->multiprocessors * 2;
@@ -1253,7 +1257,7 @@ int run_gemm_bf16(axis_device device, const GemmParams &p, int64_t batch, float 
     splits = (kp + chunk - 1) / chunk;
     axis::Bf16Gemm g{};
     g.x = sx.as<uint16_t>();
-    g.y = sy.as<uint16_t>();
+    g.y = same ? sx.as<uint16_t>() : sy.as<uint16_t>();
     g.x_batch = p.x_batch ? p.m * kp : 0;
     g.y_batch = p.y_batch ? p.n * kp : 0;
     g.bias = p.bias;
