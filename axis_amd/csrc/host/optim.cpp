@@ -178,23 +178,56 @@ Muon::Prepared Muon::prepare(const std::vector<Selected> &parameters) const {
                   " has no gradient; run backward before step");
     }
     if (parameters.empty()) raise("Muon requires at least one selected rank-2 parameter");
+    // One contiguous layout shared by every operand: the elementwise steps run as one pass each
+    // (axis_muon_momentum / axis_muon_apply, the same roundings as the op sequence below).
+    auto plain = [](const Tensor &t, const Tensor &like) {
+        return t.shape() == like.shape() && t.layout() == Layout::contiguous(t.shape()) && t.value() &&
+               t.value()->floats() == t.shape().len && !t.requires_grad();
+    };
     for (auto &s : parameters) {
         Tensor gradient = *s.parameter.grad();
         const float observation_weight = 1.0f - momentum;
         auto prev = states.find(s.parameter.id());
-        Tensor next_momentum = prev != states.end()
-                                   ? prev->second.scale(momentum).add(gradient.scale(observation_weight))
-                                   : gradient.scale(observation_weight);
-        Tensor direction = nesterov ? gradient.scale(observation_weight).add(next_momentum.scale(momentum))
-                                    : next_momentum;
+        Tensor next_momentum, direction;
+        if (plain(gradient, gradient) && (prev == states.end() || plain(prev->second, gradient))) {
+            const Device &dev = gradient.device();
+            const int64_t len = gradient.shape().len;
+            Buffer next = dev.alloc(len);
+            Buffer dir = nesterov ? dev.alloc(len) : Buffer();
+            check(axis_muon_momentum(dev.h(), gradient.value()->f32(),
+                                     prev != states.end() ? prev->second.value()->f32() : nullptr, next->f32(),
+                                     dir ? dir->f32() : nullptr, momentum, nesterov ? 1 : 0, len),
+                  "muon_momentum");
+            next_momentum = Tensor::node(gradient.shape(), gradient.layout(), next, dev, {}, false);
+            direction = nesterov ? Tensor::node(gradient.shape(), gradient.layout(), dir, dev, {}, false)
+                                 : next_momentum;
+        } else {
+            next_momentum = prev != states.end()
+                                ? prev->second.scale(momentum).add(gradient.scale(observation_weight))
+                                : gradient.scale(observation_weight);
+            direction = nesterov ? gradient.scale(observation_weight).add(next_momentum.scale(momentum))
+                                 : next_momentum;
+        }
         Tensor orthogonal = zeroth_power(direction);
         Tensor p = s.parameter.tensor();
         const auto &dims = p.shape().dims;
         int64_t fan_in = s.orientation == MuonOrientation::FanInFanOut ? dims[0].extent : dims[1].extent;
         int64_t fan_out = s.orientation == MuonOrientation::FanInFanOut ? dims[1].extent : dims[0].extent;
         const float scaling = std::sqrt(std::max((float)fan_out / (float)fan_in, 1.0f));
-        Tensor decayed = p.detach().scale(1.0f - learning_rate * weight_decay);
-        Tensor updated = decayed.sub(orthogonal.scale(learning_rate * scaling));
+        const float decay = 1.0f - learning_rate * weight_decay;
+        const float rate = learning_rate * scaling;
+        Tensor updated;
+        Tensor held = p.detach();
+        if (plain(held, held) && plain(orthogonal, held)) {
+            const Device &dev = held.device();
+            Buffer out = dev.alloc(held.shape().len);
+            check(axis_muon_apply(dev.h(), held.value()->f32(), orthogonal.value()->f32(), out->f32(), decay, rate,
+                                  held.shape().len),
+                  "muon_apply");
+            updated = Tensor::node(held.shape(), held.layout(), out, dev, {}, false);
+        } else {
+            updated = held.scale(decay).sub(orthogonal.scale(rate));
+        }
         prepared.updates.push_back(Update{s.parameter, updated, next_momentum});
     }
     profile("muon_prepare", started);

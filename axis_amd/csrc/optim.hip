@@ -150,9 +150,100 @@ AdamHyper hyper(float lr, float b1, float b2, float c1, float c2, float eps, flo
     return h;
 }
 
+// Muon's elementwise steps (model/optim.rs:644-669), each operation rounded as the reference's
+// separate tensor ops round it (this file is built with -ffp-contract=off):
+//   next = prev * momentum + g * (1 - momentum)          (prev absent: g * (1 - momentum))
+//   direction = g * (1 - momentum) + next * momentum     (Nesterov; else next)
+//   updated = p * decay - orthogonal * rate
+template <bool PREV, bool NESTEROV>
+__global__ void __launch_bounds__(256) muon_momentum_kernel(const float *__restrict__ g,
+                                                            const float *__restrict__ prev, float *__restrict__ next,
+                                                            float *__restrict__ direction, float momentum,
+                                                            float observation, int64_t len) {
+    for (int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4; i < len; i += (int64_t)gridDim.x * 1024) {
+        if (i + 4 <= len) {
+            const floatx4 gv = *reinterpret_cast<const floatx4 *>(g + i);
+            floatx4 nv, dv;
+            floatx4 pv = PREV ? *reinterpret_cast<const floatx4 *>(prev + i) : floatx4{};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float t2 = gv[e] * observation;
+                nv[e] = PREV ? pv[e] * momentum + t2 : t2;
+                dv[e] = NESTEROV ? t2 + nv[e] * momentum : nv[e];
+            }
+            *reinterpret_cast<floatx4 *>(next + i) = nv;
+            if (NESTEROV) *reinterpret_cast<floatx4 *>(direction + i) = dv;
+        } else {
+            for (int64_t j = i; j < len; ++j) {
+                const float t2 = g[j] * observation;
+                const float n = PREV ? prev[j] * momentum + t2 : t2;
+                next[j] = n;
+                if (NESTEROV) direction[j] = t2 + n * momentum;
+            }
+        }
+    }
+}
+
+__global__ void __launch_bounds__(256) muon_apply_kernel(const float *__restrict__ p,
+                                                         const float *__restrict__ orthogonal,
+                                                         float *__restrict__ out, float decay, float rate,
+                                                         int64_t len) {
+    for (int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4; i < len; i += (int64_t)gridDim.x * 1024) {
+        if (i + 4 <= len) {
+            const floatx4 pv = *reinterpret_cast<const floatx4 *>(p + i);
+            const floatx4 ov = *reinterpret_cast<const floatx4 *>(orthogonal + i);
+            floatx4 r;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) r[e] = pv[e] * decay - ov[e] * rate;
+            *reinterpret_cast<floatx4 *>(out + i) = r;
+        } else {
+            for (int64_t j = i; j < len; ++j) out[j] = p[j] * decay - orthogonal[j] * rate;
+        }
+    }
+}
+
 }  // namespace
 
 extern "C" {
+
+int axis_muon_momentum(axis_device device, const float *gradient, const float *previous, float *next,
+                       float *direction, float momentum, int nesterov, int64_t len) {
+    AXIS_ENTER(device);
+    AXIS_REQUIRE(len >= 0, "negative length");
+    if (len == 0) return AXIS_OK;
+    AXIS_REQUIRE(gradient && next && (direction || !nesterov), "null Muon buffer");
+    AXIS_REQUIRE(axis::aligned16(gradient) && axis::aligned16(next) && (!previous || axis::aligned16(previous)) &&
+                     (!nesterov || axis::aligned16(direction)),
+                 "Muon buffers must be 16-byte aligned");
+    const float observation = 1.0f - momentum;
+    const unsigned blocks = axis::blocks_for((len + 3) / 4, 256, 8192);
+    if (previous && nesterov)
+        muon_momentum_kernel<true, true><<<blocks, 256, 0, device->stream>>>(gradient, previous, next, direction,
+                                                                            momentum, observation, len);
+    else if (previous)
+        muon_momentum_kernel<true, false><<<blocks, 256, 0, device->stream>>>(gradient, previous, next, direction,
+                                                                             momentum, observation, len);
+    else if (nesterov)
+        muon_momentum_kernel<false, true><<<blocks, 256, 0, device->stream>>>(gradient, previous, next, direction,
+                                                                             momentum, observation, len);
+    else
+        muon_momentum_kernel<false, false><<<blocks, 256, 0, device->stream>>>(gradient, previous, next,
+                                                                              direction, momentum, observation, len);
+    return axis::launch_status("muon_momentum_kernel");
+}
+
+int axis_muon_apply(axis_device device, const float *value, const float *orthogonal, float *out, float decay,
+                    float rate, int64_t len) {
+    AXIS_ENTER(device);
+    AXIS_REQUIRE(len >= 0, "negative length");
+    if (len == 0) return AXIS_OK;
+    AXIS_REQUIRE(value && orthogonal && out, "null Muon buffer");
+    AXIS_REQUIRE(axis::aligned16(value) && axis::aligned16(orthogonal) && axis::aligned16(out),
+                 "Muon buffers must be 16-byte aligned");
+    muon_apply_kernel<<<axis::blocks_for((len + 3) / 4, 256, 8192), 256, 0, device->stream>>>(value, orthogonal, out,
+                                                                                             decay, rate, len);
+    return axis::launch_status("muon_apply_kernel");
+}
 
 int axis_adam(axis_device device, const float *value, const float *gradient, const float *first,
               const float *second, const float *learning_rates, int64_t len, float learning_rate,

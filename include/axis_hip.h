@@ -269,6 +269,20 @@ int axis_adam_multi(axis_device device, const axis_adam_tensor *tensors, int32_t
                     float learning_rate, float beta1, float beta2, float correction1,
                     float correction2, float epsilon, float weight_decay);
 
+/* Muon::prepare's elementwise steps (model/optim.rs:644-657 and :666-669) in one pass each, every
+ * operation rounded as the reference's separate scale / add / sub tensor ops round it:
+ *   axis_muon_momentum: next = previous * momentum + gradient * (1 - momentum) (previous NULL on the
+ *     first step: gradient * (1 - momentum)); with nesterov != 0 also
+ *     direction = gradient * (1 - momentum) + next * momentum.
+ *   axis_muon_apply: out = value * decay - orthogonal * rate, with decay = 1 - lr * weight_decay and
+ *     rate = lr * scaling computed by the caller in fp32 as the reference does.
+ * All buffers hold `len` elements in the same layout, 16-byte aligned; outputs must not alias
+ * inputs. */
+int axis_muon_momentum(axis_device device, const float *gradient, const float *previous, float *next,
+                       float *direction, float momentum, int nesterov, int64_t len);
+int axis_muon_apply(axis_device device, const float *value, const float *orthogonal, float *out, float decay,
+                    float rate, int64_t len);
+
 /* Device::sum_squares (backend.rs:411-440): out[0] = sum of a^2 (out is a device scalar). */
 int axis_sum_squares(axis_device device, const float *a, int64_t len, float *out);
 /* Device::inverse_sqrt (backend.rs:630-635, kernel :2797-2801): 1 / sqrt(x + eps). */

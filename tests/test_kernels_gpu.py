@@ -1316,3 +1316,45 @@ def test_split_sums_vector_and_scalar_forms_agree(dev, m, k, n):
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
     ref = np.asarray(dev.read(lhs, m * k), np.float64).reshape(m, k).T @ np.asarray(dev.read(g, m * n), np.float64).reshape(m, n)
     assert rel_err(a, ref.reshape(-1)) < 1e-5
+
+
+@pytest.mark.parametrize("length", [4096 * 1000 + 3, 7, 1])
+def test_muon_elementwise_entries_equal_the_op_sequence(dev, length):
+    # model/optim.rs:644-669 as separate scale / add / sub launches against the fused passes: the
+    # same bits, with and without a previous momentum and with and without Nesterov
+    rng = np.random.default_rng(length)
+    g = up(dev, rng.standard_normal(length).astype(np.float32))
+    prev = up(dev, rng.standard_normal(length).astype(np.float32))
+    p = up(dev, rng.standard_normal(length).astype(np.float32))
+    o = up(dev, rng.standard_normal(length).astype(np.float32))
+    momentum, n = np.float32(0.95), I64(length)
+    observation = np.float32(1.0) - momentum
+
+    def seq_scale(src, f):
+        out = dev.empty(length)
+        dev.call("axis_scale", src.vp, F32(f), out.vp, n)
+        return out
+
+    def seq_binary(a, b, op):
+        out = dev.empty(length)
+        dev.call("axis_binary", a.vp, b.vp, I32(op), out.vp, n)
+        return out
+
+    read = lambda b: dev.read(b, length).view(np.uint32)
+    for has_prev in (True, False):
+        t2 = seq_scale(g, observation)
+        ref_next = seq_binary(seq_scale(prev, momentum), t2, 0) if has_prev else t2
+        ref_dir = seq_binary(seq_scale(g, observation), seq_scale(ref_next, momentum), 0)
+        for nesterov in (1, 0):
+            nxt, d = dev.empty(length), dev.empty(length)
+            dev.call("axis_muon_momentum", g.vp, prev.vp if has_prev else None, nxt.vp, d.vp if nesterov else None,
+                     F32(momentum), I32(nesterov), n)
+            assert np.array_equal(read(nxt), read(ref_next))
+            if nesterov:
+                assert np.array_equal(read(d), read(ref_dir))
+    lr, wd, scaling = np.float32(0.02), np.float32(0.01), np.float32(np.sqrt(2.0))
+    decay, rate = np.float32(1.0) - lr * wd, lr * scaling
+    ref = seq_binary(seq_scale(p, decay), seq_scale(o, rate), 1)
+    out = dev.empty(length)
+    dev.call("axis_muon_apply", p.vp, o.vp, out.vp, F32(decay), F32(rate), n)
+    assert np.array_equal(read(out), read(ref))
