@@ -448,6 +448,60 @@ __global__ void __launch_bounds__(kBlock) column_chunk_kernel(const float *__res
     }
 }
 
+// The same chunk sums for wide operands: 64 columns per block, so every row read (and masked
+// write) is one 256-byte segment per wave.  A chunk's 512 rows pass through LDS 128 at a time;
+// wave 0's lane per column keeps adding in row order across the passes, so each sum has the
+// association of column_chunk_kernel.
+constexpr int kWideCols = 64, kWideRows = 128;
+template <bool MASK>
+__global__ void __launch_bounds__(kBlock) column_chunk_wide_kernel(const float *__restrict__ g,
+                                                                   const float *__restrict__ relu_input,
+                                                                   float *__restrict__ masked_out,
+                                                                   float *__restrict__ partial, int64_t rows,
+                                                                   int64_t width, int64_t chunks,
+                                                                   float *__restrict__ out) {
+    static_assert(kBlock == 256 && kWideRows % 4 == 0, "four waves stage whole row groups");
+    constexpr int kPerLane = kWideRows / 4;
+    __shared__ float staged[kWideRows][kWideCols + 1];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t c = (int64_t)blockIdx.x * kWideCols + lane;
+    for (int64_t q = blockIdx.y; q < chunks; q += gridDim.y) {
+        const int64_t r0 = q * axis::kGroupedChunk;
+        const int n_rows = (int)(r0 + axis::kGroupedChunk < rows ? axis::kGroupedChunk : rows - r0);
+        float sum = 0.0f;
+        for (int base = 0; base < n_rows; base += kWideRows) {
+            float v[kPerLane];
+#pragma unroll
+            for (int u = 0; u < kPerLane; ++u) {
+                const int r = base + 4 * u + wave;
+                v[u] = 0.0f;
+                if (r < n_rows && c < width) {
+                    const int64_t idx = (r0 + r) * width + c;
+                    v[u] = g[idx];
+                    if (MASK) {
+                        v[u] = relu_input[idx] > 0.0f ? v[u] : 0.0f;
+                        masked_out[idx] = v[u];
+                    }
+                }
+            }
+            __syncthreads();  // the previous pass's sums have read the stage
+#pragma unroll
+            for (int u = 0; u < kPerLane; ++u) staged[4 * u + wave][lane] = v[u];
+            __syncthreads();
+            if (wave == 0 && c < width) {
+                const int lim = n_rows - base < kWideRows ? n_rows - base : kWideRows;
+                for (int r = 0; r < lim; ++r) sum = sum + staged[r][lane];
+            }
+        }
+        if (wave == 0 && c < width) {
+            if (out)
+                out[c] = 0.0f + sum;
+            else
+                partial[q * width + c] = sum;
+        }
+    }
+}
+
 // out[o][i] = factor * sum_r a[o][r][i] in the reference's chunked order.
 __global__ void __launch_bounds__(kBlock) reduce_middle_kernel(const float *__restrict__ a,
                                                                float *__restrict__ out, int64_t outer,
@@ -804,14 +858,25 @@ int axis_bias_gradient(axis_device device, const float *gradient, const float *r
     if (chunks > 1)
         if (int s = partial.get(device, sizeof(float) * (size_t)pairs)) return s;
     float *direct = chunks == 1 ? out : nullptr;
-    const dim3 grid((unsigned)((width + kChunkCols - 1) / kChunkCols), (unsigned)std::min<int64_t>(chunks, 65535));
-    if (relu_input)
-        column_chunk_kernel<true><<<grid, kBlock, 0, device->stream>>>(
-            gradient, relu_input, masked_out, partial.as<float>(), rows, width, chunks, direct);
-    else
-        column_chunk_kernel<false><<<grid, kBlock, 0, device->stream>>>(
-            gradient, nullptr, nullptr, partial.as<float>(), rows, width, chunks, direct);
-    if (int s = axis::launch_status("column_chunk_kernel")) return s;
+    if (width >= 2048) {  // enough 64-column blocks to fill the chip
+        const dim3 grid((unsigned)((width + kWideCols - 1) / kWideCols), (unsigned)std::min<int64_t>(chunks, 65535));
+        if (relu_input)
+            column_chunk_wide_kernel<true><<<grid, kBlock, 0, device->stream>>>(
+                gradient, relu_input, masked_out, partial.as<float>(), rows, width, chunks, direct);
+        else
+            column_chunk_wide_kernel<false><<<grid, kBlock, 0, device->stream>>>(
+                gradient, nullptr, nullptr, partial.as<float>(), rows, width, chunks, direct);
+        if (int s = axis::launch_status("column_chunk_wide_kernel")) return s;
+    } else {
+        const dim3 grid((unsigned)((width + kChunkCols - 1) / kChunkCols), (unsigned)std::min<int64_t>(chunks, 65535));
+        if (relu_input)
+            column_chunk_kernel<true><<<grid, kBlock, 0, device->stream>>>(
+                gradient, relu_input, masked_out, partial.as<float>(), rows, width, chunks, direct);
+        else
+            column_chunk_kernel<false><<<grid, kBlock, 0, device->stream>>>(
+                gradient, nullptr, nullptr, partial.as<float>(), rows, width, chunks, direct);
+        if (int s = axis::launch_status("column_chunk_kernel")) return s;
+    }
     if (chunks == 1) return AXIS_OK;
     axis::column_combine_kernel<<<(unsigned)width, 256, 0, device->stream>>>(partial.as<float>(), chunks,
                                                                            width, 1.0f, out);

@@ -402,7 +402,10 @@ def test_adam_multi_many_tensors(dev, oracle):
 
 # ---------------------------------------------------------------- fused entries
 
-@pytest.mark.parametrize("rows,width", [(1, 1), (600, 2), (1030, 64), (777, 130)])
+# the last three take the 64-column kernel (widths from 2048): ragged columns over three chunks,
+# one chunk written directly, config 5's [4096, 8192] layer
+@pytest.mark.parametrize("rows,width", [(1, 1), (600, 2), (1030, 64), (777, 130), (1300, 2100), (300, 4096),
+                                        (4096, 8192)])
 def test_bias_entries_bit_exact(dev, oracle, rows, width):
     rng = np.random.default_rng(rows)
     a = rng.standard_normal(rows * width).astype(np.float32)
