@@ -537,6 +537,33 @@ def test_cnn_small_batch_step_matches_oracle(ax, device, oracle):
                               ref["params"][theirs])
 
 
+def test_cnn_small_batch_step_on_bf16_device_near_fp32_oracle(ax, oracle):
+    # The CNN step on a Device.hip_bf16 handle (backend.rs:274-283: every convolution and matrix
+    # product rounds its operands to bf16): the implicit-GEMM conv1 path, the deferred bias sums and
+    # the bf16 dense products together, held to bf16 operand precision of the fp32 oracle step
+    # (measured: gradients 0.6-2.0% of each tensor's max away, loss 1.5e-5 relative)
+    device = ax.Device.hip_bf16(0)
+    batch, size, classes, ch = 8, 32, 1000, (3, 64, 128, 256)
+    ref = oracle.cnn_step(batch, size, classes, 1e-3, ch)
+    model, features, head, bt, c0, h, w, cls = build_cnn(ax, device, batch, size, classes, ch)
+    mapping = {}
+    for j in range(3):
+        mapping[f"0.{3 * j}.weight"] = f"conv{j}.weight"
+        mapping[f"0.{3 * j}.bias"] = f"conv{j}.bias"
+    mapping["1.weight"], mapping["1.bias"] = "linear.weight", "linear.bias"
+    for ours, theirs in mapping.items():
+        model.parameter(ours).set_values(ref["initial"][theirs])
+    x = ax.Tensor.from_slice(ref["x"], [bt.of(batch), c0.of(3), h.of(size), w.of(size)], device)
+    y = ax.Tensor.from_slice(ref["y"], [bt.of(batch), cls.of(classes)], device)
+    loss = head.forward(features.forward(x).mean([h, w])).categorical_cross_entropy_with_logits(y, cls).mean([bt])
+    loss.backward()
+    assert abs(loss.item() - ref["loss"]) <= 1e-2 * max(1, abs(ref["loss"]))
+    for ours, theirs in mapping.items():
+        g = model.parameter(ours).grad().to_vec()
+        assert np.all(np.isfinite(g)), theirs
+        assert rel_max(g, ref["grads"][theirs]) < 5e-2, (theirs, rel_max(g, ref["grads"][theirs]))
+
+
 def test_cnn_fused_mean_backwards_match_materialised_broadcasts(ax, device):
     # The CNN step takes three fused backward paths that each fold a launch away: the loss's
     # mean over the batch into the cross-entropy backward (with the classifier's bias gradient), and
