@@ -1878,6 +1878,20 @@ int axis_conv2d_backward_data(axis_device device, const float *gradient, const f
                   s.kh - 1 - s.py, s.kw - 1 - s.px);
     const bool buffered = buffer_reach(p.conv, batch);
     const bool block = use_block_major(p.conv, batch);
+    if (out_channels % 32 == 0 && axis::aligned16(weight)) {
+        // The flipped, transposed kernel read in place: Y(r, c) with r = (ky', kx', n) is
+        // W[c * taps * n_out + (taps - 1 - (ky' * kw + kx')) * n_out + n], so a K step (32
+        // consecutive n of one tap, in either row order) is 128 contiguous bytes of each
+        // column c, at tap offset (taps - 1) * n_out - pos * n_out.  Same values in the same
+        // reduction order as the permuted copy below, so the same bits.
+        p.y = weight;
+        p.y_sr = 1;
+        p.y_sj = taps * out_channels;
+        p.ytaps = TapSteps{true, FastDiv((uint32_t)out_channels), 1, -(int64_t)out_channels,
+                           (taps - 1) * out_channels, block, FastDiv((uint32_t)taps)};
+        return buffered ? run_gemm<true, true, 4, 0>(device, p, 1, d_input)
+                        : run_gemm<true, true, 1, 0>(device, p, 1, d_input);
+    }
     axis::Scratch flipped;
     if (int st = flipped.get(device, sizeof(float) * (size_t)(taps * channels * out_channels))) return st;
     if (int st = permute_weight(device, weight, flipped.as<float>(), s, 1, channels, block)) return st;
