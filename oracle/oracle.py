@@ -822,7 +822,9 @@ def cnn_forward_backward(x, y, params, batch=256, size=64, classes=1000, channel
     accumulate in different orders can break a near-tie (two window values, or a pre-activation
     and zero, within rounding) differently, which moves a whole gradient term; replaying one set
     of decisions leaves the arithmetic as the only difference.  `return_decisions` also returns
-    this forward's own decisions in that form (argmax 255 where a window has no finite value)."""
+    this forward's own decisions in that form (argmax 255 where a window has no finite value),
+    each pair extended by how clearly it was decided: the window's best ReLU output minus its
+    runner-up, and its best pre-activation."""
     dims = [("batch", batch), ("channel", channels[0]), ("height", size), ("width", size)]
     strides = contiguous(dims)
     h = x
@@ -854,7 +856,12 @@ def cnn_forward_backward(x, y, params, batch=256, size=64, classes=1000, channel
         if return_decisions:
             won = mask.reshape(cout, batch, hh // 2, ww // 2, 4)
             own = np.where(won.any(-1), won.argmax(-1), 255).astype(np.uint8).transpose(1, 2, 3, 0)
-            made.append((np.ascontiguousarray(own), h.copy()))
+            # how clearly each window was decided: its best ReLU output minus the runner-up, and
+            # its best pre-activation (the ReLU sign at the winner), both [batch, oh, ow, channel]
+            windows = np.sort(q.reshape(cout, batch, hh // 2, ww // 2, 4), axis=-1)
+            gap = (windows[..., 3] - windows[..., 2]).transpose(1, 2, 3, 0)
+            zmax = zb.reshape(batch, hh // 2, 2, ww // 2, 2, cout).max(axis=(2, 4))
+            made.append((np.ascontiguousarray(own), h.reshape(own.shape).copy(), np.ascontiguousarray(gap), zmax))
         if decisions is not None:
             mask, relu_sign = _decision_masks(decisions[j][0], decisions[j][1], batch, hh, ww, cout)
         saved.append(dict(conv=conv, patches=patches, zb=relu_sign, m=m, pool=pool, mask=mask,

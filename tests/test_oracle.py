@@ -558,9 +558,62 @@ def test_cnn_decision_replay_is_exact_and_used(oracle):
     assert loss2 == loss
     for name in grads:
         assert np.array_equal(grads[name], grads2[name]), name
-    moved = [(a.copy(), p.copy()) for a, p in made]
+    # the decision margins: winners sit where the window's best value is, the gap is that best
+    # minus the runner-up, and the ReLU sign at the winner is the sign of the best pre-activation
+    for a, p, gap, zmax in made:
+        assert gap.shape == a.shape == zmax.shape and np.all(gap >= 0)
+        assert np.array_equal(p > 0, zmax > 0)
+        assert np.array_equal(p[p > 0], zmax[p > 0])
+    moved = [(a.copy(), p.copy()) for a, p, *_ in made]
     pos = np.argwhere(moved[2][1] > 0)[0]
     moved[2][0][tuple(pos)] = (moved[2][0][tuple(pos)] + 1) % 4
     _, grads3 = oracle.cnn_forward_backward(x, y, params, batch, size, classes, ch, decisions=moved)
     assert not np.array_equal(grads3["conv2.weight"], grads["conv2.weight"])
     assert np.array_equal(grads3["linear.weight"], grads["linear.weight"])
+
+
+def test_block_decision_check_accepts_own_and_catches_moved_winner(oracle):
+    # the config-4 decision check (tests/test_configs_gpu.check_block_decisions) passes a forward's
+    # own decisions and fails when one clearly decided winner moves or a clear ReLU sign flips
+    from tests.test_configs_gpu import check_block_decisions
+    batch, size, classes, ch = 4, 16, 10, (3, 8, 16, 32)
+    x, y, params = oracle.cnn_inputs(batch, size, classes, ch)
+    _, _, own = oracle.cnn_forward_backward(x, y, params, batch, size, classes, ch, return_decisions=True)
+    made = [(a.reshape(-1).copy(), p.reshape(-1).copy()) for a, p, *_ in own]
+    counts = check_block_decisions(made, own)
+    assert [c[2:] for c in counts] == [(0, 0)] * 3 and all(c[1] > 0.9 * c[0] for c in counts)
+    a, p, gap, z = own[1]
+    tol = 1e-4 * np.abs(z).max()
+    idx = tuple(np.argwhere((z > tol) & (gap > tol))[0])
+    moved = [(m[0].copy(), m[1].copy()) for m in made]
+    moved[1][0].reshape(a.shape)[idx] = (a[idx] + 1) % 4
+    with pytest.raises(AssertionError):
+        check_block_decisions(moved, own)
+    flipped = [(m[0].copy(), m[1].copy()) for m in made]
+    flipped[2][1].reshape(own[2][0].shape)[tuple(np.argwhere(own[2][3] > 1e-4 * np.abs(own[2][3]).max())[0])] = 0.0
+    with pytest.raises(AssertionError):
+        check_block_decisions(flipped, own)
+
+
+def test_first_adam_step_bound_is_exact(oracle):
+    # the whole-step parameter check (tests/test_host_gpu.check_first_adam_step) accepts an update
+    # whose gradient differs from the oracle's, element by element, by what lr * |u(g) - u(g_ref)|
+    # allows (u(x) = x / (|x| + eps)), and rejects a parameter moved past it
+    from tests.test_host_gpu import check_first_adam_step
+    rng = np.random.default_rng(3)
+    p0 = (rng.standard_normal(4096) * 0.05).astype(np.float32)
+    g_ref = (rng.standard_normal(4096) * 1e-3).astype(np.float32)
+    g = g_ref.copy()
+    g[:8] = -g[:8]                                   # sign flips: moves of ~2 lr are allowed there
+    g[8:16] = (g[8:16] * np.float32(1.0 + 1e-6)).astype(np.float32)
+    g_ref[100] = g[100] = np.float32(3e-6)           # too small a gradient for the 1%-agreement subset
+    c1, c2 = 1 - oracle.powi(0.9, 1), 1 - oracle.powi(0.999, 1)
+    zero = np.zeros_like(p0)
+    p_ref = oracle.adam(p0, g_ref, zero, zero, 1e-3, 0.9, 0.999, c1, c2, 1e-8, 0.0)[0]
+    v = oracle.adam(p0, g, zero, zero, 1e-3, 0.9, 0.999, c1, c2, 1e-8, 0.0)[0]
+    outside, miss = check_first_adam_step(oracle, "w", v, g, p0, g_ref, p_ref)
+    assert miss == 8 / 4096
+    bad = p_ref.copy()
+    bad[100] += np.float32(1e-4)                       # well inside 2 lr, but its gradients agree exactly
+    with pytest.raises(AssertionError):
+        check_first_adam_step(oracle, "w", v, g, p0, g_ref, bad)
