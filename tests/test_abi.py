@@ -2,6 +2,7 @@
 include/axis_hip.h declares (no compute call: there is no GPU here)."""
 import ctypes
 import os
+import re
 import subprocess
 
 import pytest
@@ -26,12 +27,96 @@ def test_library_exports_every_declared_symbol():
     assert b"gfx950" in lib.axis_version()
 
 
-def test_integration_binding_covers_every_entry():
-    # the reference-side Rust extern block must bind every entry point the header declares
-    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-    text = open(os.path.join(root, "INTEGRATION.md")).read()
-    missing = [name for name in hip.header_functions() if f"pub fn {name}(" not in text]
-    assert not missing, missing
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+RUST_SYS = os.path.join(ROOT, "ffi", "axis-hip-sys", "src", "lib.rs")
+_C_BASE = {"int": "c_int", "int32_t": "i32", "int64_t": "i64", "uint8_t": "u8", "float": "f32",
+           "double": "f64", "size_t": "usize", "char": "c_char", "void": "c_void",
+           "axis_device": "axis_device", "axis_plan": "axis_plan", "axis_unfold_spec": "axis_unfold_spec",
+           "axis_adam_tensor": "axis_adam_tensor"}
+
+
+def _c_type(decl):
+    """A C parameter or field declaration (name included) as the Rust type that binds it:
+    `const T *x` -> `*const T`, `T *x` / `T x[n]` (a parameter) -> `*mut T` / `*const T`."""
+    decl = " ".join(decl.split())
+    array = re.search(r"\[\d*\]$", decl)
+    decl = re.sub(r"\s*\[\d*\]$", "", decl)
+    m = re.fullmatch(r"(const )?(\w+)\s*(\**)\s*\w+", decl)
+    assert m, decl
+    const, base, stars = m.group(1), _C_BASE[m.group(2)], len(m.group(3)) + (1 if array else 0)
+    if stars == 0:
+        return base
+    inner = ("*const " if const else "*mut ") + base
+    return "*mut " * (stars - 1) + inner
+
+
+def _strip_c(text):
+    return re.sub(r"//[^\n]*", "", re.sub(r"/\*.*?\*/", "", text, flags=re.S))
+
+
+def c_prototypes():
+    text = _strip_c(open(hip.HEADER).read())
+    out = {}
+    for ret, name, params in re.findall(r"(int|const char \*)\s*(axis_\w+)\s*\(([^)]*)\)\s*;", text, re.S):
+        args = [] if params.strip() == "void" else [_c_type(p) for p in params.split(",")]
+        out[name] = ("c_int" if ret == "int" else "*const c_char", args)
+    return out
+
+
+def c_structs():
+    text = _strip_c(open(hip.HEADER).read())
+    out = {}
+    for body, name in re.findall(r"typedef struct \{(.*?)\}\s*(\w+)\s*;", text, re.S):
+        fields = []
+        for decl in body.split(";"):
+            decl = " ".join(decl.split())
+            if not decl:
+                continue
+            array = re.search(r"\[(\d+)\]$", decl)
+            if array:   # a struct member array is a value, not a pointer
+                base = _c_type(re.sub(r"\s*\[\d+\]$", "", decl))
+                fields.append(f"[{base}; {array.group(1)}]")
+            else:
+                fields.append(_c_type(decl))
+        out[name] = fields
+    return out
+
+
+def rust_declarations():
+    text = re.sub(r"//[^\n]*", "", open(RUST_SYS).read())
+    fns = {}
+    for name, params, ret in re.findall(r"pub fn (axis_\w+)\(([^)]*)\)\s*->\s*([^;]+);", text, re.S):
+        args = [" ".join(p.split(":", 1)[1].split()) for p in params.split(",") if p.strip()]
+        fns[name] = (" ".join(ret.split()), args)
+    structs = {}
+    for name, body in re.findall(r"#\[repr\(C\)\]\s*pub struct (\w+)\s*\{([^{}]*)\}", text):
+        if name.endswith("_s"):   # the opaque handle types
+            continue
+        structs[name] = [" ".join(f.split(":", 1)[1].split()) for f in body.split(",") if ":" in f]
+    return fns, structs
+
+
+def test_rust_sys_crate_matches_the_header_argument_by_argument():
+    # ffi/axis-hip-sys binds every prototype of include/axis_hip.h with the same argument count,
+    # order and types, the same return type, and the same struct layouts, and nothing else
+    c_fns, c_st = c_prototypes(), c_structs()
+    rust_fns, rust_st = rust_declarations()
+    assert sorted(c_fns) == hip.header_functions()
+    assert sorted(rust_fns) == sorted(c_fns), set(rust_fns) ^ set(c_fns)
+    for name, (ret, args) in c_fns.items():
+        assert rust_fns[name] == (ret, args), (name, rust_fns[name], (ret, args))
+    assert rust_st == c_st, (rust_st, c_st)
+
+
+def test_signature_parsers_catch_a_swapped_argument():
+    # the comparison above is sensitive: swapping two differently typed arguments, dropping const
+    # or changing an integer width in the Rust text all change the parsed signature
+    fns, _ = rust_declarations()
+    ret, args = fns["axis_adam"]
+    assert args[1] == "*const f32" and args[6] == "i64" and args[7] == "f32"
+    assert _c_type("const float *a") == "*const f32" and _c_type("float *a") == "*mut f32"
+    assert _c_type("void **stream") == "*mut *mut c_void" and _c_type("const int32_t kernel[2]") == "*const i32"
+    assert _c_type("int64_t len") == "i64" and _c_type("int n") == "c_int"
 
 
 def test_library_is_built_for_gfx950_only(tmp_path):
