@@ -38,14 +38,18 @@ struct axis_device_s {
     };
     std::map<std::string, std::vector<Timed>> timed;
     std::vector<hipEvent_t> spare_events;
-    // This GPU's copy of the allocation-free product's scratch array (gemm.hip), bound at create.
+    // This GPU's copy of the allocation-free product's scratch array (gemm.hip), bound at create,
+    // and the event that orders its users: every handle on this GPU shares both, so each call
+    // waits for the previous call's last launch (from any handle) before reusing the array.
     float *static_scratch = nullptr;
+    hipEvent_t static_scratch_done = nullptr;
     // Deferred finishing sums (axis_finish_defer): while on, the last sum of a weight or bias
     // gradient is recorded here instead of launched, and the scratch block it reads is held, until
     // one batched launch (axis_finish_flush) runs every recorded sum.
     bool deferring = false;
     std::vector<axis::FinishTask> deferred;
     std::vector<void *> deferred_blocks;
+    size_t deferred_bytes = 0;  // held by deferred_blocks; a batch is launched past kMaxDeferredBytes
 };
 
 struct axis_plan_s {

@@ -14,6 +14,10 @@
 namespace {
 
 constexpr int kMaxFinish = 24;  // tasks per launch (the batch travels as a kernel argument)
+// Scratch a batch may hold before it is launched: each deferred sum keeps its partial block (up to
+// 64 MiB of split slices) until the batch runs, so a deep, wide backward would otherwise hold
+// every layer's partials at once.
+constexpr size_t kMaxDeferredBytes = size_t(256) << 20;
 
 struct FinishBatch {
     axis::FinishTask task[kMaxFinish];
@@ -94,6 +98,7 @@ int flush_finish(axis_device device) {
     for (void *p : device->deferred_blocks) release(device, p);
     device->deferred.clear();
     device->deferred_blocks.clear();
+    device->deferred_bytes = 0;
     return status;
 }
 
@@ -105,7 +110,12 @@ int defer_finish(axis_device device, const FinishTask &task, Scratch &held) {
     if (device->deferred.size() == (size_t)kMaxFinish || blocks > (int64_t)INT32_MAX / 2)
         if (int st = flush_finish(device)) return st;
     device->deferred.push_back(task);
-    if (held.ptr) device->deferred_blocks.push_back(held.take());
+    if (held.ptr) {
+        auto it = device->live.find(held.ptr);
+        device->deferred_bytes += it == device->live.end() ? 0 : it->second;
+        device->deferred_blocks.push_back(held.take());
+    }
+    if (device->deferred_bytes > kMaxDeferredBytes) return flush_finish(device);
     return AXIS_OK;
 }
 

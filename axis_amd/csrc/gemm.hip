@@ -1622,19 +1622,28 @@ struct GatherInput {
 namespace axis {
 
 // The device address of this GPU's copy of `scratch`, looked up once per GPU with that GPU
-// current (axis_device_create makes it current before calling this).
+// current (axis_device_create makes it current before calling this), and one event per GPU that
+// serialises the array's users across handles (created once, like the array never released).
 int bind_static_scratch(axis_device device) {
     static std::mutex guard;
-    static std::unordered_map<int, float *> bound;
+    struct Bound {
+        float *address;
+        hipEvent_t done;
+    };
+    static std::unordered_map<int, Bound> bound;
     std::lock_guard<std::mutex> lock(guard);
     auto it = bound.find(device->ordinal);
     if (it == bound.end()) {
         void *address = nullptr;
         hipError_t e = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
         if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
-        it = bound.emplace(device->ordinal, static_cast<float *>(address)).first;
+        hipEvent_t done = nullptr;
+        e = hipEventCreateWithFlags(&done, hipEventDisableTiming);
+        if (e != hipSuccess) return hip_fail(e, "hipEventCreateWithFlags(scratch)");
+        it = bound.emplace(device->ordinal, Bound{static_cast<float *>(address), done}).first;
     }
-    device->static_scratch = it->second;
+    device->static_scratch = it->second.address;
+    device->static_scratch_done = it->second.done;
     return AXIS_OK;
 }
 
@@ -1766,7 +1775,17 @@ int axis_matmul_right_backward_noalloc(axis_device device, const float *lhs, con
     p.x_batch = m * k;
     p.y_batch = m * n;
     const Workspace ws{device->static_scratch, kStaticScratchFloats};
-    return run_gemm<false, false, 0, 0>(device, p, batch, out, &ws);
+    // Another handle on this GPU may still be running a call that uses the array: wait for its
+    // last launch (a never-recorded event is complete), and mark this call's for the next user.
+    // Under stream capture the graph's own order stands in (an event recorded outside the
+    // capture is not a node the graph can wait on).
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    AXIS_HIP(hipStreamIsCapturing(device->stream, &capture));
+    const bool order = capture == hipStreamCaptureStatusNone;
+    if (order) AXIS_HIP(hipStreamWaitEvent(device->stream, device->static_scratch_done, 0));
+    if (int st = run_gemm<false, false, 0, 0>(device, p, batch, out, &ws)) return st;
+    if (order) AXIS_HIP(hipEventRecord(device->static_scratch_done, device->stream));
+    return AXIS_OK;
 }
 
 int axis_conv2d_forward(axis_device device, const float *input, const int64_t input_strides_[4],

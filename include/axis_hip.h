@@ -134,9 +134,11 @@ int axis_matmul_right_backward(axis_device device, const float *lhs, const float
  * device array (one per GPU, held until the process ends) instead of the caching allocator; it
  * calls no allocator.  Nothing in the array needs to start at zero.  A product whose partial
  * sums exceed 64 MiB is rejected before any launch (on MI355X's 256 CUs the split rule never
- * needs more than about 53 MB); bf16 handles are rejected.  Calls on one GPU share the array:
- * calls from different handles (streams) on the same GPU that overlap in time race, while calls
- * on one handle are ordered by its stream. */
+ * needs more than about 53 MB); bf16 handles are rejected.  Calls on one GPU share the array and
+ * one event per GPU: each call's launches wait for the previous call's (from any handle on that
+ * GPU) and it records its own, so calls from different handles run one after the other instead of
+ * racing.  Calls from different host threads at the same moment must be serialised by the caller
+ * (the wait and record pair is not atomic across threads). */
 int axis_matmul_right_backward_noalloc(axis_device device, const float *lhs, const float *gradient,
                                        float *out, int64_t batch, int64_t m, int64_t k, int64_t n);
 

@@ -1,7 +1,9 @@
 """axis_matmul_right_backward_noalloc: the weight-gradient product with its split partial sums in a
 static device array.  Checked bit for bit against axis_matmul_right_backward (same kernels, same
 split rule) on consecutive calls -- larger, then smaller, then one with more than 32 slices
-(range sums) -- and the caching allocator's counters show the calls allocated nothing."""
+(range sums) -- and the caching allocator's counters show the calls allocated nothing; calls from
+two handles on the one GPU, enqueued back to back with no host wait, are ordered by the array's
+event and each gives its own product's bits."""
 import ctypes
 
 import numpy as np
@@ -25,7 +27,8 @@ def stats(dev):
 
 
 def test_noalloc_matches_allocating_entry_on_consecutive_calls(dev):
-    # (m, k, n): 13 slices, then a smaller product, then 1280 slices (range sums), then unsplit
+    # (m, k, n): 13 slices, then a smaller product, then 64 slices (the dense schedule's cap; more
+    # than 32, so two range sums), then unsplit
     shapes = [(8192, 784, 1024), (2048, 300, 200), (262144, 64, 64), (100, 70, 50)]
     for m, k, n in shapes:
         print(f"noalloc case m={m} k={k} n={n}", flush=True)
@@ -66,3 +69,26 @@ def test_noalloc_rejects_bf16_handles_and_bad_arguments(dev):
     b2 = bf.empty(64)
     with pytest.raises(hip.AxisError, match="fp32 only"):
         bf.call("axis_matmul_right_backward_noalloc", b2.vp, b2.vp, b2.vp, I64(1), I64(4), I64(4), I64(4))
+
+
+def test_noalloc_calls_from_two_handles_are_ordered(dev):
+    # two handles (two streams) on one GPU share the array: a large product on the first handle,
+    # then a different product on the second with no host wait between; each must equal its
+    # allocating entry's result
+    other = hip.Device(0)
+    cases = [(dev, (65536, 576, 128), 1), (other, (16384, 1152, 256), 2), (dev, (8192, 784, 1024), 3)]
+    made = []
+    for d, (m, k, n), seed in cases:
+        rng = np.random.default_rng(seed)
+        lhs = d.upload(rng.standard_normal(m * k).astype(np.float32))
+        grad = d.upload(rng.standard_normal(m * n).astype(np.float32))
+        want, got = d.empty(k * n), d.empty(k * n)
+        d.call("axis_matmul_right_backward", lhs.vp, grad.vp, want.vp, I64(1), I64(m), I64(k), I64(n))
+        d.synchronize()
+        made.append((d, lhs, grad, want, got, (m, k, n)))
+    print("noalloc two handles: enqueue without waits", flush=True)
+    for d, lhs, grad, want, got, (m, k, n) in made:
+        d.call("axis_matmul_right_backward_noalloc", lhs.vp, grad.vp, got.vp, I64(1), I64(m), I64(k), I64(n))
+    for d, lhs, grad, want, got, (m, k, n) in made:
+        w, g = d.read(want, k * n), d.read(got, k * n)
+        assert np.array_equal(w.view(np.uint32), g.view(np.uint32)), (m, k, n)
