@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <initializer_list>
 #include <map>
 #include <vector>
 #include <string>
@@ -104,6 +105,21 @@ int defer_finish(axis_device device, const FinishTask &task, Scratch &held);
 // Launches every recorded sum in one kernel and returns their blocks to the allocator.
 int flush_finish(axis_device device);
 
+// A buffer an entry reads or writes: its first byte and extent (1 when the entry reads it through
+// strides, so only a pending output that holds its first byte is seen).
+struct Span {
+    const void *ptr;
+    int64_t bytes;
+};
+// Launches the recorded sums when one of them writes into a span (finish.hip).
+int finish_overlapping(axis_device device, std::initializer_list<Span> spans);
+// Every kernel entry passes its buffers here before it launches: a pending finishing sum that
+// writes one of them runs first, so no entry reads (or overwrites) a gradient whose last sum is
+// still deferred.  Free when nothing is pending.
+inline int guard(axis_device device, std::initializer_list<Span> spans) {
+    return device->deferred.empty() ? AXIS_OK : finish_overlapping(device, spans);
+}
+
 inline unsigned blocks_for(int64_t work, int per_block, int64_t cap = 1 << 20) {
     int64_t b = (work + per_block - 1) / per_block;
     if (b < 1) b = 1;
@@ -135,6 +151,11 @@ inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 
 #define AXIS_REQUIRE(cond, msg)                                         \
     do {                                                                \
         if (!(cond)) return axis::fail(AXIS_ERROR_INVALID, (msg));     \
+    } while (0)
+
+#define AXIS_GUARD(dev, ...)                                                   \
+    do {                                                                       \
+        if (int axis_guard_status = axis::guard((dev), {__VA_ARGS__})) return axis_guard_status; \
     } while (0)
 
 #define AXIS_HIP(call)                                       \

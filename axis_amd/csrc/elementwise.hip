@@ -740,6 +740,7 @@ extern "C" {
 int axis_mask_gradient(axis_device device, const float *gradient, const float *winners, float *out,
                        int64_t len) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {gradient, 4 * len}, {winners, 4 * len}, {out, 4 * len});
     AXIS_REQUIRE(len >= 0 && (len == 0 || (gradient && winners && out)), "bad mask_gradient args");
     return launch_map(device, MaskGradient{gradient, winners, out}, len,
                       all_aligned({gradient, winners, out}), "mask_gradient");
@@ -747,6 +748,7 @@ int axis_mask_gradient(axis_device device, const float *gradient, const float *w
 
 int axis_relu(axis_device device, const float *a, float *out, int64_t len) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {a, 4 * len}, {out, 4 * len});
     AXIS_REQUIRE(len >= 0 && (len == 0 || (a && out)), "bad relu args");
     return launch_map(device, Relu{a, out}, len, all_aligned({a, out}), "relu");
 }
@@ -754,6 +756,7 @@ int axis_relu(axis_device device, const float *a, float *out, int64_t len) {
 int axis_relu_backward(axis_device device, const float *gradient, const float *a, float *out,
                        int64_t len) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {gradient, 4 * len}, {a, 4 * len}, {out, 4 * len});
     AXIS_REQUIRE(len >= 0 && (len == 0 || (gradient && a && out)), "bad relu_backward args");
     return launch_map(device, ReluBackward{gradient, a, out}, len, all_aligned({gradient, a, out}),
                       "relu_backward");
@@ -761,6 +764,7 @@ int axis_relu_backward(axis_device device, const float *gradient, const float *a
 
 int axis_scale(axis_device device, const float *a, float factor, float *out, int64_t len) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {a, 4 * len}, {out, 4 * len});
     AXIS_REQUIRE(len >= 0 && (len == 0 || (a && out)), "bad scale args");
     return launch_map(device, Scale{a, factor, out}, len, all_aligned({a, out}), "scale");
 }
@@ -768,6 +772,7 @@ int axis_scale(axis_device device, const float *a, float factor, float *out, int
 int axis_binary(axis_device device, const float *a, const float *b, int32_t op, float *out,
                 int64_t len) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {a, 4 * len}, {b, 4 * len}, {out, 4 * len});
     AXIS_REQUIRE(op >= 0 && op <= 3, "binary op must be 0 (add), 1 (sub), 2 (mul) or 3 (div)");
     AXIS_REQUIRE(len >= 0 && (len == 0 || (a && b && out)), "bad binary args");
     const bool v = all_aligned({a, b, out});
@@ -782,6 +787,7 @@ int axis_binary(axis_device device, const float *a, const float *b, int32_t op, 
 int axis_select_axis(axis_device device, const float *input, float *out, const int32_t *metadata,
                      int32_t rank, int32_t coordinate, int64_t output_len) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {input, 1}, {out, 4 * output_len});
     AXIS_REQUIRE(input && out, "null select_axis buffer");
     SelectArgs a{};
     if (int s = select_args(metadata, rank, coordinate, output_len, true, &a)) return s;
@@ -796,6 +802,7 @@ int axis_select_axis_backward(axis_device device, const float *gradient, float *
                               const int32_t *metadata, int32_t rank, int32_t coordinate,
                               int64_t input_len) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {gradient, 1}, {out, 4 * input_len});
     AXIS_REQUIRE(gradient && out, "null select_axis_backward buffer");
     SelectArgs a{};
     if (int s = select_args(metadata, rank, coordinate, input_len, false, &a)) return s;
@@ -808,6 +815,7 @@ int axis_select_axis_backward(axis_device device, const float *gradient, float *
 
 int axis_inverse_sqrt(axis_device device, const float *a, float epsilon, float *out, int64_t len) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {a, 4 * len}, {out, 4 * len});
     AXIS_REQUIRE(len >= 0 && (len == 0 || (a && out)), "bad inverse_sqrt args");
     return launch_map(device, InverseSqrt{a, epsilon, out}, len, all_aligned({a, out}),
                       "inverse_sqrt");
@@ -816,6 +824,7 @@ int axis_inverse_sqrt(axis_device device, const float *a, float epsilon, float *
 int axis_multiply_scalar(axis_device device, const float *a, const float *scalar, float *out,
                          int64_t len) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {a, 4 * len}, {scalar, 4}, {out, 4 * len});
     AXIS_REQUIRE(scalar, "device scalar multiplier must contain exactly one value");
     AXIS_REQUIRE(len >= 0 && (len == 0 || (a && out)), "bad multiply_scalar args");
     return launch_map(device, MultiplyScalar{a, scalar, out}, len, all_aligned({a, out}),
@@ -824,6 +833,7 @@ int axis_multiply_scalar(axis_device device, const float *a, const float *scalar
 
 int axis_sum_squares(axis_device device, const float *a, int64_t len, float *out) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {a, 4 * len}, {out, 4});
     AXIS_REQUIRE(len >= 1, "sum of squares requires a nonempty buffer");
     AXIS_REQUIRE(a && out, "null sum_squares buffer");
     const int blocks = (int)axis::blocks_for(len, kBlock * 8, 1024);
@@ -838,6 +848,7 @@ int axis_sum_squares(axis_device device, const float *a, int64_t len, float *out
 int axis_bias_add(axis_device device, const float *a, const float *bias, float *out,
                   float *relu_out, int64_t rows, int64_t width) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {a, 4 * rows * width}, {bias, 4 * width}, {out, 4 * rows * width}, {relu_out, 4 * rows * width});
     AXIS_REQUIRE(a && bias && out, "null bias_add buffer");
     AXIS_REQUIRE(rows >= 1 && width >= 1, "bias_add extents must be positive");
     const bool v = width % 4 == 0 && all_aligned({a, bias, out, relu_out});
@@ -848,6 +859,7 @@ int axis_bias_add(axis_device device, const float *a, const float *bias, float *
 int axis_bias_gradient(axis_device device, const float *gradient, const float *relu_input,
                        float *masked_out, float *out, int64_t rows, int64_t width) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {gradient, 4 * rows * width}, {relu_input, 4 * rows * width}, {masked_out, 4 * rows * width}, {out, 4 * width});
     AXIS_REQUIRE(gradient && out, "null bias_gradient buffer");
     AXIS_REQUIRE(!relu_input || masked_out, "a masked bias gradient needs masked_out");
     AXIS_REQUIRE(rows >= 1 && width >= 1, "bias_gradient extents must be positive");
@@ -886,6 +898,7 @@ int axis_bias_gradient(axis_device device, const float *gradient, const float *r
 int axis_reduce_middle(axis_device device, const float *a, float *out, int64_t outer,
                        int64_t reduce, int64_t inner, float factor) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {a, 4 * outer * reduce * inner}, {out, 4 * outer * inner});
     AXIS_REQUIRE(a && out, "null reduce_middle buffer");
     AXIS_REQUIRE(outer >= 1 && reduce >= 1 && inner >= 1, "reduce_middle extents must be positive");
     reduce_middle_kernel<<<axis::blocks_for(outer * inner, kBlock, INT32_MAX), kBlock, 0,
@@ -896,6 +909,7 @@ int axis_reduce_middle(axis_device device, const float *a, float *out, int64_t o
 int axis_reduce_axes(axis_device device, const float *a, float *out, int32_t rank, const int64_t *extents,
                      const int64_t *strides, const int32_t *reduced, float factor) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {a, 1}, {out, 1});
     AXIS_REQUIRE(a && out && reduced, "null reduce_axes buffer");
     int order[kMaxReduceDims];
     int64_t len = 0;
@@ -974,6 +988,7 @@ int axis_reduce_axes_backward(axis_device device, const float *gradient, float *
                               const int64_t *extents, const int64_t *strides, const int32_t *reduced,
                               float factor) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {gradient, 1}, {out, 1});
     AXIS_REQUIRE(gradient && out && reduced, "null reduce_axes_backward buffer");
     int order[kMaxReduceDims];
     int64_t len = 0;
@@ -1004,6 +1019,7 @@ int axis_reduce_axes_backward(axis_device device, const float *gradient, float *
 int axis_extreme_axis(axis_device device, const float *a, int32_t rank, const int64_t *extents,
                       const int64_t *strides, int32_t axis, int32_t maximum, float *out, float *winner_mask) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {a, 1}, {out, 1}, {winner_mask, 1});
     AXIS_REQUIRE(a && out && winner_mask, "null extreme_axis buffer");
     ExtremeAxisArgs x;
     if (int st = extreme_axis_args(rank, extents, strides, axis, x)) return st;
@@ -1018,6 +1034,7 @@ int axis_extreme_axis(axis_device device, const float *a, int32_t rank, const in
 int axis_extreme_axis_backward(axis_device device, const float *gradient, const float *winner_mask, int32_t rank,
                                const int64_t *extents, const int64_t *strides, int32_t axis, float *out) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {gradient, 1}, {winner_mask, 1}, {out, 1});
     AXIS_REQUIRE(gradient && winner_mask && out, "null extreme_axis_backward buffer");
     ExtremeAxisArgs x;
     if (int st = extreme_axis_args(rank, extents, strides, axis, x)) return st;
@@ -1029,6 +1046,7 @@ int axis_extreme_axis_backward(axis_device device, const float *gradient, const 
 int axis_broadcast_middle(axis_device device, const float *gradient, float *out, int64_t outer,
                           int64_t reduce, int64_t inner, float factor) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {gradient, 4 * outer * inner}, {out, 4 * outer * reduce * inner});
     AXIS_REQUIRE(gradient && out, "null broadcast_middle buffer");
     AXIS_REQUIRE(outer >= 1 && reduce >= 1 && inner >= 1, "broadcast_middle extents must be positive");
     const bool v = inner % 4 == 0 && all_aligned({gradient, out});

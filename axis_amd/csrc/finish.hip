@@ -102,6 +102,16 @@ int flush_finish(axis_device device) {
     return status;
 }
 
+int finish_overlapping(axis_device device, std::initializer_list<Span> spans) {
+    for (const Span &sp : spans) {
+        if (!sp.ptr || sp.bytes <= 0) continue;
+        const char *lo = static_cast<const char *>(sp.ptr);
+        for (const FinishTask &t : device->deferred)
+            if (overlaps(t, lo, lo + sp.bytes)) return flush_finish(device);
+    }
+    return AXIS_OK;
+}
+
 int defer_finish(axis_device device, const FinishTask &task, Scratch &held) {
     if (task.blocks < 1 || (int64_t)task.blocks > (int64_t)INT32_MAX / 2)
         return fail(AXIS_ERROR_INVALID, "finishing sum too large to defer");

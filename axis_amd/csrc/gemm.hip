@@ -1654,6 +1654,7 @@ extern "C" {
 int axis_matmul(axis_device device, const float *a, const float *b, float *out, int64_t batch,
                 int64_t m, int64_t k, int64_t n) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {a, 4 * batch * m * k}, {b, 4 * batch * k * n}, {out, 4 * batch * m * n});
     if (int s = check_dims(a, b, out, batch, m, k, n)) return s;
     GemmParams p{};
     p.x = a;
@@ -1673,6 +1674,7 @@ int axis_matmul(axis_device device, const float *a, const float *b, float *out, 
 int axis_matmul_bias(axis_device device, const float *a, const float *b, const float *bias, float *out,
                      int64_t batch, int64_t m, int64_t k, int64_t n) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {a, 4 * batch * m * k}, {b, 4 * batch * k * n}, {bias, 4 * n}, {out, 4 * batch * m * n});
     if (int s = check_dims(a, b, out, batch, m, k, n)) return s;
     AXIS_REQUIRE(bias, "null matmul bias");
     AXIS_REQUIRE(bias + n <= out || bias >= out + batch * m * n, "matmul bias must not alias the output");
@@ -1695,6 +1697,7 @@ int axis_matmul_bias(axis_device device, const float *a, const float *b, const f
 int axis_matmul_axpby(axis_device device, const float *a, const float *b, const float *d, float *out,
                       int64_t batch, int64_t m, int64_t k, int64_t n, float alpha, float beta) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {a, 4 * batch * m * k}, {b, 4 * batch * k * n}, {d, 4 * batch * m * n}, {out, 4 * batch * m * n});
     if (int s = check_dims(a, b, out, batch, m, k, n)) return s;
     AXIS_REQUIRE(d, "null axpby addend");
     AXIS_REQUIRE(d != out, "axpby addend must not alias the output");
@@ -1719,6 +1722,7 @@ int axis_matmul_axpby(axis_device device, const float *a, const float *b, const 
 int axis_matmul_left_backward(axis_device device, const float *gradient, const float *rhs,
                               float *out, int64_t batch, int64_t m, int64_t k, int64_t n) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {gradient, 4 * batch * m * n}, {rhs, 4 * batch * k * n}, {out, 4 * batch * m * k});
     if (int s = check_dims(gradient, rhs, out, batch, m, k, n)) return s;
     // out [m, k] = gradient [m, n] . rhs[k, n]^T : i = m, j = k, r = n.
     GemmParams p{};
@@ -1739,6 +1743,7 @@ int axis_matmul_left_backward(axis_device device, const float *gradient, const f
 int axis_matmul_right_backward(axis_device device, const float *lhs, const float *gradient,
                                float *out, int64_t batch, int64_t m, int64_t k, int64_t n) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {lhs, 4 * batch * m * k}, {gradient, 4 * batch * m * n}, {out, 4 * batch * k * n});
     if (int s = check_dims(lhs, gradient, out, batch, m, k, n)) return s;
     // out [k, n] = lhs[m, k]^T . gradient [m, n] : i = k, j = n, r = m.
     GemmParams p{};
@@ -1759,6 +1764,7 @@ int axis_matmul_right_backward(axis_device device, const float *lhs, const float
 int axis_matmul_right_backward_noalloc(axis_device device, const float *lhs, const float *gradient,
                                        float *out, int64_t batch, int64_t m, int64_t k, int64_t n) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {lhs, 4 * batch * m * k}, {gradient, 4 * batch * m * n}, {out, 4 * batch * k * n});
     if (int s = check_dims(lhs, gradient, out, batch, m, k, n)) return s;
     AXIS_REQUIRE(!device->bf16_matmul, "the allocation-free product is fp32 only (a bf16 handle stages operands)");
     AXIS_REQUIRE(device->static_scratch, "static scratch is not bound on this device");
@@ -1793,6 +1799,7 @@ int axis_conv2d_forward(axis_device device, const float *input, const int64_t in
                         int32_t height, int32_t width, int32_t channels, int32_t out_channels,
                         const int32_t kernel[2], const int32_t stride[2], const int32_t padding[2]) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {input, 1}, {weight, 1}, {bias, 4 * (int64_t)out_channels}, {out, 1});
     AXIS_REQUIRE(input && weight && out, "null convolution buffer");
     ConvShape s{};
     if (int st = conv_shape(batch, height, width, channels, out_channels, kernel, stride, padding, &s))
@@ -1828,6 +1835,7 @@ int axis_conv2d_relu_pool_forward(axis_device device, const float *input,
                                   const int32_t stride[2], const int32_t padding[2],
                                   const int32_t pool[2]) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {input, 1}, {weight, 1}, {bias, 4 * (int64_t)out_channels}, {pooled, 1}, {argmax, 1});
     AXIS_REQUIRE(input && weight && pooled && argmax && pool, "null convolution buffer");
     ConvShape s{};
     if (int st = conv_shape(batch, height, width, channels, out_channels, kernel, stride, padding, &s))
@@ -1875,6 +1883,7 @@ int axis_conv2d_backward_data(axis_device device, const float *gradient, const f
                               int32_t channels, int32_t out_channels, const int32_t kernel[2],
                               const int32_t stride[2], const int32_t padding[2]) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {gradient, 1}, {weight, 1}, {d_input, 4 * batch * height * width * channels});
     AXIS_REQUIRE(gradient && weight && d_input, "null convolution buffer");
     ConvShape s{};
     if (int st = conv_shape(batch, height, width, channels, out_channels, kernel, stride, padding, &s))
@@ -1927,6 +1936,7 @@ int axis_conv2d_backward_weight(axis_device device, const float *input,
                                 int32_t channels, int32_t out_channels, const int32_t kernel[2],
                                 const int32_t stride[2], const int32_t padding[2]) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {input, 1}, {gradient, 1}, {d_weight, 1});
     AXIS_REQUIRE(input && gradient && d_weight, "null convolution buffer");
     ConvShape s{};
     if (int st = conv_shape(batch, height, width, channels, out_channels, kernel, stride, padding, &s))
@@ -1977,6 +1987,7 @@ int axis_conv2d_relu_pool_backward_weight(axis_device device, const float *input
                                           const int32_t stride[2], const int32_t padding[2],
                                           const int32_t pool[2]) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {input, 1}, {gradient, 1}, {pooled, 1}, {argmax, 1}, {d_weight, 1}, {d_bias, 4 * (int64_t)out_channels});
     AXIS_REQUIRE(input && gradient && pooled && argmax && d_weight && pool, "null convolution buffer");
     ConvShape s{};
     if (int st = conv_shape(batch, height, width, channels, out_channels, kernel, stride, padding, &s))

@@ -81,6 +81,7 @@ template <bool MAXIMUM>
 int grouped_extreme(axis_device device, const float *a, int64_t input_len, axis_plan forward,
                     axis_plan reverse, float *out, int32_t *winners, float *winner_mask) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {a, 4 * input_len}, {out, 1}, {winners, 1}, {winner_mask, 1});
     AXIS_REQUIRE(a && forward && reverse && out && winner_mask, "null grouped extreme argument");
     AXIS_REQUIRE(reverse->count == input_len && reverse->groups == input_len,
                  "reverse plan must be a gather plan over every input position");
@@ -106,6 +107,7 @@ extern "C" {
 int axis_grouped(axis_device device, const float *a, const float *b, axis_plan plan, float scale,
                  float *out) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {a, 1}, {b, 1}, {out, 1});
     AXIS_REQUIRE(a && plan && out, "null grouped argument");
     AXIS_REQUIRE(!b || plan->right, "a product reduction needs a plan with right indices");
     axis::Scratch partial;

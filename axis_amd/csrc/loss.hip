@@ -213,6 +213,7 @@ extern "C" {
 
 int axis_softmax(axis_device device, const float *a, float *out, int64_t rows, int64_t width) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {a, 4 * rows * width}, {out, 4 * rows * width});
     if (int s = check_rows(a, out, rows, width)) return s;
     return launch_softmax_ce(device->stream, a, nullptr, out, nullptr, rows, width);
 }
@@ -220,6 +221,7 @@ int axis_softmax(axis_device device, const float *a, float *out, int64_t rows, i
 int axis_softmax_backward(axis_device device, const float *gradient, const float *probability,
                           float *out, int64_t rows, int64_t width) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {gradient, 4 * rows * width}, {probability, 4 * rows * width}, {out, 4 * rows * width});
     if (int s = check_rows(gradient, out, rows, width)) return s;
     AXIS_REQUIRE(probability, "null probability");
     softmax_backward_kernel<<<(unsigned)rows, kBlock, 0, device->stream>>>(gradient, probability, out,
@@ -230,6 +232,7 @@ int axis_softmax_backward(axis_device device, const float *gradient, const float
 int axis_categorical_cross_entropy(axis_device device, const float *logits, const float *targets,
                                    float *out, int64_t rows, int64_t width) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {logits, 4 * rows * width}, {targets, 4 * rows * width}, {out, 4 * rows});
     if (int s = check_rows(logits, out, rows, width)) return s;
     AXIS_REQUIRE(targets, "null targets");
     return launch_softmax_ce(device->stream, logits, targets, nullptr, out, rows, width);
@@ -239,6 +242,7 @@ int axis_categorical_cross_entropy_backward(axis_device device, const float *gra
                                             const float *probability, const float *targets,
                                             float *out, int64_t rows, int64_t width) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {gradient, 4 * rows}, {probability, 4 * rows * width}, {targets, 4 * rows * width}, {out, 4 * rows * width});
     if (int s = check_rows(gradient, out, rows, width)) return s;
     AXIS_REQUIRE(probability && targets, "null probability/targets");
     ce_backward_kernel<<<axis::blocks_for(rows * width, kBlock, 16384), kBlock, 0, device->stream>>>(
@@ -250,6 +254,7 @@ int axis_categorical_cross_entropy_backward_mean(axis_device device, const float
                                                  const float *probability, const float *targets, float *out,
                                                  float *d_bias, int64_t rows, int64_t width) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {gradient, 4}, {probability, 4 * rows * width}, {targets, 4 * rows * width}, {out, 4 * rows * width}, {d_bias, 4 * width});
     if (int s = check_rows(gradient, out, rows, width)) return s;
     AXIS_REQUIRE(probability && targets, "null probability/targets");
     AXIS_REQUIRE(factor != 0.0f && std::isfinite(factor), "mean factor must be finite and nonzero");
@@ -276,6 +281,7 @@ int axis_categorical_cross_entropy_backward_mean(axis_device device, const float
 int axis_softmax_cross_entropy(axis_device device, const float *logits, const float *targets,
                                float *probability, float *loss, int64_t rows, int64_t width) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {logits, 4 * rows * width}, {targets, 4 * rows * width}, {probability, 4 * rows * width}, {loss, 4 * rows});
     if (int s = check_rows(logits, probability, rows, width)) return s;
     AXIS_REQUIRE(targets && loss, "null targets/loss");
     return launch_softmax_ce(device->stream, logits, targets, probability, loss, rows, width);

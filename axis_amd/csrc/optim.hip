@@ -209,6 +209,7 @@ extern "C" {
 int axis_muon_momentum(axis_device device, const float *gradient, const float *previous, float *next,
                        float *direction, float momentum, int nesterov, int64_t len) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {gradient, 4 * len}, {previous, 4 * len}, {next, 4 * len}, {direction, 4 * len});
     AXIS_REQUIRE(len >= 0, "negative length");
     if (len == 0) return AXIS_OK;
     AXIS_REQUIRE(gradient && next && (direction || !nesterov), "null Muon buffer");
@@ -235,6 +236,7 @@ int axis_muon_momentum(axis_device device, const float *gradient, const float *p
 int axis_muon_apply(axis_device device, const float *value, const float *orthogonal, float *out, float decay,
                     float rate, int64_t len) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {value, 4 * len}, {orthogonal, 4 * len}, {out, 4 * len});
     AXIS_REQUIRE(len >= 0, "negative length");
     if (len == 0) return AXIS_OK;
     AXIS_REQUIRE(value && orthogonal && out, "null Muon buffer");
@@ -250,6 +252,7 @@ int axis_adam(axis_device device, const float *value, const float *gradient, con
               float beta1, float beta2, float correction1, float correction2, float epsilon,
               float weight_decay, float *out_value, float *out_first, float *out_second) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {value, 4 * len}, {gradient, 4 * len}, {first, 4 * len}, {second, 4 * len}, {learning_rates, 4 * len}, {out_value, 4 * len}, {out_first, 4 * len}, {out_second, 4 * len});
     AXIS_REQUIRE(len >= 0, "negative length");
     if (len == 0) return AXIS_OK;
     AXIS_REQUIRE(value && gradient && first && second && out_value && out_first && out_second,
@@ -272,6 +275,8 @@ int axis_adam_multi(axis_device device, const axis_adam_tensor *tensors, int32_t
         AXIS_REQUIRE(t.len >= 0, "negative adam tensor length");
         AXIS_REQUIRE(t.len == 0 || (t.value && t.gradient && t.first && t.second),
                      "null adam tensor buffer");
+        AXIS_GUARD(device, {t.value, 4 * t.len}, {t.gradient, 4 * t.len}, {t.first, 4 * t.len},
+                   {t.second, 4 * t.len}, {t.learning_rates, 4 * t.len});
     }
     const AdamHyper h = hyper(learning_rate, beta1, beta2, correction1, correction2, epsilon,
                               weight_decay);

@@ -394,6 +394,7 @@ int axis_max_pool2d(axis_device device, const float *input, float *out, uint8_t 
                     int64_t outer, int32_t height, int32_t width, int64_t channels,
                     const int32_t kernel[2], const int32_t stride[2], const int32_t padding[2]) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {input, 4 * outer * height * width * channels}, {out, 1}, {argmax, 1});
     AXIS_REQUIRE(input && out && argmax, "null max_pool2d buffer");
     PoolArgs a{};
     if (int s = pool_args(outer, height, width, channels, kernel, stride, padding, &a)) return s;
@@ -416,6 +417,7 @@ int axis_max_pool2d_backward(axis_device device, const float *gradient, const ui
                              int64_t channels, const int32_t kernel[2], const int32_t stride[2],
                              const int32_t padding[2]) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {gradient, 1}, {argmax, 1}, {out, 4 * outer * height * width * channels});
     AXIS_REQUIRE(gradient && argmax && out, "null max_pool2d_backward buffer");
     PoolArgs a{};
     if (int s = pool_args(outer, height, width, channels, kernel, stride, padding, &a)) return s;
@@ -449,6 +451,7 @@ int axis_relu_pool_backward(axis_device device, const float *gradient, const flo
                             const uint8_t *argmax, float *d_pre, float *d_bias, int64_t outer,
                             int32_t height, int32_t width, int32_t channels, const int32_t pool[2]) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {gradient, 1}, {pooled, 1}, {argmax, 1}, {d_pre, 4 * outer * height * width * channels}, {d_bias, 4 * (int64_t)channels});
     return relu_pool_backward(device, gradient, false, 1.0f, pooled, argmax, d_pre, d_bias, outer, height, width,
                               channels, pool);
 }
@@ -457,6 +460,7 @@ int axis_relu_pool_backward_mean(axis_device device, const float *gradient, floa
                                  const uint8_t *argmax, float *d_pre, float *d_bias, int64_t outer,
                                  int32_t height, int32_t width, int32_t channels, const int32_t pool[2]) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {gradient, 1}, {pooled, 1}, {argmax, 1}, {d_pre, 4 * outer * height * width * channels}, {d_bias, 4 * (int64_t)channels});
     return relu_pool_backward(device, gradient, true, factor, pooled, argmax, d_pre, d_bias, outer, height, width,
                               channels, pool);
 }

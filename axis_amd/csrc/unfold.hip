@@ -257,6 +257,7 @@ extern "C" {
 
 int axis_unfold(axis_device device, const float *input, float *out, const axis_unfold_spec *spec) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {input, spec ? 4 * spec->input_len : 1}, {out, spec ? 4 * spec->output_len : 1});
     if (int st = validate(spec)) return st;
     AXIS_REQUIRE(input && out, "null unfold buffer");
     Im2colArgs fast{};
@@ -288,6 +289,7 @@ int axis_unfold(axis_device device, const float *input, float *out, const axis_u
 int axis_unfold_backward(axis_device device, const float *gradient, float *out,
                          const axis_unfold_spec *spec) {
     AXIS_ENTER(device);
+    AXIS_GUARD(device, {gradient, spec ? 4 * spec->output_len : 1}, {out, spec ? 4 * spec->input_len : 1});
     if (int st = validate(spec)) return st;
     AXIS_REQUIRE(gradient && out, "null unfold_backward buffer");
     UnfoldArgs a = common_args(spec);

@@ -93,9 +93,11 @@ int axis_timing_read(axis_device device, const char *family, int64_t *launches, 
  * of launching it; those outputs hold their values only once the recorded sums have run.
  * axis_finish_flush runs every recorded sum in one launch, with the same results bit for bit;
  * axis_finish_before_read flushes when a recorded sum writes into [ptr, ptr + bytes);
- * axis_finish_defer(device, 0) flushes and stops deferring.  axis_read, axis_copy, axis_upload,
- * axis_fill, axis_free and axis_device_synchronize flush first themselves when they touch such an
- * output; any other entry that reads or writes one must be preceded by one of the calls above. */
+ * axis_finish_defer(device, 0) flushes and stops deferring.  Every entry that touches such an
+ * output flushes first by itself: axis_read, axis_copy, axis_upload, axis_fill, axis_free and
+ * axis_device_synchronize, and every compute entry, for each buffer it reads or writes (a buffer
+ * read through strides is checked at its first byte).  A batch that holds more than 256 MiB of
+ * partial results is launched early. */
 int axis_finish_defer(axis_device device, int enabled);
 int axis_finish_flush(axis_device device);
 int axis_finish_before_read(axis_device device, const void *ptr, size_t bytes);

@@ -1303,6 +1303,79 @@ def test_deferred_finishing_sums_flush_on_read_free_and_overflow(dev):
         dev.call("axis_finish_defer", I32(0))
 
 
+def test_kernel_entries_run_a_pending_sum_before_touching_its_output(dev, oracle):
+    # any compute entry given a buffer a pending finishing sum writes (as input or output) runs the
+    # batch first: the reader sees the finished gradient, a later writer's values win; entries on
+    # other buffers leave the batch pending
+    rng = np.random.default_rng(11)
+    m, k, n = 8192, 32, 24
+    lhs = up(dev, rng.standard_normal(m * k).astype(np.float32))
+    g = up(dev, rng.standard_normal(m * n).astype(np.float32))
+    geo = (I64(1), I64(m), I64(k), I64(n))
+    ref = dev.empty(k * n)
+    dev.call("axis_matmul_right_backward", lhs.vp, g.vp, ref.vp, *geo)
+    expected = dev.read(ref, k * n)
+    other_in, other_out = up(dev, np.ones(64, np.float32)), dev.empty(64)
+    dev.call("axis_finish_defer", I32(1))
+    try:
+        pend = dev.empty(k * n)
+        dev.call("axis_matmul_right_backward", lhs.vp, g.vp, pend.vp, *geo)
+        assert _pending(dev) == 1
+        dev.call("axis_scale", other_in.vp, F32(2.0), other_out.vp, I64(64))      # unrelated
+        assert _pending(dev) == 1
+        scaled = dev.empty(k * n)
+        dev.call("axis_scale", pend.vp, F32(2.0), scaled.vp, I64(k * n))          # reads it
+        assert _pending(dev) == 0
+        assert np.array_equal(dev.read(scaled, k * n), np.float32(2.0) * expected)
+        # an Adam update whose gradient is pending
+        p0 = up(dev, np.zeros(k * n, np.float32))
+        m0, v0 = up(dev, np.zeros(k * n, np.float32)), up(dev, np.zeros(k * n, np.float32))
+        dev.call("axis_matmul_right_backward", lhs.vp, g.vp, pend.vp, *geo)
+        assert _pending(dev) == 1
+        table = (hip.AdamTensor * 1)(hip.AdamTensor(p0.ptr, pend.ptr, m0.ptr, v0.ptr, None, k * n))
+        dev.call("axis_adam_multi", table, I32(1), F32(1e-3), F32(0.9), F32(0.999), F32(0.1), F32(0.001),
+                 F32(1e-8), F32(0.0))
+        assert _pending(dev) == 0
+        # a pending output overwritten by another entry keeps the later values
+        dev.call("axis_matmul_right_backward", lhs.vp, g.vp, pend.vp, *geo)
+        dev.call("axis_relu", other_in.vp, VP(pend.ptr), I64(64))
+        assert _pending(dev) == 0
+        got = dev.read(pend, k * n)
+        assert np.all(got[:64] == 1.0) and np.array_equal(got[64:], expected[64:])
+    finally:
+        dev.call("axis_finish_defer", I32(0))
+    zero = np.zeros(k * n, np.float32)
+    want_p, want_m, want_v = oracle.adam(zero, expected, zero, zero, 1e-3, 0.9, 0.999, 0.1, 0.001, 1e-8, 0.0)
+    for buf, want in ((p0, want_p), (m0, want_m), (v0, want_v)):
+        assert np.array_equal(dev.read(buf, k * n).view(np.uint32), want.view(np.uint32))
+
+
+def test_deferred_finishing_sums_flush_past_the_held_byte_limit(dev):
+    # large split weight gradients deferred one after another: the batch is launched once the
+    # partial blocks it holds pass 256 MiB, well before the 24-task limit, with the same bits
+    rng = np.random.default_rng(12)
+    m, k, n = 65536, 1024, 1024
+    lhs = up(dev, rng.standard_normal(m * k).astype(np.float32))
+    g = up(dev, rng.standard_normal(m * n).astype(np.float32))
+    geo = (I64(1), I64(m), I64(k), I64(n))
+    ref = dev.empty(k * n)
+    dev.call("axis_matmul_right_backward", lhs.vp, g.vp, ref.vp, *geo)
+    expected = dev.read(ref, k * n)
+    outs, most = [], 0
+    dev.call("axis_finish_defer", I32(1))
+    try:
+        for _ in range(20):
+            o = dev.empty(k * n)
+            dev.call("axis_matmul_right_backward", lhs.vp, g.vp, o.vp, *geo)
+            outs.append(o)
+            most = max(most, _pending(dev))
+    finally:
+        dev.call("axis_finish_defer", I32(0))
+    assert _pending(dev) == 0 and 1 <= most < 20, most
+    for o in outs:
+        assert np.array_equal(dev.read(o, k * n).view(np.uint32), expected.view(np.uint32))
+
+
 @pytest.mark.parametrize("m,k,n", [(8192, 64, 48), (65536, 16, 20), (4096, 7, 9)])
 def test_split_sums_vector_and_scalar_forms_agree(dev, m, k, n):
     # a split weight gradient into a 16-byte aligned output (four outputs per lane when k*n % 4 == 0)
