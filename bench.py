@@ -114,13 +114,13 @@ def _cpu_model() -> str:
     return "unknown"
 
 
-def cpu_baseline(sample_batch: int, repeats: int = 5):
+def cpu_baseline(sample_batch: int, seconds: float = 10.0, min_repeats: int = 5):
     """The same config-4 step on this host's cores: oracle/cpu_step.c, a blocked fp32 SGEMM
     (NN / NT / TN, packed panels, AVX-512 or AVX2 register tiles) OpenMP port with the same
     im2col / col2im, bias + ReLU + max pool, mean pool, softmax cross-entropy and Adam, held to the
     oracle by tests/test_cpu_baseline.py.  One untimed step (it pages in the step's buffers), then
-    the median of `repeats` timed steps at `sample_batch` images of the same inputs; images/s and
-    the GEMM GFLOP/s are per that median step."""
+    timed steps at `sample_batch` images of the same inputs for about `seconds` (at least
+    `min_repeats`); images/s and the GEMM GFLOP/s are per the median step."""
     import ctypes as C
     from oracle import cpu_baseline as cb
     from oracle import oracle
@@ -130,7 +130,7 @@ def cpu_baseline(sample_batch: int, repeats: int = 5):
     times, phases = [], []
     names = ("input", "im2col", "gemm_forward", "bias_relu_pool", "head", "pool_backward", "gemm_weight_gradient",
              "gemm_data_gradient", "col2im", "adam")
-    for _ in range(repeats):
+    while len(times) < min_repeats or sum(times) < seconds:
         start = time.perf_counter()
         cb.cnn_step(x, y, params, sample_batch, SIZE, CLASSES, CHANNELS)
         times.append(time.perf_counter() - start)
@@ -143,9 +143,10 @@ def cpu_baseline(sample_batch: int, repeats: int = 5):
     flops = cnn_gemm_flops(batch=sample_batch)
     return {"value": round(sample_batch / median, 3), "unit": "images/sec", "cores": threads,
             "kind": "port",
-            "sample": f"median of {repeats} timed fwd+bwd+Adam steps of the same 3-block CNN at batch "
-                      f"{sample_batch} (64x64x3, blocked fp32 SGEMM + OpenMP, {cb.kernel_width()}-wide "
-                      f"register tiles) after one untimed step: {', '.join(f'{t:.3f}' for t in times)} s",
+            "sample": f"median of {len(times)} timed fwd+bwd+Adam steps ({sum(times):.1f} s) of the same "
+                      f"3-block CNN at batch {sample_batch} (64x64x3, blocked fp32 SGEMM + OpenMP, "
+                      f"{cb.kernel_width()}-wide register tiles) after one untimed step; min "
+                      f"{min(times):.3f} s, max {max(times):.3f} s",
             "gemm_gflops": round(flops / median / 1e9, 1),
             "phases_ms": {n: round(v * 1e3, 1) for n, v in zip(names, median_phases)},
             "omp_threads": threads, "nproc": os.cpu_count(), "cpu_model": _cpu_model()}
