@@ -413,6 +413,409 @@ __global__ void __launch_bounds__(256, 4) small_conv_pool_wgrad_kernel(SmallConv
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Fixed-geometry instances.  For the usual first layer (1 or 3 channels under a 3x3 kernel, images
+// whose windows span at least 25 columns, whole 64-column groups of outputs) the patch shape and the
+// band shape (32 window columns) are compile-time constants, so that:
+// * the next band's input cells stream straight into a second LDS buffer (buffer_load ... lds, one
+//   4-byte cell per lane; cells outside the image are loads past the resource's record count and
+//   land as 0), with no prefetch registers and no LDS store pass;
+// * every LDS operand read is a base register plus an immediate offset;
+// * the forward's max pool runs on the bit patterns of the pre-activations (a signed integer
+//   compare orders positive floats like the float compare and puts every negative value, -0 and
+//   negative NaN below +0), with one check per tile for +inf or positive NaN, which take the exact
+//   scan instead;
+// * the weight gradient selects each MFMA operand from the band's pooled gradient, pooled values
+//   and winner bytes in registers (g at the window's winner when the pooled value is positive,
+//   else 0) instead of expanding the pre-activation gradient in LDS.
+// Both instances make the same MFMA calls in the same order as the generic kernels above.
+
+constexpr uint32_t kOutside = 0x80000000u;  // a buffer offset past the record count: loads 0, stores drop
+
+__device__ __forceinline__ uint64_t uniform_u64(uint64_t v) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return ((uint64_t)hi << 32) | lo;
+}
+
+template <typename T>
+__device__ __forceinline__ T *uniform_ptr(T *p) {
+    return reinterpret_cast<T *>(uniform_u64(reinterpret_cast<uint64_t>(p)));
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_of(const void *base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, 0x7fffffff, 0x00020000);
+}
+
+typedef __attribute__((address_space(3))) void *lds_void;
+
+// C channels under a KH x KW kernel; bands of BR x 32 windows.  Staged rows are SW cells apart and
+// planes PP cells apart (both at least the band's extent), chosen per kernel so that one operand
+// read of a wave meets no LDS bank conflict.
+template <int C, int KH, int KW, int BR, int SW_, int PP>
+struct Fixed {
+    static constexpr int BS = 32;                     // window columns per band
+    static constexpr int WIDTH = 2 * BS + KW - 1;     // staged columns
+    static constexpr int SW = SW_;                    // row pitch
+    static constexpr int SH = 2 * BR + KH - 1;        // staged rows
+    static constexpr int CELLS = SW * SH;             // cells of a plane, row padding included
+    static constexpr int CHUNKS = (CELLS + 63) / 64;  // 64-cell wave loads per plane
+    static constexpr int PLANE = PP;                  // plane pitch
+    static constexpr int K = C * KH * KW;             // patch terms; term K is the bias
+    static constexpr int LOADS = C * CHUNKS;          // wave loads per band
+    static constexpr int SLOTS = (LOADS + 3) / 4;     // wave loads per wave
+    static constexpr int XBUF = (C + 1) * PLANE;      // input planes and the ones plane
+    static_assert(SW >= WIDTH && PLANE >= 64 * CHUNKS, "pitches cover the band");
+    // LDS offset of patch term k = (c, ky, kx) from its pixel's cell; terms from K on read the
+    // ones plane
+    static constexpr int off(int k) {
+        return k >= K ? C * PLANE : (k / (KH * KW)) * PLANE + (k % (KH * KW)) / KW * SW + k % KW;
+    }
+};
+
+// The staging of a band's input planes: wave load q = wave + 4 s moves cells 64 (q % CHUNKS) ..
+// + 63 of plane q / CHUNKS (lane i: cell 64 (q % CHUNKS) + i), so each wave load fills 256
+// consecutive LDS bytes; the row padding (columns WIDTH .. SW - 1) loads 0.  A cell's offset from
+// the band's corner is fixed; its row and column are recomputed per band (a multiply-shift by the
+// constant row pitch) for the image-bounds test.
+template <class F>
+struct StripStream {
+    uint32_t rel[F::SLOTS];  // byte offset of the cell from the band's corner (row 0, column 0)
+    int wave, lane;
+
+    __device__ __forceinline__ void init(const SmallConvArgs &a, int tid) {
+        wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+        lane = tid & 63;
+#pragma unroll
+        for (int s = 0; s < F::SLOTS; ++s) {
+            const int q = wave + 4 * s;
+            const int t = 64 * (q % F::CHUNKS) + lane;
+            const int r = t / F::SW, c = t - r * F::SW;
+            rel[s] = (uint32_t)((r * a.ld_h + c * a.ld_w + q / F::CHUNKS * a.ld_c) * 4);
+        }
+    }
+
+    __device__ __forceinline__ void load(const SmallConvArgs &a, const Band &b, float *buf) const {
+        const int32_t iy0 = 2 * b.wr0 - a.py, ix0 = 2 * b.wc0 - a.px;
+        const __amdgpu_buffer_rsrc_t rsrc = rsrc_of(uniform_ptr(a.x + (int64_t)b.img * a.ld_b));
+        const int32_t corner = (iy0 * a.ld_h + ix0 * a.ld_w) * 4;  // negative inside the padding
+#pragma unroll
+        for (int s = 0; s < F::SLOTS; ++s) {
+            const int q = wave + 4 * s;
+            if (q < F::LOADS) {
+                const uint32_t t = 64u * (uint32_t)(q % F::CHUNKS) + (uint32_t)lane;
+                const uint32_t r = t / F::SW, c = t - r * F::SW;
+                const bool in = t < (uint32_t)F::CELLS && c < (uint32_t)F::WIDTH &&
+                                (uint32_t)(iy0 + (int32_t)r) < (uint32_t)a.height &&
+                                (uint32_t)(ix0 + (int32_t)c) < (uint32_t)a.width;
+                const uint32_t off = in ? (uint32_t)corner + rel[s] : kOutside;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    rsrc, (lds_void)(buf + q / F::CHUNKS * F::PLANE + 64 * (q % F::CHUNKS)), 4, off, 0, 0, 0);
+            }
+        }
+    }
+};
+
+// Term pairs (2j, 2j + 1) of the forward's k-pairs: the lane half that reads term 2j + 1 reads it
+// delta[j] cells past term 2j.  Lanes keep one base register per distinct delta: pair j reads
+// through the base of pair first[j], the first pair with the same delta.
+template <class F, int KP>
+struct PairTable {
+    int delta[KP], first[KP];
+    constexpr PairTable() : delta{}, first{} {
+        for (int j = 0; j < KP; ++j) delta[j] = F::off(2 * j + 1) - F::off(2 * j);
+        for (int j = 0; j < KP; ++j) {
+            int i = 0;
+            while (delta[i] != delta[j]) ++i;
+            first[j] = i;
+        }
+    }
+};
+
+// Forward with ReLU + 2x2 max pool (the POOL form of small_conv_forward_kernel) over bands of 2 x 32
+// windows: wave w computes tiles (window row 0 and 1, window columns 8w .. 8w + 7) of each band.
+template <int C, int KH, int KW>
+__global__ void __launch_bounds__(256, 4) small_conv_pool_forward_fixed_kernel(SmallConvArgs a) {
+    // rows 80 cells apart (16 banks): a tile's two pixel rows fill the 32 banks of a half-wave read
+    using F = Fixed<C, KH, KW, 2, 80, 512>;
+    constexpr int KP = (F::K + 2) / 2;  // the K terms and the bias
+    constexpr PairTable<F, KP> pairs{};
+    __shared__ float lds[2 * F::XBUF];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int l32 = lane & 31, half = lane >> 5;
+    const int32_t col0 = (int32_t)blockIdx.y * 64;
+
+    // MFMA B operand of k-pair j: W[2j + half][col0 + 2 l32 + b], the bias at term K, 0 past it
+    float wreg[KP][2];
+#pragma unroll
+    for (int j = 0; j < KP; ++j) {
+        const int32_t k = 2 * j + half;
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const int32_t n = col0 + 2 * l32 + b;
+            float w = 0.0f;
+            if (k < F::K) w = a.w[(int64_t)k * a.n + n];
+            if (k == F::K && a.bias != nullptr) w = a.bias[n];
+            wreg[j][b] = w;
+        }
+    }
+    for (int32_t t = tid; t < F::PLANE; t += 256) {
+        lds[C * F::PLANE + t] = 1.0f;
+        lds[F::XBUF + C * F::PLANE + t] = 1.0f;
+    }
+    StripStream<F> stream;
+    stream.init(a, tid);
+    const int wave = stream.wave;
+    // the lane's pixel cell: window l32 / 4 of the wave's tile, position (l32 / 2 % 2, l32 % 2)
+    const int32_t lane_cell = ((l32 >> 1) & 1) * F::SW + 2 * (l32 >> 2) + (l32 & 1) + 16 * wave;
+    // pooled element of the lane's first window (2q + half, q = 0) from the tile's first window
+    // at column col0
+    const int32_t lane_out = half * a.n + 2 * l32;
+    const uint32_t bands = (uint32_t)a.bands;
+
+    uint32_t band = blockIdx.x;
+    if (band < bands) stream.load(a, decode_band(a, band), lds);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+
+    auto run = [&](uint32_t bnd, auto parity) {
+        constexpr int P = decltype(parity)::value;
+        const Band bd = decode_band(a, bnd);
+        if (bnd + gridDim.x < bands) stream.load(a, decode_band(a, bnd + gridDim.x), lds + (P ^ 1) * F::XBUF);
+        const float *px = lds + P * F::XBUF + lane_cell;
+        const float *pd[KP];
+#pragma unroll
+        for (int j = 0; j < KP; ++j)
+            if (pairs.first[j] == j) pd[j] = px + (half ? pairs.delta[j] : 0);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {  // the wave's tile in window row i of the band
+            if (bd.wr0 + i >= a.win_rows) break;
+            float av[KP];
+#pragma unroll
+            for (int j = 0; j < KP; ++j) av[j] = pd[pairs.first[j]][2 * i * F::SW + F::off(2 * j)];
+            __builtin_amdgcn_sched_barrier(0);
+            floatx16 acc[2];
+#pragma unroll
+            for (int b = 0; b < 2; ++b) acc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[0], wreg[0][b], floatx16{}, 0, 0, 0);
+#pragma unroll
+            for (int j = 1; j < KP; ++j)
+#pragma unroll
+                for (int b = 0; b < 2; ++b)
+                    acc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[j], wreg[j][b], acc[b], 0, 0, 0);
+            // Register group q of block b: window 2q + half of the tile, positions 0..3.  The
+            // largest bit pattern of each window; +inf or a positive NaN anywhere in the wave's
+            // windows sends the tile to the exact scan.
+            int32_t top[2][4];
+            int32_t most = INT32_MIN;
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int32_t y0 = __float_as_int(acc[b][4 * q]), y1 = __float_as_int(acc[b][4 * q + 1]);
+                    const int32_t y2 = __float_as_int(acc[b][4 * q + 2]), y3 = __float_as_int(acc[b][4 * q + 3]);
+                    top[b][q] = max(max(max(y0, y1), y2), y3);
+                    most = max(most, top[b][q]);
+                }
+            // pooled values of window pair q (block b: window 2q + half, columns col0 + 2 l32 + b)
+            // and their winner bytes; the tile's first window is window row wr0 + i, column
+            // wc0 + 8 wave, and `room` windows of the lane's half-row lie inside the image
+            const int64_t first =
+                (((int64_t)bd.img * a.win_rows + bd.wr0 + i) * a.win_cols + bd.wc0 + 8 * wave) * a.n + col0;
+            const int32_t room = a.win_cols - bd.wc0 - 8 * wave - half;
+            auto put = [&](int q, const float best[2], const int winner[2]) {
+                if (2 * q >= room) return;
+                *reinterpret_cast<float2 *>(a.pooled + first + 2 * q * a.n + lane_out) = make_float2(best[0], best[1]);
+                *reinterpret_cast<uint16_t *>(a.argmax + first + 2 * q * a.n + lane_out) =
+                    (uint16_t)(winner[0] | (winner[1] << 8));
+            };
+            if (__builtin_amdgcn_ballot_w64(most >= 0x7f800000) == 0) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    float best[2];
+                    int winner[2];
+#pragma unroll
+                    for (int b = 0; b < 2; ++b) {
+                        const int32_t m = top[b][q];
+                        best[b] = __int_as_float(m > 0 ? m : 0);
+                        int w = __float_as_int(acc[b][4 * q + 2]) == m ? 2 : 3;
+                        w = __float_as_int(acc[b][4 * q + 1]) == m ? 1 : w;
+                        winner[b] = (m <= 0 || __float_as_int(acc[b][4 * q]) == m) ? 0 : w;
+                    }
+                    put(q, best, winner);
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    float best[2];
+                    int winner[2];
+#pragma unroll
+                    for (int b = 0; b < 2; ++b) {
+                        float y[4];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) y[e] = acc[b][4 * q + e];
+                        relu_pool_window4(y, best[b], winner[b]);
+                    }
+                    put(q, best, winner);
+                }
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0);  // the next band's cells have landed
+        __syncthreads();                // ... for every wave, and this band's reads are done
+    };
+    while (band < bands) {
+        run(band, std::integral_constant<int, 0>{});
+        band += gridDim.x;
+        if (band >= bands) break;
+        run(band, std::integral_constant<int, 1>{});
+        band += gridDim.x;
+    }
+}
+
+// Weight and bias gradient through ReLU -> 2x2 max pool (small_conv_pool_wgrad_kernel) over bands
+// of 1 x 32 windows.  Per band the LDS buffer holds the gradient and the pooled values
+// [32 windows][64 columns], the winner bytes [32][64] and the input planes.  MFMA row r of column
+// block nb is output column 4 r + nb, so a lane reads its four columns' values with one 16-byte
+// read; A operand of lane (r, pixel p) = g where the winner byte is p and the pooled value is
+// positive, else 0.  Wave w takes windows w, w + 4, ... of each band, as the generic kernel does.
+template <int C, int KH, int KW>
+__global__ void __launch_bounds__(256, 3) small_conv_pool_wgrad_fixed_kernel(SmallConvArgs a,
+                                                                               const float *__restrict__ g,
+                                                                               const float *__restrict__ pooled,
+                                                                               const uint8_t *__restrict__ argmax,
+                                                                               float *__restrict__ partial) {
+    // rows 68 cells apart (4 banks), planes 332 (12 banks): the 16 terms x 2 pixels of a half-wave
+    // read fall in distinct banks or share a cell
+    using F = Fixed<C, KH, KW, 1, 68, 332>;
+    constexpr int W = F::BS;                        // windows per band
+    constexpr int GP = W * 64;                      // floats of the band's gradient (and pooled values)
+    constexpr int XO = 2 * GP + W * 16;             // the input planes, after the winner bytes
+    constexpr int BUF = XO + F::XBUF;
+    static_assert(2 * BUF >= 4 * 32 * 64, "the four waves' sums fit the buffers");
+    __shared__ __attribute__((aligned(16))) float lds[2 * BUF];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int nl = lane & 15, pos = lane >> 4;
+    const int32_t col0 = (int32_t)blockIdx.y * 64;
+
+    for (int32_t t = tid; t < F::PLANE; t += 256) {
+        lds[XO + C * F::PLANE + t] = 1.0f;
+        lds[BUF + XO + C * F::PLANE + t] = 1.0f;
+    }
+    StripStream<F> stream;
+    stream.init(a, tid);
+    const int wave = stream.wave;
+    // Gradient and pooled loads e = wave, wave + 4 (16 bytes per lane): window 4 e + lane / 16,
+    // columns col0 + 4 (lane % 16) ..; winner loads e = wave < 2: window 16 e + lane / 4, bytes
+    // col0 + 16 (lane % 4) ..
+    int32_t gwin[2];
+    uint32_t grel[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        gwin[s] = 4 * (wave + 4 * s) + (lane >> 4);
+        grel[s] = (uint32_t)((gwin[s] * a.n + col0 + 4 * (lane & 15)) * 4);
+    }
+    const int32_t awin = 16 * wave + (lane >> 2);
+    const uint32_t arel = (uint32_t)(awin * a.n + col0 + 16 * (lane & 3));
+    // B operand cells: the lane's two terms (nl, nl + 16) at pixel pos of a window
+    const int32_t lane_px = (pos >> 1) * F::SW + (pos & 1) + 2 * wave;
+    int32_t xoff[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+        const int t = nl + 16 * kb;
+        xoff[kb] = XO + lane_px + F::off(t);
+    }
+    const uint32_t bands = (uint32_t)a.bands;
+
+    auto load = [&](const Band &b, float *buf) {
+        const int64_t first = (((int64_t)b.img * a.win_rows + b.wr0) * a.win_cols + b.wc0) * a.n;
+        const int32_t room = a.win_cols - b.wc0;  // windows of the band inside the image
+        const __amdgpu_buffer_rsrc_t rg = rsrc_of(uniform_ptr(g + first));
+        const __amdgpu_buffer_rsrc_t rp = rsrc_of(uniform_ptr(pooled + first));
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const uint32_t off = gwin[s] < room ? grel[s] : kOutside;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rg, (lds_void)(buf + 256 * (wave + 4 * s)), 16, off, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rp, (lds_void)(buf + GP + 256 * (wave + 4 * s)), 16, off, 0, 0,
+                                                     0);
+        }
+        if (wave < 2) {
+            const __amdgpu_buffer_rsrc_t ra = rsrc_of(uniform_ptr(argmax + first));
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void)(buf + 2 * GP + 256 * wave), 16,
+                                                     awin < room ? arel : kOutside, 0, 0, 0);
+        }
+        stream.load(a, b, buf + XO);
+    };
+
+    floatx4 acc[4][2];
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) acc[nb][kb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    uint32_t band = blockIdx.x;
+    if (band < bands) load(decode_band(a, band), lds);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+
+    auto run = [&](uint32_t bnd, auto parity) {
+        constexpr int P = decltype(parity)::value;
+        if (bnd + gridDim.x < bands) load(decode_band(a, bnd + gridDim.x), lds + (P ^ 1) * BUF);
+        const float *gv = lds + P * BUF + 64 * wave + 4 * nl;
+        const uint8_t *av = reinterpret_cast<const uint8_t *>(lds + P * BUF + 2 * GP) + 64 * wave + 4 * nl;
+        const float *xv[2] = {lds + P * BUF + xoff[0], lds + P * BUF + xoff[1]};
+        const uint32_t match = 0x01010101u * (uint32_t)pos;
+#pragma unroll
+        for (int i = 0; i < W / 4; i += 2) {  // windows wave + 4 i and wave + 4 i + 4
+            floatx4 g4[2], p4[2];
+            uint32_t a4[2];
+            float x[2][2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int w4 = 4 * (i + h);  // window offset from the wave's first window
+                g4[h] = *reinterpret_cast<const floatx4 *>(gv + 64 * w4);
+                p4[h] = *reinterpret_cast<const floatx4 *>(gv + GP + 64 * w4);
+                a4[h] = *reinterpret_cast<const uint32_t *>(av + 64 * w4) ^ match;
+                x[h][0] = xv[0][2 * w4];
+                x[h][1] = xv[1][2 * w4];
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int nb = 0; nb < 4; ++nb) {
+                    const float d = ((a4[h] >> (8 * nb)) & 0xffu) == 0 && p4[h][nb] > 0.0f ? g4[h][nb] : 0.0f;
+                    acc[nb][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(d, x[h][0], acc[nb][0], 0, 0, 0);
+                    acc[nb][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(d, x[h][1], acc[nb][1], 0, 0, 0);
+                }
+        }
+        __builtin_amdgcn_s_waitcnt(0);  // the next band has landed
+        __syncthreads();                // ... for every wave, and this band's reads are done
+    };
+    while (band < bands) {
+        run(band, std::integral_constant<int, 0>{});
+        band += gridDim.x;
+        if (band >= bands) break;
+        run(band, std::integral_constant<int, 1>{});
+        band += gridDim.x;
+    }
+
+    // The four waves' sums meet in LDS ([wave][term][64 columns]) and are added in wave order.  D
+    // register v of lane l in block (nb, kb): term 16 kb + l % 16, column 16 (l / 16) + 4 v + nb.
+    float *const red = lds;
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) red[(wave * 32 + nl + 16 * kb) * 64 + 16 * pos + 4 * v + nb] = acc[nb][kb][v];
+    __syncthreads();
+    float *dst = partial + (int64_t)blockIdx.x * 32 * a.n;
+    for (int32_t e = tid; e < 32 * 64; e += 256) {
+        const int32_t t = e >> 6, col = col0 + (e & 63);
+        const float sum = ((red[e] + red[2048 + e]) + red[4096 + e]) + red[6144 + e];
+        dst[(int64_t)t * a.n + col] = sum;
+    }
+}
+
 // Windows per band: S columns (a multiple of 8, at most 32; windows past the image are skipped)
 // by R rows, R * S <= cap, with at most 512 staged cells (rows x columns), the capacity of the
 // threads' prefetch registers.
@@ -477,11 +880,27 @@ size_t gradient_bytes(const SmallConvArgs &a) {
     return sizeof(float) * (expansion > 4 * 32 * 64 ? expansion : 4 * 32 * 64);
 }
 
-unsigned persistent_blocks(axis_device device, int64_t bands, int64_t columns) {
-    const int64_t slots = (int64_t)device->multiprocessors * 4 / (columns > 0 ? columns : 1);
+unsigned persistent_blocks(axis_device device, int64_t bands, int64_t columns, int per_cu = 4) {
+    const int64_t slots = (int64_t)device->multiprocessors * per_cu / (columns > 0 ? columns : 1);
     int64_t per = (bands + (slots > 0 ? slots : 1) - 1) / (slots > 0 ? slots : 1);
     if (per < 1) per = 1;
     return (unsigned)((bands + per - 1) / per);
+}
+
+// The fixed-geometry instances: a 3x3 kernel over 1 or 3 channels, bands of `rows` x 32 windows,
+// whole 64-column groups, and every input cell's byte offset (and the band corners') within 31 bits.
+bool fixed_applies(const SmallConvArgs &a, int32_t rows) {
+    if (a.kh != 3 || a.kw != 3 || (a.c_in != 1 && a.c_in != 3)) return false;
+    if (a.band_s != 32 || a.band_r != rows || a.n % 64 != 0) return false;
+    if (a.ld_h < 0 || a.ld_w < 0 || a.ld_c < 0) return false;
+    const int64_t reach = ((int64_t)a.height + 8) * a.ld_h + ((int64_t)a.width + 72) * a.ld_w + (int64_t)a.c_in * a.ld_c;
+    return reach * 4 < ((int64_t)1 << 31);
+}
+
+template <int C>
+int launch_pool_forward_fixed(axis_device device, const SmallConvArgs &a, dim3 grid) {
+    small_conv_pool_forward_fixed_kernel<C, 3, 3><<<grid, 256, 0, device->stream>>>(a);
+    return axis::launch_status("small_conv_pool_forward_fixed_kernel");
 }
 
 template <bool POOL>
@@ -489,6 +908,8 @@ int launch_forward(axis_device device, const SmallConvArgs &a) {
     const int kp = (a.k + 2) / 2;  // the k terms and the bias term
     const unsigned columns = (unsigned)((a.n + 63) / 64);
     dim3 grid(persistent_blocks(device, a.bands, columns), columns);
+    if (POOL && a.wide && fixed_applies(a, 2))
+        return a.c_in == 3 ? launch_pool_forward_fixed<3>(device, a, grid) : launch_pool_forward_fixed<1>(device, a, grid);
     const size_t lds = strip_bytes(a, 2);
     hipStream_t st = device->stream;
 #define AXIS_SMALL_FWD(KPV)                                                      \
@@ -548,14 +969,24 @@ int small_conv_pool_backward_weight(axis_device device, const SmallConvShape &s,
     a.vec = (a.n & 3) == 0 && aligned16(gradient) && aligned16(pooled) &&
             (reinterpret_cast<uintptr_t>(argmax) & 3) == 0;
     const unsigned columns = (unsigned)((a.n + 63) / 64);
-    const unsigned blocks = persistent_blocks(device, a.bands, columns);
+    const bool fixed = a.vec && aligned16(argmax) && fixed_applies(a, 1);
+    const unsigned blocks = persistent_blocks(device, a.bands, columns, fixed ? 3 : 4);
     Scratch partial;
     if (int st = partial.get(device, sizeof(float) * (size_t)blocks * 32 * (size_t)a.n)) return st;
     const size_t lds = strip_bytes(a, 1) + gradient_bytes(a);
     {
         TimedLaunch timed(device, "gemm", 2.0 * (double)s.batch * s.out_h * s.out_w * s.out_channels * a.k);
-        small_conv_pool_wgrad_kernel<<<dim3(blocks, columns), 256, lds, device->stream>>>(a, gradient, pooled, argmax,
-                                                                                          partial.as<float>());
+        const dim3 grid(blocks, columns);
+        if (fixed && a.c_in == 3) {
+            small_conv_pool_wgrad_fixed_kernel<3, 3, 3><<<grid, 256, 0, device->stream>>>(a, gradient, pooled, argmax,
+                                                                                            partial.as<float>());
+        } else if (fixed) {
+            small_conv_pool_wgrad_fixed_kernel<1, 3, 3><<<grid, 256, 0, device->stream>>>(a, gradient, pooled, argmax,
+                                                                                            partial.as<float>());
+        } else {
+            small_conv_pool_wgrad_kernel<<<grid, 256, lds, device->stream>>>(a, gradient, pooled, argmax,
+                                                                              partial.as<float>());
+        }
         if (int st = launch_status("small_conv_pool_wgrad_kernel")) return st;
     }
     // d_weight[t][n] (t < k) and d_bias[n] (t = k) = the sum over blocks of partial[block][t][n]

@@ -954,6 +954,77 @@ def test_conv2d_relu_pool_forward(dev, oracle, case):
         assert np.array_equal(dev.read(a2, pooled_len, np.uint8), got_arg)
 
 
+FIXED_GEOMETRY_CASES = [
+    # layout, b, c, h, w, n: 3x3 under padding 1 over 1 or 3 channels, windows at least 25 columns
+    # wide, whole 64-column groups -- the shapes the fixed-geometry kernels take
+    ("nchw", 2, 3, 64, 64, 64),   # conv1 of the CNN
+    ("nchw", 1, 3, 14, 72, 128),  # 36 windows per row (a partial second band), 7 window rows, two groups
+    ("nhwc", 2, 1, 50, 52, 64),   # one channel, 26 windows per row (a partial band), 25 window rows
+]
+
+
+@pytest.mark.parametrize("values", ["normal", "ties", "special"])
+@pytest.mark.parametrize("case", range(len(FIXED_GEOMETRY_CASES)))
+def test_conv2d_relu_pool_forward_fixed_geometry(dev, oracle, case, values):
+    """The fused forward on the fixed-geometry kernels is bit-identical to the separate GPU entries
+    (plain convolution, ReLU, max pool; the pool rule is bit-exact against the oracle in
+    test_relu_pool_backward_bit_exact and its neighbours) on both pooling paths: the bit-pattern
+    comparison ("normal", "ties": exact integer pre-activations with tied maxima, zeros and
+    all-negative windows) and the exact scan that tiles holding +inf or NaN take ("special")."""
+    layout, b, c, h, w, n = FIXED_GEOMETRY_CASES[case]
+    k = 3
+    rng = np.random.default_rng(90 + case)
+    size = b * c * h * w
+    if values == "ties":
+        x = rng.integers(-2, 3, size).astype(np.float32)
+        weight = rng.integers(-1, 2, c * k * k * n).astype(np.float32)
+        bias = rng.integers(-1, 2, n).astype(np.float32)
+    else:
+        x = rng.standard_normal(size).astype(np.float32)
+        weight = rng.standard_normal(c * k * k * n).astype(np.float32) * 0.2
+        bias = rng.standard_normal(n).astype(np.float32) * 0.1
+    if values == "special":
+        cells = rng.choice(size, 30, replace=False)
+        x[cells[:10]], x[cells[10:20]], x[cells[20:]] = np.nan, np.inf, -np.inf
+    if layout == "nchw":
+        dims = [("batch", b), ("c", c), ("height", h), ("width", w)]
+        strides = (I64 * 4)(c * h * w, h * w, w, 1)
+    else:
+        dims = [("batch", b), ("height", h), ("width", w), ("c", c)]
+        strides = None
+    geo = [(I32 * 2)(k, k), (I32 * 2)(1, 1), (I32 * 2)(1, 1)]
+    pooled_len = b * (h // 2) * (w // 2) * n
+    dx, dw, db = up(dev, x), up(dev, weight), up(dev, bias)
+    pooled, arg = dev.empty(pooled_len), dev.empty(pooled_len, np.uint8)
+    dev.call("axis_conv2d_relu_pool_forward", dx.vp, strides, dw.vp, db.vp, pooled.vp, arg.vp, I64(b), I32(h),
+             I32(w), I32(c), I32(n), *geo, (I32 * 2)(2, 2))
+    got, got_arg = dev.read(pooled, pooled_len), dev.read(arg, pooled_len, np.uint8)
+    zz, yy = dev.empty(b * h * w * n), dev.empty(b * h * w * n)
+    dev.call("axis_conv2d_forward", dx.vp, strides, dw.vp, db.vp, zz.vp, I64(b), I32(h), I32(w), I32(c), I32(n),
+             *geo)
+    dev.call("axis_relu", zz.vp, yy.vp, I64(b * h * w * n))
+    p2, a2 = dev.empty(pooled_len), dev.empty(pooled_len, np.uint8)
+    dev.call("axis_max_pool2d", yy.vp, p2.vp, a2.vp, I64(b), I32(h), I32(w), I64(n), (I32 * 2)(2, 2),
+             (I32 * 2)(2, 2), (I32 * 2)(0, 0))
+    want, want_arg = dev.read(p2, pooled_len), dev.read(a2, pooled_len, np.uint8)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+    assert np.array_equal(got_arg, want_arg)
+    if values == "ties":
+        z = dev.read(zz, b * h * w * n)
+        wins = _windows(z, b, h, w, n, 2, 2).reshape(pooled_len, 4)
+        tied = ((wins == wins.max(axis=1, keepdims=True)).sum(axis=1) > 1) & (wins.max(axis=1) > 0)
+        assert tied.mean() > 0.05 and (wins.max(axis=1) <= 0).mean() > 0.05  # both cases are exercised
+    if values == "special":
+        assert 0 < nan.sum() and np.isinf(got).sum() == 0  # +inf outputs have no finite winner: NaN
+        assert (~np.isfinite(dev.read(zz, b * h * w * n))).any()
+    if values == "normal":
+        z, _ = _oracle_conv(oracle, x, weight, bias, dims, b, c, n, k, 1, 1, h, w)
+        ref, _ = _first_max(_windows(np.where(z > 0, z, np.float32(0)), b, h, w, n, 2, 2))
+        assert np.abs(got - ref.reshape(-1)).max() <= 1e-5 * np.abs(z).max()
+
+
 def test_conv2d_relu_pool_rejects_partial_windows(dev):
     buf = dev.empty(4096)
     arg = dev.empty(4096, np.uint8)
@@ -974,6 +1045,10 @@ RELU_POOL_WGRAD_CASES = [
     ("nchw", 2, 1, 10, 70, 32, 1, False),   # 35 windows per row: two bands across; no bias
     ("nchw", 2, 3, 18, 18, 64, 0, True),    # no padding
     ("nhwc", 2, 8, 8, 8, 16, 1, True),      # 72-term reduction: composed from the separate entries
+    # the fixed-geometry kernel: 3x3 over 1 or 3 channels, windows >= 25 columns, 64-column groups
+    ("nchw", 1, 3, 14, 72, 128, 1, True),   # 36 windows per row: a partial second band; two groups
+    ("nhwc", 2, 1, 50, 52, 64, 1, False),   # one channel, 26 windows per row (a partial band)
+    ("nchw", 2, 3, 66, 66, 64, 0, True),    # no padding
 ]
 
 
