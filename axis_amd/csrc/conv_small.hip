@@ -673,19 +673,23 @@ __global__ void __launch_bounds__(256, 4) small_conv_pool_forward_fixed_kernel(S
 
 // Weight and bias gradient through ReLU -> 2x2 max pool (small_conv_pool_wgrad_kernel) over bands
 // of 1 x 32 windows.  Per band the LDS buffer holds the gradient and the pooled values
-// [32 windows][64 columns], the winner bytes [32][64] and the input planes.  MFMA row r of column
-// block nb is output column 4 r + nb, so a lane reads its four columns' values with one 16-byte
-// read; A operand of lane (r, pixel p) = g where the winner byte is p and the pooled value is
-// positive, else 0.  Wave w takes windows w, w + 4, ... of each band, as the generic kernel does.
+// [32 windows][64 columns], the winner bytes [32][64] and the input planes.  Wave w takes windows
+// 8w .. 8w + 7 of each band as two quads of four windows, and the reduction step of one
+// v_mfma_f32_16x16x4_f32 is one pixel position p of the quad's four windows (k = window in the
+// quad): MFMA row r of column block nb is output column 4 r + nb, so lane (r, k) reads its own
+// window's four gradient, pooled and winner values once per quad with 16- and 4-byte reads, and
+// its A operand at position p is g where the winner byte is p and the pooled value positive,
+// else 0.  The sums run window quad by window quad, position by position (deterministic; not the
+// generic kernel's window-major order).
 template <int C, int KH, int KW>
 __global__ void __launch_bounds__(256, 3) small_conv_pool_wgrad_fixed_kernel(SmallConvArgs a,
                                                                                const float *__restrict__ g,
                                                                                const float *__restrict__ pooled,
                                                                                const uint8_t *__restrict__ argmax,
                                                                                float *__restrict__ partial) {
-    // rows 68 cells apart (4 banks), planes 332 (12 banks): the 16 terms x 2 pixels of a half-wave
+    // rows 69 cells apart (5 banks), planes 335 (15 banks): the 16 terms x 2 windows of a half-wave
     // read fall in distinct banks or share a cell
-    using F = Fixed<C, KH, KW, 1, 68, 332>;
+    using F = Fixed<C, KH, KW, 1, 69, 335>;
     constexpr int W = F::BS;                        // windows per band
     constexpr int GP = W * 64;                      // floats of the band's gradient (and pooled values)
     constexpr int XO = 2 * GP + W * 16;             // the input planes, after the winner bytes
@@ -693,7 +697,7 @@ __global__ void __launch_bounds__(256, 3) small_conv_pool_wgrad_fixed_kernel(Sma
     static_assert(2 * BUF >= 4 * 32 * 64, "the four waves' sums fit the buffers");
     __shared__ __attribute__((aligned(16))) float lds[2 * BUF];
     const int tid = threadIdx.x, lane = tid & 63;
-    const int nl = lane & 15, pos = lane >> 4;
+    const int nl = lane & 15, wq = lane >> 4;  // MFMA row r = nl; k = window wq of a quad
     const int32_t col0 = (int32_t)blockIdx.y * 64;
 
     for (int32_t t = tid; t < F::PLANE; t += 256) {
@@ -715,14 +719,12 @@ __global__ void __launch_bounds__(256, 3) small_conv_pool_wgrad_fixed_kernel(Sma
     }
     const int32_t awin = 16 * wave + (lane >> 2);
     const uint32_t arel = (uint32_t)(awin * a.n + col0 + 16 * (lane & 3));
-    // B operand cells: the lane's two terms (nl, nl + 16) at pixel pos of a window
-    const int32_t lane_px = (pos >> 1) * F::SW + (pos & 1) + 2 * wave;
+    // the lane's window of a quad: 8 wave + 4 q + wq; B operand cells of its two terms (nl, nl + 16)
+    // at the window's first pixel
+    const int32_t lane_win = 8 * wave + wq;
     int32_t xoff[2];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-        const int t = nl + 16 * kb;
-        xoff[kb] = XO + lane_px + F::off(t);
-    }
+    for (int kb = 0; kb < 2; ++kb) xoff[kb] = XO + 2 * lane_win + F::off(nl + 16 * kb);
     const uint32_t bands = (uint32_t)a.bands;
 
     auto load = [&](const Band &b, float *buf) {
@@ -759,32 +761,31 @@ __global__ void __launch_bounds__(256, 3) small_conv_pool_wgrad_fixed_kernel(Sma
     auto run = [&](uint32_t bnd, auto parity) {
         constexpr int P = decltype(parity)::value;
         if (bnd + gridDim.x < bands) load(decode_band(a, bnd + gridDim.x), lds + (P ^ 1) * BUF);
-        const float *gv = lds + P * BUF + 64 * wave + 4 * nl;
-        const uint8_t *av = reinterpret_cast<const uint8_t *>(lds + P * BUF + 2 * GP) + 64 * wave + 4 * nl;
+        const float *gv = lds + P * BUF + 64 * lane_win + 4 * nl;
+        const uint8_t *av = reinterpret_cast<const uint8_t *>(lds + P * BUF + 2 * GP) + 64 * lane_win + 4 * nl;
         const float *xv[2] = {lds + P * BUF + xoff[0], lds + P * BUF + xoff[1]};
-        const uint32_t match = 0x01010101u * (uint32_t)pos;
 #pragma unroll
-        for (int i = 0; i < W / 4; i += 2) {  // windows wave + 4 i and wave + 4 i + 4
-            floatx4 g4[2], p4[2];
-            uint32_t a4[2];
-            float x[2][2];
+        for (int q = 0; q < 2; ++q) {  // windows 8 wave + 4 q + (0 .. 3)
+            const floatx4 g4 = *reinterpret_cast<const floatx4 *>(gv + 256 * q);
+            const floatx4 p4 = *reinterpret_cast<const floatx4 *>(gv + GP + 256 * q);
+            const uint32_t a4 = *reinterpret_cast<const uint32_t *>(av + 256 * q);
+            float x[4][2];
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int w4 = 4 * (i + h);  // window offset from the wave's first window
-                g4[h] = *reinterpret_cast<const floatx4 *>(gv + 64 * w4);
-                p4[h] = *reinterpret_cast<const floatx4 *>(gv + GP + 64 * w4);
-                a4[h] = *reinterpret_cast<const uint32_t *>(av + 64 * w4) ^ match;
-                x[h][0] = xv[0][2 * w4];
-                x[h][1] = xv[1][2 * w4];
-            }
+            for (int p = 0; p < 4; ++p)
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) x[p][kb] = xv[kb][8 * q + (p >> 1) * F::SW + (p & 1)];
+            // the position whose pre-activation takes column 4 nl + nb's gradient (none: 255)
+            uint32_t key[4];
+#pragma unroll
+            for (int nb = 0; nb < 4; ++nb) key[nb] = p4[nb] > 0.0f ? (a4 >> (8 * nb)) & 0xffu : 0xffu;
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int h = 0; h < 2; ++h)
+            for (int p = 0; p < 4; ++p)
 #pragma unroll
                 for (int nb = 0; nb < 4; ++nb) {
-                    const float d = ((a4[h] >> (8 * nb)) & 0xffu) == 0 && p4[h][nb] > 0.0f ? g4[h][nb] : 0.0f;
-                    acc[nb][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(d, x[h][0], acc[nb][0], 0, 0, 0);
-                    acc[nb][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(d, x[h][1], acc[nb][1], 0, 0, 0);
+                    const float d = key[nb] == (uint32_t)p ? g4[nb] : 0.0f;
+                    acc[nb][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(d, x[p][0], acc[nb][0], 0, 0, 0);
+                    acc[nb][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(d, x[p][1], acc[nb][1], 0, 0, 0);
                 }
         }
         __builtin_amdgcn_s_waitcnt(0);  // the next band has landed
@@ -806,7 +807,7 @@ __global__ void __launch_bounds__(256, 3) small_conv_pool_wgrad_fixed_kernel(Sma
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) red[(wave * 32 + nl + 16 * kb) * 64 + 16 * pos + 4 * v + nb] = acc[nb][kb][v];
+            for (int v = 0; v < 4; ++v) red[(wave * 32 + nl + 16 * kb) * 64 + 16 * wq + 4 * v + nb] = acc[nb][kb][v];
     __syncthreads();
     float *dst = partial + (int64_t)blockIdx.x * 32 * a.n;
     for (int32_t e = tid; e < 32 * 64; e += 256) {
