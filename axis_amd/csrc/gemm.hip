@@ -729,7 +729,11 @@ __global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
             }
             // The operands of the next k-quad are read before this quad's MFMAs issue, and the
             // scheduling barriers keep that order: each LDS read has a whole MFMA group to land
-            // (left to itself the compiler sinks every read to just before its use).
+            // (left to itself the compiler sinks every read to just before its use).  A wave
+            // issuing a quad's MFMAs runs at raised priority, so the SIMD's arbiter feeds the matrix
+            // pipe before the other block's loads, stores and address arithmetic (the large
+            // convolution products -1% to -5%; the held quads below stay at normal priority, where
+            // raising it cost 3-6%).
 #pragma unroll
             for (int q = 0; q < kQuads - 2; ++q) {
                 const int cur = q & 1;
@@ -740,7 +744,9 @@ __global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
                     read_operands(4 * (kQuads - 1), hold_a[1], hold_b[1]);
                 }
                 __builtin_amdgcn_sched_barrier(0);
+                __builtin_amdgcn_s_setprio(1);
                 mma_quad(av[cur], bv[cur]);
+                __builtin_amdgcn_s_setprio(0);
                 __builtin_amdgcn_sched_barrier(0);
             }
             // After the last step the stores, the barrier and the reads below handle stale
