@@ -709,6 +709,14 @@ __global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
     // two 128x128, three 128x64 or four 64x64 blocks per CU).
     constexpr int kQuads = BK / 4;
     static_assert(kQuads >= 3, "the held-quad schedule needs three k-quads per stage");
+    // Wave priority while a stage's k-quads issue their MFMAs and while the two held quads do, per
+    // tile shape (measured on the CNN's convolution products and config 2's 4096^3 and skinny
+    // products): the SIMD's arbiter then feeds the matrix pipe before the co-resident blocks'
+    // loads, stores and address arithmetic.  128-row tiles: quads at 1, held quads at 0 (held at 1
+    // cost 3-6%); 64x128 tiles (three blocks per CU): quads at 2, held at 1; 64x64 tiles (four per
+    // CU): no change, which the skinny products lost 1-3% to.
+    constexpr int kQuadPrio = (BM == 64 && BN == 64) ? 0 : (BM == 64 && BN == 128) ? 2 : 1;
+    constexpr int kHeldPrio = (BM == 64 && BN == 128) ? 1 : 0;
     // The K loop in two forms for dense products: every step whole (the depth tests of
     // r-contiguous operands compiled out) or a partial last step; a launch takes one.
     // Convolution launches keep one form (their dense operand is bounded by the record count).
@@ -729,11 +737,7 @@ __global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
             }
             // The operands of the next k-quad are read before this quad's MFMAs issue, and the
             // scheduling barriers keep that order: each LDS read has a whole MFMA group to land
-            // (left to itself the compiler sinks every read to just before its use).  A wave
-            // issuing a quad's MFMAs runs at raised priority, so the SIMD's arbiter feeds the matrix
-            // pipe before the other block's loads, stores and address arithmetic (the large
-            // convolution products -1% to -5%; the held quads below stay at normal priority, where
-            // raising it cost 3-6%).
+            // (left to itself the compiler sinks every read to just before its use).
 #pragma unroll
             for (int q = 0; q < kQuads - 2; ++q) {
                 const int cur = q & 1;
@@ -744,9 +748,9 @@ __global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
                     read_operands(4 * (kQuads - 1), hold_a[1], hold_b[1]);
                 }
                 __builtin_amdgcn_sched_barrier(0);
-                __builtin_amdgcn_s_setprio(1);
+                if constexpr (kQuadPrio > 0) __builtin_amdgcn_s_setprio(kQuadPrio);
                 mma_quad(av[cur], bv[cur]);
-                __builtin_amdgcn_s_setprio(0);
+                if constexpr (kQuadPrio > 0) __builtin_amdgcn_s_setprio(0);
                 __builtin_amdgcn_sched_barrier(0);
             }
             // After the last step the stores, the barrier and the reads below handle stale
@@ -754,11 +758,15 @@ __global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
             __syncthreads();  // every wave is done reading this stage
             lx.store(xs, tid, bf16);
             ly.store(ys, tid, bf16);
+            if constexpr (kHeldPrio > 0) __builtin_amdgcn_s_setprio(kHeldPrio);
             mma_quad(hold_a[0], hold_b[0]);
+            if constexpr (kHeldPrio > 0) __builtin_amdgcn_s_setprio(0);
             __builtin_amdgcn_sched_barrier(0);
             __syncthreads();  // the next stage is in LDS
             read_operands(0, av[0], bv[0]);
+            if constexpr (kHeldPrio > 0) __builtin_amdgcn_s_setprio(kHeldPrio);
             mma_quad(hold_a[1], hold_b[1]);
+            if constexpr (kHeldPrio > 0) __builtin_amdgcn_s_setprio(0);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
