@@ -31,6 +31,10 @@ struct axis_device_s {
     // Device::cuda_bf16 (backend.rs:274-283): matrix products take bf16-rounded operands and
     // accumulate in fp32; everything else stays fp32.
     bool bf16_matmul = false;
+    // Short split-K products over few tiles run their slices in one block's waves (gemm.hip,
+    // gemm_fold_kernel); AXIS_GEMM_UNFOLDED set at creation keeps them as separate slices plus a
+    // sum launch (the same bits, for comparison).
+    bool fold_splits = true;
     // launch timing (axis_timing_*): event pairs and work per family
     bool timing = false;
     struct Timed {

@@ -1,6 +1,7 @@
 // Device handle, caching allocator, host<->device copies, CSR plan upload
 // (runtime/backend.rs:203-392, :1449-1475, :1542-1597).
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -166,6 +167,7 @@ int axis_device_create(int ordinal, axis_device *out) {
     auto *device = new axis_device_s();
     device->ordinal = ordinal;
     device->multiprocessors = prop.multiProcessorCount;
+    device->fold_splits = std::getenv("AXIS_GEMM_UNFOLDED") == nullptr;
     hipError_t e = hipStreamCreateWithFlags(&device->stream, hipStreamNonBlocking);
     if (e != hipSuccess) {
         delete device;

@@ -175,18 +175,23 @@ __device__ __forceinline__ void buffer_into(float *reg, __amdgpu_buffer_rsrc_t r
 // of one row per lane) stay single 16- or 8-byte reads, and one k-quad (4 rows) shares one
 // swizzle.  It spreads the transposing stores of r-contiguous operands (a lane writes rows
 // 4j..4j+3 of one column) over distinct banks.
-__device__ __forceinline__ constexpr int stage_swizzle(int r) { return 8 * ((r >> 2) & 7); }
+// Tiles 32 wide (the folded products) permute inside their 32 columns: swizzle(r) = 8 * ((r / 4) % 4).
+template <int BT>
+__device__ __forceinline__ constexpr int stage_swizzle(int r) {
+    return 8 * ((r >> 2) & (BT >= 64 ? 7 : 3));
+}
 
 template <int BT, int BK, int NT, bool RCONTIG, int VEC>
 struct Staging {
-    static_assert(BT % 64 == 0, "the swizzle permutes columns inside aligned groups of 64");
+    static_assert(BT % 64 == 0 || BT == 32, "the swizzle permutes columns inside aligned groups of 64 (or 32)");
     static constexpr int kElems = BT * BK / NT;  // floats per thread
     static constexpr int kVecs = kElems / VEC;
     // Row pitch: t-contiguous operands BT + 4 (their 16-byte stores along t spread over the banks
     // by the padding); r-contiguous ones BT + 64, a multiple of 64 words, so the four rows a lane
     // writes sit 3 x 256 bytes apart and two ds_write2st64 reach them from one address register
     // (the XOR swizzle alone keeps those stores and the operand reads free of bank conflicts).
-    static constexpr int LD = RCONTIG ? BT + 64 : BT + 4;
+    // 32-wide tiles (the folded products' four stages share one CU's LDS): BT + 4 for both.
+    static constexpr int LD = RCONTIG && BT >= 64 ? BT + 64 : BT + 4;
     static constexpr int kPer = RCONTIG ? BK / VEC : BT / VEC;  // vectors per contiguous line
     float reg[kElems];
 
@@ -203,15 +208,15 @@ struct Staging {
                 const int rr = (idx % kPer) * VEC;
                 const int tt = idx / kPer;
 #pragma unroll
-                for (int c = 0; c < VEC; ++c) lds[(rr + c) * LD + (tt ^ stage_swizzle(rr + c))] = reg[e * VEC + c];
+                for (int c = 0; c < VEC; ++c) lds[(rr + c) * LD + (tt ^ stage_swizzle<BT>(rr + c))] = reg[e * VEC + c];
             } else {
                 const int tt = (idx % kPer) * VEC;
                 const int rr = idx / kPer;
                 if (VEC == 4) {
                     floatx4 v = {reg[e * 4 + 0], reg[e * 4 + 1], reg[e * 4 + 2], reg[e * 4 + 3]};
-                    *reinterpret_cast<floatx4 *>(lds + rr * LD + (tt ^ stage_swizzle(rr))) = v;
+                    *reinterpret_cast<floatx4 *>(lds + rr * LD + (tt ^ stage_swizzle<BT>(rr))) = v;
                 } else {
-                    lds[rr * LD + (tt ^ stage_swizzle(rr))] = reg[e];
+                    lds[rr * LD + (tt ^ stage_swizzle<BT>(rr))] = reg[e];
                 }
             }
         }
@@ -586,14 +591,24 @@ using axis::finish_value;
 // pixel steps, 4 rows mode through buffer loads.
 // EPI: 0 store C (+ bias), 1 bias + ReLU + max pool of whole windows (rows are output pixels).
 // Blocks per CU the register budget is held to (two large, three tall or wide, four small tiles).
-constexpr int gemm_blocks_per_cu(int bm, int bn) {
-    return bm == 128 && bn == 128 ? 2 : bm == 128 || bn == 128 ? 3 : 4;
+// tall4: the vectorised data gradient through the gathered convolution loader (128x64 tiles), which
+// fits 128 VGPRs without spilling -- four blocks per CU, under which conv2's data gradient runs in
+// 302 us against 343 at three (the other tall instances spill at that budget).
+constexpr int gemm_blocks_per_cu(int bm, int bn, bool tall4 = false) {
+    return bm == 128 && bn == 128 ? 2 : bm == 128 && bn == 64 && tall4 ? 4 : bm == 128 || bn == 128 ? 3 : 4;
 }
 
-template <int BM, int BN, int BK, int WM, int WN, bool XR, bool YR, int VX, int VY, int XMODE, int EPI>
-__global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
-    gemm_kernel(GemmParams p) {
-    constexpr int NT = WM * WN * 64;
+// WS: waves of the block that split the reduction among them.  1: the WM x WN waves share the
+// tile and its K steps.  WS > 1 (WM = WN = 1, EPI 0): wave w computes the whole tile over slice w
+// of the launch's p.splits slices (none when w >= p.splits) through its own LDS stage, ordered by
+// its own instruction stream (no barrier inside the K loop), and the block adds the WS partial
+// tiles in the association of split_sum_part / split_sum_store: the same bits as split slices
+// summed by split_sum_kernel, without their partial buffer and second launch.
+template <int BM, int BN, int BK, int WM, int WN, bool XR, bool YR, int VX, int VY, int XMODE, int EPI, int WS>
+__device__ __forceinline__ void gemm_body(const GemmParams &p) {
+    static_assert(WS == 1 || (WS == 4 && WM == 1 && WN == 1 && EPI == 0 && XMODE == 0),
+                  "reduction split among waves: one-wave dense tiles, four slices");
+    constexpr int NT = WM * WN * 64;  // threads that stage one tile's operands
     static_assert(XMODE != 4 || BK == 32, "the buffer rows loader's tap steps are 32 deep");
     constexpr int TM = BM / WM, TN = BN / WN;
     // 16x16 MFMA blocks per wave side.  Block a of a wave holds the wave's tile rows FM*i + a
@@ -612,12 +627,15 @@ __global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
     using LY = DenseLoader<BN, BK, NT, YR, VY>;
     constexpr int kStage = BK * LX::LD + BK * LY::LD;
     constexpr int kPoolPitch = TN + 1;
-    constexpr int kEpilogue = EPI == 1 ? BM * kPoolPitch : 0;
-    __shared__ __attribute__((aligned(16))) float lds[kStage > kEpilogue ? kStage : kEpilogue];
-    float *const xs = lds;
-    float *const ys = lds + BK * LX::LD;
+    constexpr int kEpilogue = EPI == 1 ? BM * kPoolPitch : WS > 1 ? WS * BM * BN : 0;
+    constexpr int kStages = WS * kStage;
+    __shared__ __attribute__((aligned(16))) float lds[kStages > kEpilogue ? kStages : kEpilogue];
+    // the wave's reduction slice inside the block (WS > 1), and its own stage
+    const int kw = WS > 1 ? (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : 0;
+    float *const xs = lds + kw * kStage;
+    float *const ys = xs + BK * LX::LD;
 
-    const int tid = threadIdx.x;
+    const int tid = WS > 1 ? (int)(threadIdx.x & 63) : (int)threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int wm = wave % WM, wn = wave / WM;
@@ -630,11 +648,11 @@ __global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
     const uint32_t L = blockIdx.x;
     const uint32_t logical = L < 8u * p.xcd_span ? (L % 8u) * p.xcd_span + L / 8u : L;
     const uint32_t tile = logical % tiles;
-    const uint32_t slice = logical / tiles;
+    const uint32_t slice = logical / tiles;  // WS > 1: the batch index (the block holds every slice)
     const int64_t i0 = (int64_t)(tile % (uint32_t)p.tiles_m) * BM;
     const int64_t j0 = (int64_t)(tile / (uint32_t)p.tiles_m) * BN;
-    const int split = (int)(slice % (uint32_t)p.splits);
-    const int64_t batch = slice / (uint32_t)p.splits;
+    const int split = WS > 1 ? kw : (int)(slice % (uint32_t)p.splits);
+    const int64_t batch = WS > 1 ? (int64_t)slice : (int64_t)(slice / (uint32_t)p.splits);
     const int64_t r_begin = (int64_t)split * p.k_chunk;
     const int64_t r_end = r_begin + p.k_chunk < p.k ? r_begin + p.k_chunk : p.k;
 
@@ -670,7 +688,18 @@ __global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
         lx.store(xs, tid, bf16);
         ly.store(ys, tid, bf16);
     }
-    __syncthreads();
+    // Orders a stage's LDS stores and reads: the block's barrier, or with one wave per stage
+    // (WS > 1) the wave's own instruction order (its LDS operations run in issue order): a wait
+    // for its LDS operations and a compiler-only fence.
+    auto stage_sync = [&]() {
+        if constexpr (WS > 1) {
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        } else {
+            __syncthreads();
+        }
+    };
+    stage_sync();
 
     // v_mfma_f32_16x16x4_f32: lane l feeds k = l / 16 of the quad, A row i = l % 16, B column
     // j = l % 16; its result registers v hold rows 4 * (l / 16) + v of column l % 16.
@@ -678,9 +707,8 @@ __global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
     const int l16 = lane & 15;
     // MFMA operands of the k-quad starting at kk (its four rows share one swizzle).
     auto read_operands = [&](int kk, float *av, float *bv) {
-        const int sw = stage_swizzle(kk);
-        const float *xa = xs + (kk + quad) * LX::LD + ((wm * TM + FM * l16) ^ sw);
-        const float *yb = ys + (kk + quad) * LY::LD + ((wn * TN + FN * l16) ^ sw);
+        const float *xa = xs + (kk + quad) * LX::LD + ((wm * TM + FM * l16) ^ stage_swizzle<BM>(kk));
+        const float *yb = ys + (kk + quad) * LY::LD + ((wn * TN + FN * l16) ^ stage_swizzle<BN>(kk));
         if constexpr (FM == 4) {
             const floatx4 v = *reinterpret_cast<const floatx4 *>(xa);
             av[0] = v[0], av[1] = v[1], av[2] = v[2], av[3] = v[3];
@@ -715,7 +743,9 @@ __global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
     // loads, stores and address arithmetic.  128-row tiles: quads at 1, held quads at 0 (held at 1
     // cost 3-6%); 64x128 tiles (three blocks per CU): quads at 2, held at 1; 64x64 tiles (four per
     // CU): no change, which the skinny products lost 1-3% to.
-    constexpr int kQuadPrio = (BM == 64 && BN == 64) ? 0 : (BM == 64 && BN == 128) ? 2 : 1;
+    // With the reduction split among waves (one block per CU, one wave per SIMD) there is no
+    // other wave to arbitrate against.
+    constexpr int kQuadPrio = (WS > 1 || (BM == 64 && BN == 64)) ? 0 : (BM == 64 && BN == 128) ? 2 : 1;
     constexpr int kHeldPrio = (BM == 64 && BN == 128) ? 1 : 0;
     // The K loop in two forms for dense products: every step whole (the depth tests of
     // r-contiguous operands compiled out) or a partial last step; a launch takes one.
@@ -755,14 +785,14 @@ __global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
             }
             // After the last step the stores, the barrier and the reads below handle stale
             // registers and LDS nothing reads: unconditional, they keep the loop free of flag tests.
-            __syncthreads();  // every wave is done reading this stage
+            stage_sync();  // every wave is done reading this stage
             lx.store(xs, tid, bf16);
             ly.store(ys, tid, bf16);
             if constexpr (kHeldPrio > 0) __builtin_amdgcn_s_setprio(kHeldPrio);
             mma_quad(hold_a[0], hold_b[0]);
             if constexpr (kHeldPrio > 0) __builtin_amdgcn_s_setprio(0);
             __builtin_amdgcn_sched_barrier(0);
-            __syncthreads();  // the next stage is in LDS
+            stage_sync();  // the next stage is in LDS
             read_operands(0, av[0], bv[0]);
             if constexpr (kHeldPrio > 0) __builtin_amdgcn_s_setprio(kHeldPrio);
             mma_quad(hold_a[1], hold_b[1]);
@@ -786,7 +816,49 @@ __global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
     // is not split; split sums add it once at the end.
     auto row_of = [&](int a, int v) { return wm * TM + FM * (4 * quad + v) + a; };
     const int col_l = wn * TN + FN * l16;  // tile column of the lane's first column
-    if constexpr (EPI == 0) {
+    if constexpr (WS > 1) {
+        // The waves' partial tiles meet in LDS ([wave][row][column]), then each output is
+        // 0 + slice w per wave (split_sum_part's group sums, one slice per group), added in wave
+        // order and finished once (split_sum_store): the bits of the split launch and its sum.
+        __syncthreads();  // every wave is done with its stage
+        float *const red = lds + kw * BM * BN;
+#pragma unroll
+        for (int a = 0; a < FM; ++a)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                float *row = red + row_of(a, v) * BN + col_l;
+                if constexpr (FN == 4)
+                    *reinterpret_cast<floatx4 *>(row) = floatx4{acc[a][0][v], acc[a][1][v], acc[a][2][v], acc[a][3][v]};
+                else
+                    *reinterpret_cast<float2 *>(row) = make_float2(acc[a][0][v], acc[a][1][v]);
+            }
+        __syncthreads();
+        float *c = p.c + batch * p.c_batch;
+        const int64_t out_base = batch * p.m * p.n;
+        const bool vec = p.n % 4 == 0 && (reinterpret_cast<uintptr_t>(c) & 15) == 0;
+        for (int e = (int)threadIdx.x; e < BM * BN / 4; e += WS * 64) {
+            const int r = e / (BN / 4), cl = (e % (BN / 4)) * 4;
+            const int64_t row = i0 + r, col = j0 + cl;
+            if (row >= p.m || col >= p.n) continue;
+            float o[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                float g[WS];
+#pragma unroll
+                for (int w = 0; w < WS; ++w) g[w] = 0.f + lds[w * BM * BN + r * BN + cl + u];
+                const float total = ((g[0] + g[1]) + g[2]) + g[3];
+                o[u] = finish_value(p.bias, p.d, p.alpha, p.beta, total, out_base + row * p.n + col + u, col + u);
+            }
+            const int64_t idx = row * p.n + col;
+            if (vec) {
+                *reinterpret_cast<floatx4 *>(c + idx) = floatx4{o[0], o[1], o[2], o[3]};
+            } else {
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (col + u < p.n) c[idx + u] = o[u];
+            }
+        }
+    } else if constexpr (EPI == 0) {
         float *c = p.c + batch * p.c_batch + (int64_t)split * p.c_split;
         // bias / axpby apply to whole sums only; split sums finish them at the end
         const bool whole = p.splits == 1;
@@ -938,6 +1010,21 @@ __global__ void __launch_bounds__(WM *WN * 64, gemm_blocks_per_cu(BM, BN))
             }
         }
     }
+}
+
+template <int BM, int BN, int BK, int WM, int WN, bool XR, bool YR, int VX, int VY, int XMODE, int EPI>
+__global__ void __launch_bounds__(WM *WN * 64,
+                                  gemm_blocks_per_cu(BM, BN, XMODE == 4 && XR && YR && VX == 4 && VY == 4 && EPI == 0))
+    gemm_kernel(GemmParams p) {
+    gemm_body<BM, BN, BK, WM, WN, XR, YR, VX, VY, XMODE, EPI, 1>(p);
+}
+
+// Dense 32x32 tiles whose two to four reduction slices are the block's four waves (gemm_body,
+// WS = 4), staged 64 deep: for short split reductions over few tiles, one launch instead of the
+// slices' launch and their sum, a slice of up to 64 in one load round trip.
+template <bool XR, bool YR, int VX, int VY>
+__global__ void __launch_bounds__(256, 1) gemm_fold_kernel(GemmParams p) {
+    gemm_body<32, 32, 64, 1, 1, XR, YR, VX, VY, 0, 0, 4>(p);
 }
 
 // Sum of reduction slices (split_sum_part / split_sum_store): lane group g (of 4) adds slices
@@ -1101,6 +1188,18 @@ void launch_vec(const GemmParams &p, dim3 grid, hipStream_t stream, bool vx, boo
         launch_config<BM, BN, BK, WM, WN, XR, YR, 1, 4, XMODE, EPI>(p, grid, stream);
     else
         launch_config<BM, BN, BK, WM, WN, XR, YR, 1, 1, XMODE, EPI>(p, grid, stream);
+}
+
+template <bool XR, bool YR>
+void launch_fold(const GemmParams &p, dim3 grid, hipStream_t stream, bool vx, bool vy) {
+    if (vx && vy)
+        gemm_fold_kernel<XR, YR, 4, 4><<<grid, 256, 0, stream>>>(p);
+    else if (vx)
+        gemm_fold_kernel<XR, YR, 4, 1><<<grid, 256, 0, stream>>>(p);
+    else if (vy)
+        gemm_fold_kernel<XR, YR, 1, 4><<<grid, 256, 0, stream>>>(p);
+    else
+        gemm_fold_kernel<XR, YR, 1, 1><<<grid, 256, 0, stream>>>(p);
 }
 
 // Vector loads need the contiguous extent, the other stride and the base to be 4-aligned.
@@ -1350,6 +1449,18 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out, const 
     if (splits < 1) splits = 1;
     p.k_chunk = chunk;
     p.splits = static_cast<int32_t>(splits);
+    // Two to four slices of at most 128 over at most one 32x32 tile per CU: one block per tile whose
+    // waves are the slices (gemm_fold_kernel), with no partial buffer and no sum launch; the same
+    // bits as the slices and their sum.  Its 64-deep stages reach 31 * s_t + 63 * s_r elements.
+    auto fold_reach = [](int64_t st, int64_t sr) { return 31 * st + 63 * sr < (int64_t(1) << 29); };
+    const int64_t fold_tiles = ((p.m + 31) / 32) * ((p.n + 31) / 32) * batch;
+    const bool fold = XMODE == 0 && EPI == 0 && scheduled_splits > 1 && ch.shape == Shape::Small && splits >= 2 &&
+                      splits <= 4 && chunk <= 128 && fold_tiles <= cus && !p.perm_c && device->fold_splits &&
+                      fold_reach(p.x_si, p.x_sr) && fold_reach(p.y_sj, p.y_sr);
+    if (fold) {
+        p.tiles_m = static_cast<int32_t>((p.m + 31) / 32);
+        p.tiles_n = static_cast<int32_t>((p.n + 31) / 32);
+    }
 
     // Dense operands read through 32-bit offsets inside a tile: at most 127 * s_t + 31 * s_r elements.
     auto reach = [](int64_t st, int64_t sr) { return st >= 0 && sr >= 0 && 127 * st + 31 * sr < (int64_t(1) << 29); };
@@ -1376,7 +1487,8 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out, const 
     float *partials = nullptr, *spare = nullptr;
     if (ws) {
         const int64_t ranges = splits > 32 ? (splits + 31) / 32 : 0;
-        const int64_t need = (splits > 1 ? splits + ranges : 0) * out_len + (splits == 1 && p.perm_c ? out_len : 0);
+        const int64_t need =
+            (splits > 1 && !fold ? splits + ranges : 0) * out_len + (splits == 1 && p.perm_c ? out_len : 0);
         if (need > ws->floats)
             return axis::fail(AXIS_ERROR_INVALID, "product needs " + std::to_string(need * 4) +
                                                       " bytes of partial sums; the static scratch holds " +
@@ -1384,7 +1496,7 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out, const 
         partials = ws->ptr;
         spare = ws->ptr + splits * out_len;
     }
-    if (splits > 1) {
+    if (splits > 1 && !fold) {
         if (!partials) {
             int status = partial.get(device, sizeof(float) * (size_t)(out_len * splits));
             if (status) return status;
@@ -1407,13 +1519,15 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out, const 
         p.c_split = 0;
         p.c_batch = p.m * p.n;
     }
-    const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n * batch * splits;
+    const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n * batch * (fold ? 1 : splits);
     if (blocks >= INT32_MAX) return axis::fail(AXIS_ERROR_INVALID, "matmul too large for one launch");
     p.xcd_span = (uint32_t)(blocks / 8);
     const double k_work = (double)(p.k_work > 0 ? p.k_work : p.k);
     axis::TimedLaunch timed(ws ? nullptr : device, "gemm", 2.0 * (double)batch * (double)p.m * (double)p.n * k_work);
     dim3 grid(static_cast<unsigned>(blocks));
-    if constexpr (EPI == 1) {
+    if (fold) {
+        if constexpr (XMODE == 0 && EPI == 0) launch_fold<XR, YR>(p, grid, device->stream, vx, vy);
+    } else if constexpr (EPI == 1) {
         if (ch.shape == Shape::Large)
             launch_vec<128, 128, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, device->stream, vx, vy);
         else
@@ -1430,7 +1544,7 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out, const 
     }
     int status = axis::launch_status("gemm_kernel");
     if (status) return status;
-    if (splits > 1)
+    if (splits > 1 && !fold)
         status = sum_splits(device, partials, out, out_len, splits, p.bias, p.n, p.d, p.alpha, p.beta,
                             p.perm_c, p.perm_taps, spare, final_out && !ws ? &partial : nullptr);
     else if (p.perm_c) {

@@ -5,6 +5,7 @@ evaluation order (col2im, CSR sums, elementwise, Adam) must be bit-identical; GE
 softmax family are checked to the stated fp32 tolerance.
 """
 import ctypes
+import os
 
 import numpy as np
 import pytest
@@ -75,6 +76,84 @@ def test_matmul_bias_equals_product_then_bias_add(dev, dev_bf16, batch, m, k, n)
         assert np.array_equal(got.view(np.uint32), d.read(sep, batch * m * n).view(np.uint32))
     with pytest.raises(hip.AxisError, match="alias"):
         d.call("axis_matmul_bias", da.vp, db.vp, fused.vp, fused.vp, *geo)
+
+
+# Products whose two to four short slices run in one block's waves (gemm_fold_kernel): (batch, m,
+# k, n) and the entries that fold at that shape on a 256-CU part
+FOLD_CASES = [(1, 256, 256, 1000),   # the classifier: product and weight gradient, 4 slices of 64
+              (1, 256, 1000, 256),   # left and right backward, 4 slices of 64
+              (2, 200, 300, 90),     # batched, ragged tiles, odd width: product 4, right backward 3 slices of 96
+              (1, 100, 200, 999),    # product in 3 slices, width not a multiple of 4
+              (1, 300, 576, 128)]    # right backward in 4 slices of 96
+
+
+@pytest.fixture(scope="module")
+def unfolded():
+    """fp32 and bf16 handles that keep every split product as slices plus a sum launch."""
+    os.environ["AXIS_GEMM_UNFOLDED"] = "1"
+    try:
+        return hip.Device(0), hip.Device(0, bf16_matmul=True)
+    finally:
+        del os.environ["AXIS_GEMM_UNFOLDED"]
+
+
+def _stats(d):
+    in_use, cached = ctypes.c_size_t(), ctypes.c_size_t()
+    d.call("axis_memory_stats", ctypes.byref(in_use), ctypes.byref(cached))
+    return in_use.value, cached.value
+
+
+@pytest.mark.parametrize("batch,m,k,n", FOLD_CASES)
+def test_folded_split_products_match_split_launches(dev, dev_bf16, unfolded, oracle, batch, m, k, n):
+    # bit for bit against the slices and their sum on handles that do not fold, on every product
+    # entry (bias and axpby finished once, as the sum does), fp32 and bf16 handles; the oracle to
+    # GEMM tolerance
+    rng = np.random.default_rng(batch * 31 + m + k + n)
+    a = rng.standard_normal(batch * m * k).astype(np.float32)
+    b = rng.standard_normal(batch * k * n).astype(np.float32)
+    g = rng.standard_normal(batch * m * n).astype(np.float32)
+    bias = rng.standard_normal(n).astype(np.float32)
+    geo = (I64(batch), I64(m), I64(k), I64(n))
+    entries = [("axis_matmul", (a, b), (), batch * m * n),
+               ("axis_matmul_bias", (a, b, bias), (), batch * m * n),
+               ("axis_matmul_axpby", (a, b, g), (F32(1.75), F32(-0.5)), batch * m * n),
+               ("axis_matmul_left_backward", (g, b), (), batch * m * k),
+               ("axis_matmul_right_backward", (a, g), (), batch * k * n)]
+    for folded, split in ((dev, unfolded[0]), (dev_bf16, unfolded[1])):
+        for name, operands, scalars, size in entries:
+            print(f"fold case {name} batch={batch} m={m} k={k} n={n}", flush=True)
+            got = []
+            for d in (folded, split):
+                ops = [up(d, x) for x in operands]
+                out = d.empty(size)
+                d.call(name, *[o.vp for o in ops], out.vp, *geo, *scalars)
+                got.append(d.read(out, size))
+            assert np.array_equal(got[0].view(np.uint32), got[1].view(np.uint32)), name
+            if folded is dev and name == "axis_matmul":
+                assert rel_err(got[0], oracle.matmul(a, b, batch, m, k, n)) < 1e-5
+            if folded is dev and name == "axis_matmul_left_backward":
+                assert rel_err(got[0], oracle.matmul_left_backward(g, b, batch, m, k, n)) < 1e-5
+            if folded is dev and name == "axis_matmul_right_backward":
+                assert rel_err(got[0], oracle.matmul_right_backward(a, g, batch, m, k, n)) < 1e-5
+
+
+def test_folded_classifier_product_allocates_no_partial_sums(unfolded):
+    # the classifier's product (4 slices over 64 tiles) folds: no partial buffer is taken from the
+    # allocator, where the unfolded handle takes one of 4 x 256 x 1000 floats
+    m, k, n = 256, 256, 1000
+    rng = np.random.default_rng(3)
+    for d, folds in ((hip.Device(0), True), (unfolded[0], False)):
+        a, b = up(d, rng.standard_normal(m * k)), up(d, rng.standard_normal(k * n))
+        out = d.empty(m * n)
+        d.call("axis_empty_cache")  # a cached block would serve the partials without a count change
+        before = _stats(d)
+        d.call("axis_matmul", a.vp, b.vp, out.vp, I64(1), I64(m), I64(k), I64(n))
+        d.synchronize()
+        after = _stats(d)
+        if folds:
+            assert after == before
+        else:
+            assert after[1] >= before[1] + 4 * m * n * 4
 
 
 def test_matmul_rejects_bad_extents(dev):
