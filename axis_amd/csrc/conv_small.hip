@@ -449,6 +449,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_of(const void *base) {
 }
 
 typedef __attribute__((address_space(3))) void *lds_void;
+typedef __attribute__((address_space(3))) float lds_float;
 
 // C channels under a KH x KW kernel; bands of BR x 32 windows.  Staged rows are SW cells apart and
 // planes PP cells apart (both at least the band's extent), chosen per kernel so that one operand
@@ -674,39 +675,40 @@ __global__ void __launch_bounds__(256, 4) small_conv_pool_forward_fixed_kernel(S
     }
 }
 
-// Weight and bias gradient through ReLU -> 2x2 max pool (small_conv_pool_wgrad_kernel) over bands
-// of 1 x 32 windows.  Per band the LDS buffer holds the gradient and the pooled values
-// [32 windows][64 columns], the winner bytes [32][64] and the input planes.  Wave w takes windows
-// 8w .. 8w + 7 of each band as two quads of four windows, and the reduction step of one
-// v_mfma_f32_16x16x4_f32 is one pixel position p of the quad's four windows (k = window in the
-// quad): MFMA row r of column block nb is output column 4 r + nb, so lane (r, k) reads its own
-// window's four gradient, pooled and winner values once per quad with 16- and 4-byte reads, and
-// its A operand at position p is g where the winner byte is p and the pooled value positive,
-// else 0.  The sums run window quad by window quad, position by position (deterministic; not the
-// generic kernel's window-major order).
+// Weight and bias gradient through ReLU -> 2x2 max pool (small_conv_pool_wgrad_kernel) over bands of
+// 1 x 32 windows, for the fixed geometries, through the pool's winners.  Per band the LDS buffer
+// holds the gradient and the pooled values [32 windows][64 columns], the winner bytes [32][64] and
+// the input planes (streamed in by buffer_load ... lds, double-buffered).  Column n of a window takes
+// its gradient at one pixel only -- its winner, when the pooled value is positive -- so the product
+// over the window's four pixels is g * x at that pixel plus 0 * x at the other three, and the zeros
+// change nothing while x is finite.  A lane per output column gathers its winner pixel's C*KH*KW
+// input terms from the staged band (one LDS read each, at compile-time offsets from a per-lane
+// base) and adds g * x to each term's sum, and g to the bias's: a quarter of the products, none of
+// them padded.  A wave whose windows read a non-finite input value in a band then also adds the
+// other three positions' 0 * x, so 0 * inf = NaN reaches the sums as in the dense product.  Wave w
+// takes windows 8 w .. 8 w + 7 of each band; the sums run window by window, band by band
+// (deterministic).
 template <int C, int KH, int KW>
-__global__ void __launch_bounds__(256, 3) small_conv_pool_wgrad_fixed_kernel(SmallConvArgs a,
-                                                                               const float *__restrict__ g,
-                                                                               const float *__restrict__ pooled,
-                                                                               const uint8_t *__restrict__ argmax,
-                                                                               float *__restrict__ partial) {
-    // rows 69 cells apart (5 banks), planes 335 (15 banks): the 16 terms x 2 windows of a half-wave
-    // read fall in distinct banks or share a cell
+__global__ void __launch_bounds__(256, 3) small_conv_pool_wgrad_gather_kernel(SmallConvArgs a,
+                                                                                const float *__restrict__ g,
+                                                                                const float *__restrict__ pooled,
+                                                                                const uint8_t *__restrict__ argmax,
+                                                                                float *__restrict__ partial) {
     using F = Fixed<C, KH, KW, 1, 69, 335>;
-    constexpr int W = F::BS;                        // windows per band
-    constexpr int GP = W * 64;                      // floats of the band's gradient (and pooled values)
-    constexpr int XO = 2 * GP + W * 16;             // the input planes, after the winner bytes
-    constexpr int BUF = XO + F::XBUF;
-    static_assert(2 * BUF >= 4 * 32 * 64, "the four waves' sums fit the buffers");
+    constexpr int W = F::BS;             // windows per band
+    constexpr int GP = W * 64;           // floats of the band's gradient (and pooled values)
+    constexpr int XO = 2 * GP + W * 16;  // the input planes, after the winner bytes
+    constexpr int BUF = XO + C * F::PLANE;
+    constexpr int T = F::K;              // input terms per pixel; term T is the bias
+    static_assert(2 * BUF >= 4 * (T + 1) * 64, "the four waves' sums fit the buffers");
+    // the wave's input region in a band: C planes x SH rows x 18 columns (8 windows and the halo)
+    constexpr int RW = 2 * 8 + KW - 1;
+    constexpr int REGION = C * F::SH * RW;
+    constexpr int CHECKS = (REGION + 63) / 64;
     __shared__ __attribute__((aligned(16))) float lds[2 * BUF];
     const int tid = threadIdx.x, lane = tid & 63;
-    const int nl = lane & 15, wq = lane >> 4;  // MFMA row r = nl; k = window wq of a quad
     const int32_t col0 = (int32_t)blockIdx.y * 64;
 
-    for (int32_t t = tid; t < F::PLANE; t += 256) {
-        lds[XO + C * F::PLANE + t] = 1.0f;
-        lds[BUF + XO + C * F::PLANE + t] = 1.0f;
-    }
     StripStream<F> stream;
     stream.init(a, tid);
     const int wave = stream.wave;
@@ -722,12 +724,14 @@ __global__ void __launch_bounds__(256, 3) small_conv_pool_wgrad_fixed_kernel(Sma
     }
     const int32_t awin = 16 * wave + (lane >> 2);
     const uint32_t arel = (uint32_t)(awin * a.n + col0 + 16 * (lane & 3));
-    // the lane's window of a quad: 8 wave + 4 q + wq; B operand cells of its two terms (nl, nl + 16)
-    // at the window's first pixel
-    const int32_t lane_win = 8 * wave + wq;
-    int32_t xoff[2];
+    // the lane's cells of the wave's input region (the non-finite test), as offsets in the band
+    int32_t check[CHECKS];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) xoff[kb] = XO + 2 * lane_win + F::off(nl + 16 * kb);
+    for (int i = 0; i < CHECKS; ++i) {
+        const int cell = lane + 64 * i < REGION ? lane + 64 * i : 0;
+        const int plane = cell / (F::SH * RW), rest = cell % (F::SH * RW);
+        check[i] = XO + plane * F::PLANE + (rest / RW) * F::SW + 16 * wave + rest % RW;
+    }
     const uint32_t bands = (uint32_t)a.bands;
 
     auto load = [&](const Band &b, float *buf) {
@@ -750,72 +754,89 @@ __global__ void __launch_bounds__(256, 3) small_conv_pool_wgrad_fixed_kernel(Sma
         stream.load(a, b, buf + XO);
     };
 
-    floatx4 acc[4][2];
+    float acc[T + 1];
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) acc[nb][kb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int t = 0; t <= T; ++t) acc[t] = 0.0f;
 
     uint32_t band = blockIdx.x;
     if (band < bands) load(decode_band(a, band), lds);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
-    auto run = [&](uint32_t bnd, auto parity) {
-        constexpr int P = decltype(parity)::value;
+    // one body for both buffers (the buffer a runtime offset): the sums stay in the same registers
+    auto run = [&](uint32_t bnd, int P) {
         if (bnd + gridDim.x < bands) load(decode_band(a, bnd + gridDim.x), lds + (P ^ 1) * BUF);
-        const float *gv = lds + P * BUF + 64 * lane_win + 4 * nl;
-        const uint8_t *av = reinterpret_cast<const uint8_t *>(lds + P * BUF + 2 * GP) + 64 * lane_win + 4 * nl;
-        const float *xv[2] = {lds + P * BUF + xoff[0], lds + P * BUF + xoff[1]};
+        const float *buf = lds + P * BUF;
+        bool bad = false;
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {  // windows 8 wave + 4 q + (0 .. 3)
-            const floatx4 g4 = *reinterpret_cast<const floatx4 *>(gv + 256 * q);
-            const floatx4 p4 = *reinterpret_cast<const floatx4 *>(gv + GP + 256 * q);
-            const uint32_t a4 = *reinterpret_cast<const uint32_t *>(av + 256 * q);
-            float x[4][2];
+        for (int i = 0; i < CHECKS; ++i)
+            if (lane + 64 * i < REGION) bad |= !(__builtin_fabsf(buf[check[i]]) <= FLT_MAX);
+        // the wave's window j: its gradient where its winner takes it (else 0) and the winner
+        auto window = [&](int j, float &ge, uint32_t &key) {
+            const int w = 8 * wave + j;
+            const float gv = buf[w * 64 + lane];
+            const float pv = buf[GP + w * 64 + lane];
+            key = reinterpret_cast<const uint8_t *>(buf + 2 * GP)[w * 64 + lane];
+            const bool take = pv > 0.0f && key < 4u;
+            ge = take ? gv : 0.0f;
+            key = take ? key : 0u;
+        };
+        // the winner's offset from the window's first pixel, (key / 2) * SW + key % 2, as byte key
+        // of a packed table
+        static_assert(F::SW + 1 < 256, "winner offsets fit a byte");
+        constexpr uint32_t kWinnerOffsets = 0u | (1u << 8) | ((uint32_t)F::SW << 16) | ((uint32_t)(F::SW + 1) << 24);
+        float ge_next;
+        uint32_t key_next;
+        window(0, ge_next, key_next);
 #pragma unroll
-            for (int p = 0; p < 4; ++p)
+        for (int j = 0; j < 8; ++j) {
+            const float ge = ge_next;
+            const uint32_t key = key_next;
+            if (j + 1 < 8) window(j + 1, ge_next, key_next);  // the next window's operands ahead
+            // one ds_read_b32 per term at a compile-time offset from the lane's base (read through
+            // volatile so they are not paired into ds_read2, whose 8-bit offsets would take an
+            // address add per pair)
+            const uint32_t at = __builtin_amdgcn_ubfe(kWinnerOffsets, 8 * key, 8);
+            const volatile lds_float *xp = (const volatile lds_float *)(buf + XO + 2 * (8 * wave + j) + at);
+            float xv[T];
 #pragma unroll
-                for (int kb = 0; kb < 2; ++kb) x[p][kb] = xv[kb][8 * q + (p >> 1) * F::SW + (p & 1)];
-            // the position whose pre-activation takes column 4 nl + nb's gradient (none: 255)
-            uint32_t key[4];
+            for (int t = 0; t < T; ++t) xv[t] = xp[F::off(t)];
 #pragma unroll
-            for (int nb = 0; nb < 4; ++nb) key[nb] = p4[nb] > 0.0f ? (a4 >> (8 * nb)) & 0xffu : 0xffu;
-            __builtin_amdgcn_sched_barrier(0);
+            for (int t = 0; t < T; ++t) acc[t] = __builtin_fmaf(ge, xv[t], acc[t]);
+            acc[T] = acc[T] + ge;
+        }
+        if (__builtin_amdgcn_ballot_w64(bad) != 0) {
+            // a non-finite input in the wave's windows: the other three positions' 0 * x as well
+#pragma unroll 1
+            for (int j = 0; j < 8; ++j) {
+                float ge;
+                uint32_t key;
+                window(j, ge, key);
+#pragma unroll 1
+                for (int p = 0; p < 4; ++p) {
+                    // the winner's own term is in already (g * x, which is not 0 * x for infinite x)
+                    if ((uint32_t)p == key) continue;
+                    const float *xp = buf + XO + 2 * (8 * wave + j) + (p >> 1) * F::SW + (p & 1);
 #pragma unroll
-            for (int p = 0; p < 4; ++p)
-#pragma unroll
-                for (int nb = 0; nb < 4; ++nb) {
-                    const float d = key[nb] == (uint32_t)p ? g4[nb] : 0.0f;
-                    acc[nb][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(d, x[p][0], acc[nb][0], 0, 0, 0);
-                    acc[nb][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(d, x[p][1], acc[nb][1], 0, 0, 0);
+                    for (int t = 0; t < T; ++t) acc[t] = __builtin_fmaf(0.0f, xp[F::off(t)], acc[t]);
                 }
+            }
         }
         __builtin_amdgcn_s_waitcnt(0);  // the next band has landed
         __syncthreads();                // ... for every wave, and this band's reads are done
     };
-    while (band < bands) {
-        run(band, std::integral_constant<int, 0>{});
-        band += gridDim.x;
-        if (band >= bands) break;
-        run(band, std::integral_constant<int, 1>{});
-        band += gridDim.x;
-    }
+    for (int P = 0; band < bands; band += gridDim.x, P ^= 1) run(band, P);
 
-    // The four waves' sums meet in LDS ([wave][term][64 columns]) and are added in wave order.  D
-    // register v of lane l in block (nb, kb): term 16 kb + l % 16, column 16 (l / 16) + 4 v + nb.
+    // The four waves' sums meet in LDS ([wave][term][64 columns]) and are added in wave order.
     float *const red = lds;
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) red[(wave * 32 + nl + 16 * kb) * 64 + 16 * wq + 4 * v + nb] = acc[nb][kb][v];
+    for (int t = 0; t <= T; ++t) red[(wave * (T + 1) + t) * 64 + lane] = acc[t];
     __syncthreads();
     float *dst = partial + (int64_t)blockIdx.x * 32 * a.n;
-    for (int32_t e = tid; e < 32 * 64; e += 256) {
+    constexpr int SUMS = (T + 1) * 64;
+    for (int32_t e = tid; e < SUMS; e += 256) {
         const int32_t t = e >> 6, col = col0 + (e & 63);
-        const float sum = ((red[e] + red[2048 + e]) + red[4096 + e]) + red[6144 + e];
+        const float sum = ((red[e] + red[SUMS + e]) + red[2 * SUMS + e]) + red[3 * SUMS + e];
         dst[(int64_t)t * a.n + col] = sum;
     }
 }
@@ -982,11 +1003,11 @@ int small_conv_pool_backward_weight(axis_device device, const SmallConvShape &s,
         TimedLaunch timed(device, "gemm", 2.0 * (double)s.batch * s.out_h * s.out_w * s.out_channels * a.k);
         const dim3 grid(blocks, columns);
         if (fixed && a.c_in == 3) {
-            small_conv_pool_wgrad_fixed_kernel<3, 3, 3><<<grid, 256, 0, device->stream>>>(a, gradient, pooled, argmax,
-                                                                                            partial.as<float>());
+            small_conv_pool_wgrad_gather_kernel<3, 3, 3><<<grid, 256, 0, device->stream>>>(a, gradient, pooled, argmax,
+                                                                                             partial.as<float>());
         } else if (fixed) {
-            small_conv_pool_wgrad_fixed_kernel<1, 3, 3><<<grid, 256, 0, device->stream>>>(a, gradient, pooled, argmax,
-                                                                                            partial.as<float>());
+            small_conv_pool_wgrad_gather_kernel<1, 3, 3><<<grid, 256, 0, device->stream>>>(a, gradient, pooled, argmax,
+                                                                                             partial.as<float>());
         } else {
             small_conv_pool_wgrad_kernel<<<grid, 256, lds, device->stream>>>(a, gradient, pooled, argmax,
                                                                               partial.as<float>());

@@ -1192,6 +1192,48 @@ def test_conv2d_relu_pool_backward_weight(dev, oracle, case):
     assert np.array_equal(dev.read(gw2, c * k * k * n).view(np.uint32), got_w.view(np.uint32))
 
 
+@pytest.mark.parametrize("layout", ["nchw", "nhwc"])
+def test_conv2d_relu_pool_backward_weight_nonfinite_input(dev, layout):
+    # conv1's weight gradient through the pool's winners adds g * x at each window's winner only; a
+    # band with a non-finite input also adds the other positions' 0 * x, so NaN and inf reach the
+    # sums as in the dense product over the pre-activation gradient (the separate entries).  At 64 x 64
+    # with padding 1 every input pixel lies in some pooling window, so both see the same terms.
+    b, c, h, w, n, k, p = 1, 3, 64, 64, 64, 3, 1
+    rng = np.random.default_rng(91)
+    x = rng.uniform(-1, 1, b * c * h * w).astype(np.float32)
+    x[[5, 300, 4100]] = [np.inf, np.nan, -np.inf]  # channels 0 and 1; channel 2's terms stay finite
+    weight = rng.standard_normal(c * k * k * n).astype(np.float32) * 0.3
+    bias = rng.standard_normal(n).astype(np.float32) * 0.1
+    if layout == "nchw":
+        strides = (I64 * 4)(c * h * w, h * w, w, 1)
+    else:
+        x = x.reshape(b, c, h, w).transpose(0, 2, 3, 1).copy().reshape(-1)
+        strides = None
+    geo = [(I32 * 2)(k, k), (I32 * 2)(1, 1), (I32 * 2)(p, p)]
+    win = (I32 * 2)(2, 2)
+    pooled_len = b * (h // 2) * (w // 2) * n
+    dx, dw, db = up(dev, x), up(dev, weight), up(dev, bias)
+    pooled, arg = dev.empty(pooled_len), dev.empty(pooled_len, np.uint8)
+    dev.call("axis_conv2d_relu_pool_forward", dx.vp, strides, dw.vp, db.vp, pooled.vp, arg.vp, I64(b), I32(h),
+             I32(w), I32(c), I32(n), *geo, win)
+    dg = up(dev, rng.standard_normal(pooled_len).astype(np.float32))
+    gw = dev.empty(c * k * k * n)
+    dev.call("axis_conv2d_relu_pool_backward_weight", dx.vp, strides, dg.vp, pooled.vp, arg.vp, gw.vp, None,
+             I64(b), I32(h), I32(w), I32(c), I32(n), *geo, win)
+    m = b * h * w
+    pre, sep_b, sep_w = dev.empty(m * n), dev.empty(n), dev.empty(c * k * k * n)
+    dev.call("axis_relu_pool_backward", dg.vp, pooled.vp, arg.vp, pre.vp, sep_b.vp, I64(b), I32(h), I32(w),
+             I32(n), win)
+    dev.call("axis_conv2d_backward_weight", dx.vp, strides, pre.vp, sep_w.vp, I64(b), I32(h), I32(w), I32(c),
+             I32(n), *geo)
+    got, ref = dev.read(gw, c * k * k * n), dev.read(sep_w, c * k * k * n)
+    assert np.isnan(ref).any()
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    assert np.array_equal(np.isinf(got), np.isinf(ref)) and np.array_equal(got[np.isinf(got)], ref[np.isinf(ref)])
+    fin = np.isfinite(ref)
+    assert rel_err(got[fin], ref[fin]) < 1e-5
+
+
 @pytest.mark.parametrize("b,h,w,c,pool", [(5, 16, 18, 64, (2, 2)), (3, 10, 12, 6, (2, 3)), (2, 8, 8, 20, (4, 4)),
                                           (64, 32, 32, 128, (2, 2)), (4, 8, 8, 16, (2, 2))])
 def test_relu_pool_backward_bit_exact(dev, oracle, b, h, w, c, pool):
