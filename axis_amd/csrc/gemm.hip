@@ -1530,13 +1530,23 @@ int run_gemm(axis_device device, GemmParams p, int64_t batch, float *out, const 
     if (fold) {
         if constexpr (XMODE == 0 && EPI == 0) launch_fold<XR, YR>(p, grid, device->stream, vx, vy);
     } else if constexpr (EPI == 1) {
+        // the fused forward's 128x128 tiles in eight waves of 64x32 (307.8 -> 302.8 us per launch)
         if (ch.shape == Shape::Large)
-            launch_vec<128, 128, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, device->stream, vx, vy);
+            launch_vec<128, 128, 32, 2, 4, XR, YR, XMODE, EPI>(p, grid, device->stream, vx, vy);
         else
             launch_vec<128, 64, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, device->stream, vx, vy);
     } else {
-        if (ch.shape == Shape::Large)
-            launch_vec<128, 128, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, device->stream, vx, vy);
+        // 128x128 tiles of the gathered convolution loader, and dense ones with both operands
+        // contiguous along the reduction, in eight waves of 64x32: two blocks and sixteen waves per
+        // CU at 128 VGPRs (conv3's data gradient 293 -> 284 us, the 4096^3 data gradient 141 -> 144
+        // TFLOP/s); other dense ones in four waves of 64x64 (the eight-wave instances need 132-154
+        // VGPRs, one block per CU)
+        if (ch.shape == Shape::Large) {
+            if constexpr (XMODE == 4 || (XMODE == 0 && XR && YR))
+                launch_vec<128, 128, 32, 2, 4, XR, YR, XMODE, EPI>(p, grid, device->stream, vx, vy);
+            else
+                launch_vec<128, 128, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, device->stream, vx, vy);
+        }
         else if (ch.shape == Shape::Tall)
             launch_vec<128, 64, 32, 2, 2, XR, YR, XMODE, EPI>(p, grid, device->stream, vx, vy);
         else if (ch.shape == Shape::Small)
