@@ -1359,7 +1359,7 @@ int run_gemm_bf16(axis_device device, const GemmParams &p, int64_t batch, float 
             return st;
     const axis::Bf16Tile tile = axis::bf16_gemm_tile(p.m, p.n, batch, kp, device->multiprocessors);
     const int64_t tiles = ((p.m + tile.rows - 1) / tile.rows) * ((p.n + tile.cols - 1) / tile.cols) * batch;
-    const int64_t slots = device->multiprocessors * 2;
+    const int64_t slots = device->multiprocessors * (tile.rows == 256 ? 1 : 2);  // resident blocks
     const int64_t out_len = batch * p.m * p.n;
     // split as the fp32 path does: fill one round of resident blocks, reductions of 8 stages or more
     int64_t splits = 1;

@@ -7,9 +7,12 @@
 // along the reduction are rounded in place order; those contiguous along t go through a 64 x 64
 // LDS transpose so both the fp32 reads and the bf16 writes stay coalesced.
 //
-// Product: 256 threads (2 x 2 waves) per BM x BN tile, 64-deep LDS stages of both operands in
+// Product: WM x WN waves per BM x BN tile (2 x 2 for 128 x 128 and 64 x 64, two blocks per CU;
+// 2 x 4 waves of 128 x 64 for 256 x 256, one block per CU), 64-deep LDS stages of both operands in
 // two LDS buffers; the next stage streams straight into the idle buffer (buffer_load ... lds)
 // while the current one feeds v_mfma_f32_16x16x32_bf16, then one wait and one barrier per stage.
+// The 256 x 256 tile halves the operand bytes per product of two 128 x 128 blocks (the stage
+// loads of a CU: 64 KB per 2048 MFMA cycles instead of 64 KB per 1024).
 #include <algorithm>
 #include <type_traits>
 
@@ -172,10 +175,11 @@ __device__ __forceinline__ float finish(const float *bias, const float *d, float
 // rows 8q..8q+7 (1 KB); lane i writes row 8q + i/8 at chunk position i % 8, so it loads that row's
 // chunk (i % 8) ^ ((i / 8) & 7), the swizzled layout above.  Rows past the operand's end read
 // out of range; they only reach output rows or columns that are never stored.
-template <int BT>
+template <int BT, int NW>
 struct DirectLoader {
     static_assert(axis::kBf16Depth == 64, "eight 16-byte chunks per staged row");
-    static constexpr int CH = BT * 64 / 8 / 256;  // instructions per wave and stage
+    static constexpr int CH = BT * 64 / 8 / (64 * NW);  // instructions per wave and stage (NW waves)
+    static_assert(CH * 64 * NW * 8 == BT * 64, "the block's waves split the stage's rows evenly");
     uint32_t off[CH];
     const uint16_t *base;
     int wave;
@@ -185,7 +189,7 @@ struct DirectLoader {
         const int i = tid & 63;
 #pragma unroll
         for (int e = 0; e < CH; ++e) {
-            const int q = e * 4 + wave;
+            const int q = e * NW + wave;
             const int row = 8 * q + (i >> 3);
             const int c = (i & 7) ^ ((i >> 3) & 7);
             off[e] = t0 + row < rows ? (uint32_t)((row * kp + c * 8) * 2) : kOutside;
@@ -195,7 +199,7 @@ struct DirectLoader {
         const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(uniform_ptr(base + r0));
 #pragma unroll
         for (int e = 0; e < CH; ++e) {
-            const int q = e * 4 + wave;
+            const int q = e * NW + wave;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 rsrc, (__attribute__((address_space(3))) void *)(stage + q * 512), 16, off[e], 0, 0, 0);
         }
@@ -215,12 +219,12 @@ __device__ __forceinline__ void grouped_tile(uint32_t tile, uint32_t tiles_m, ui
     tj = in / height;
 }
 
-template <int BM, int BN, int BK>
-__global__ void __launch_bounds__(256, 2) bf16_gemm_kernel(KernelArgs a) {
+template <int BM, int BN, int BK, int WM, int WN>
+__global__ void __launch_bounds__(WM * WN * 64, WM * WN == 8 ? 1 : 2) bf16_gemm_kernel(KernelArgs a) {
     static_assert(axis::kBf16Depth % BK == 0 && BK % 32 == 0, "stages tile the staged depth");
     using Lay = Layout<BK>;
     constexpr int LDK = BK;  // bf16 per LDS row
-    constexpr int WM = 2, WN = 2, TM = BM / WM, TN = BN / WN, FM = TM / 16, FN = TN / 16;
+    constexpr int NW = WM * WN, TM = BM / WM, TN = BN / WN, FM = TM / 16, FN = TN / 16;
     constexpr int kBuf = (BM + BN) * LDK;  // one stage of both operands
     __shared__ __attribute__((aligned(16))) uint16_t lds[2 * kBuf];
     const axis::Bf16Gemm &g = a.g;
@@ -254,8 +258,8 @@ __global__ void __launch_bounds__(256, 2) bf16_gemm_kernel(KernelArgs a) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    using LX = DirectLoader<BM>;
-    using LY = DirectLoader<BN>;
+    using LX = DirectLoader<BM, NW>;
+    using LY = DirectLoader<BN, NW>;
     LX lx;
     LY ly;
     lx.init(g.x + batch * g.x_batch, i0, g.m, g.kp, tid);
@@ -370,6 +374,11 @@ int stage_bf16(axis_device device, const Bf16Source &src, int64_t batch, int64_t
 }
 
 Bf16Tile bf16_gemm_tile(int64_t m, int64_t n, int64_t batch, int64_t kp, int64_t cus) {
+    // 256 x 256 tiles when they alone fill the chip (one per CU): 4096^3 data and weight gradients
+    // 870 / 852 -> 919 / 907 TFLOP/s, staging included.
+    // (Their 32-bit row offsets reach 257 * kp * 2 bytes: longer reductions keep 128 x 128.)
+    if (((m + 255) / 256) * ((n + 255) / 256) * batch >= cus && (int64_t)257 * kp * 2 < (int64_t(1) << 31))
+        return Bf16Tile{256, 256};
     // (A 256 x 128 tile of 32-deep stages, 128 x 64 per wave, measured no faster.)  A reduction
     // long enough to split keeps the 128 x 128 tile and fills the chip with slices instead: the
     // skinny 784 x 1024 x 8192 weight gradient runs 15% faster that way than on 64 x 64 tiles.
@@ -396,10 +405,12 @@ int bf16_gemm(axis_device device, const Bf16Gemm &g, int64_t batch, Bf16Tile til
         return fail(AXIS_ERROR_INVALID, "bf16 matmul reduction too long");
     a.xcd_span = (uint32_t)(blocks / 8);
     dim3 grid((unsigned)blocks);
-    if (tile.rows == 128)
-        bf16_gemm_kernel<128, 128, 64><<<grid, 256, 0, device->stream>>>(a);
+    if (tile.rows == 256)
+        bf16_gemm_kernel<256, 256, 64, 2, 4><<<grid, 512, 0, device->stream>>>(a);
+    else if (tile.rows == 128)
+        bf16_gemm_kernel<128, 128, 64, 2, 2><<<grid, 256, 0, device->stream>>>(a);
     else
-        bf16_gemm_kernel<64, 64, 64><<<grid, 256, 0, device->stream>>>(a);
+        bf16_gemm_kernel<64, 64, 64, 2, 2><<<grid, 256, 0, device->stream>>>(a);
     return launch_status("bf16_gemm_kernel");
 }
 

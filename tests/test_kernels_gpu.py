@@ -800,6 +800,30 @@ def test_bf16_backward_at_config2_sizes(dev_bf16, oracle, m, k, n):
         assert rel_err(got, want) < 1e-5
 
 
+@pytest.mark.parametrize("batch,m,k,n", [(1, 4096, 192, 4096), (1, 4352, 320, 4100), (4, 2048, 96, 2048)])
+def test_bf16_products_on_256_tiles(dev_bf16, oracle, batch, m, k, n):
+    """Products whose 256 x 256 tiles alone fill a 256-CU part (one block of eight waves per CU):
+    every output, ragged edges and batches included, against float64 products of the bf16-rounded
+    operands (fp32 accumulation of exact bf16 products: rel 1e-5); the bias entry adds the bias to
+    the same sums."""
+    rng = np.random.default_rng(m + k + n)
+    a = rng.standard_normal(batch * m * k).astype(np.float32)
+    b = rng.standard_normal(batch * k * n).astype(np.float32)
+    bias = rng.standard_normal(n).astype(np.float32)
+    A, B, BIAS = up(dev_bf16, a), up(dev_bf16, b), up(dev_bf16, bias)
+    out, out_b = dev_bf16.empty(batch * m * n), dev_bf16.empty(batch * m * n)
+    geo = (I64(batch), I64(m), I64(k), I64(n))
+    dev_bf16.call("axis_matmul", A.vp, B.vp, out.vp, *geo)
+    dev_bf16.call("axis_matmul_bias", A.vp, B.vp, BIAS.vp, out_b.vp, *geo)
+    R = oracle.bf16_round
+    ra, rb = R(a).reshape(batch, m, k).astype(np.float64), R(b).reshape(batch, k, n).astype(np.float64)
+    want = ra @ rb
+    got = dev_bf16.read(out, batch * m * n).reshape(batch, m, n)
+    assert rel_err(got, want) < 1e-5
+    got_b = dev_bf16.read(out_b, batch * m * n).reshape(batch, m, n)
+    assert np.array_equal(got_b.view(np.uint32), (got + bias).astype(np.float32).view(np.uint32))
+
+
 @pytest.mark.parametrize("m", [4_194_368, 8_400_000])
 def test_bf16_weight_gradient_over_long_reductions(dev_bf16, m):
     """matmul_right_backward on a bf16 handle reducing over more than 4,194,304 rows (its operands
