@@ -374,10 +374,13 @@ int stage_bf16(axis_device device, const Bf16Source &src, int64_t batch, int64_t
 }
 
 Bf16Tile bf16_gemm_tile(int64_t m, int64_t n, int64_t batch, int64_t kp, int64_t cus) {
-    // 256 x 256 tiles when they alone fill the chip (one per CU): 4096^3 data and weight gradients
-    // 870 / 852 -> 919 / 907 TFLOP/s, staging included.
+    // 256 x 256 tiles when they alone fill the chip (one per CU) and cover the output with at most
+    // 1/8 of their rows and columns past its edges (a batch of small products keeps the smaller
+    // tiles): 4096^3 data and weight gradients 870 / 852 -> 919 / 907 TFLOP/s, staging included.
     // (Their 32-bit row offsets reach 257 * kp * 2 bytes: longer reductions keep 128 x 128.)
-    if (((m + 255) / 256) * ((n + 255) / 256) * batch >= cus && (int64_t)257 * kp * 2 < (int64_t(1) << 31))
+    const int64_t pm = (m + 255) / 256 * 256, pn = (n + 255) / 256 * 256;
+    if ((pm / 256) * (pn / 256) * batch >= cus && 8 * m * n >= 7 * pm * pn &&
+        (int64_t)257 * kp * 2 < (int64_t(1) << 31))
         return Bf16Tile{256, 256};
     // (A 256 x 128 tile of 32-deep stages, 128 x 64 per wave, measured no faster.)  A reduction
     // long enough to split keeps the 128 x 128 tile and fills the chip with slices instead: the

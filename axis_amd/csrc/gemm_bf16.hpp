@@ -44,8 +44,9 @@ struct Bf16Tile {
 };
 
 // Output tile for a device with `cus` compute units and a reduction padded to kp: 256 x 256 when
-// the output has at least one per CU; else 128 x 128 unless the output has too few of them to fill
-// the chip and the reduction is too short to be split into slices (under 8 stages), then 64 x 64.
+// the output has at least one per CU and they waste at most 1/8 of their area past its edges; else
+// 128 x 128 unless the output has too few of them to fill the chip and the reduction is too short
+// to be split into slices (under 8 stages), then 64 x 64.
 Bf16Tile bf16_gemm_tile(int64_t m, int64_t n, int64_t batch, int64_t kp, int64_t cus);
 
 // Whether bf16_gemm takes this product: its loads address one tile's staged rows with 32-bit
