@@ -804,8 +804,8 @@ def test_bf16_backward_at_config2_sizes(dev_bf16, oracle, m, k, n):
 def test_bf16_products_on_256_tiles(dev_bf16, oracle, batch, m, k, n):
     """Products whose 256 x 256 tiles alone fill a 256-CU part (one block of eight waves per CU):
     every output, ragged edges and batches included, against float64 products of the bf16-rounded
-    operands (fp32 accumulation of exact bf16 products: rel 1e-5); the bias entry adds the bias to
-    the same sums."""
+    operands (fp32 accumulation of exact bf16 products: rel 1e-5); the bias and axpby entries
+    finish the same sums (each operation rounded on its own)."""
     rng = np.random.default_rng(m + k + n)
     a = rng.standard_normal(batch * m * k).astype(np.float32)
     b = rng.standard_normal(batch * k * n).astype(np.float32)
@@ -822,6 +822,12 @@ def test_bf16_products_on_256_tiles(dev_bf16, oracle, batch, m, k, n):
     assert rel_err(got, want) < 1e-5
     got_b = dev_bf16.read(out_b, batch * m * n).reshape(batch, m, n)
     assert np.array_equal(got_b.view(np.uint32), (got + bias).astype(np.float32).view(np.uint32))
+    g = rng.standard_normal(batch * m * n).astype(np.float32)
+    G, fused = up(dev_bf16, g), dev_bf16.empty(batch * m * n)
+    alpha, beta = 0.8125, -1.4375
+    dev_bf16.call("axis_matmul_axpby", A.vp, B.vp, G.vp, fused.vp, *geo, F32(alpha), F32(beta))
+    expect = (np.float32(beta) * g) + (np.float32(alpha) * got.reshape(-1))
+    assert np.array_equal(dev_bf16.read(fused, batch * m * n).view(np.uint32), expect.astype(np.float32).view(np.uint32))
 
 
 @pytest.mark.parametrize("m", [4_194_368, 8_400_000])
